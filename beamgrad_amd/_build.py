@@ -1,0 +1,97 @@
+# SPDX-License-Identifier: MIT
+"""In-tree build of the native parts of beamgrad_amd for gfx950.
+
+* ``_lib/libdbs_hip.so``: the HIP engine and its C ABI (include/dbs_cuda.h,
+  include/dbs_hip.h), compiled by hipcc for gfx950 only;
+* ``_C*.so``: the torch.ops.beamgrad operators, linked against libdbs_hip.
+
+Run ``python -m beamgrad_amd._build`` (or ``__graft_entry__.build()``).
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+import sysconfig
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+ARCH = "gfx950"
+
+# Device numerics must be the reference's bit for bit: no FMA contraction, no
+# fast math, IEEE f32 division, denormals kept; packed FP32 instructions off.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-fno-fast-math",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+LIB_SOURCES = ["csrc/api.hip", "csrc/decode.hip", "csrc/backward.hip"]
+
+
+def lib_path() -> str:
+    return os.path.join(HERE, "_lib", "libdbs_hip.so")
+
+
+def ext_path() -> str:
+    suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    return os.path.join(HERE, "_C" + suffix)
+
+
+def _run(cmd: list[str]) -> None:
+    print("[beamgrad_amd build]", " ".join(cmd[:3]), "...", flush=True)
+    subprocess.run(cmd, check=True, cwd=HERE)
+
+
+def build_lib() -> str:
+    os.makedirs(os.path.join(HERE, "_lib"), exist_ok=True)
+    out = lib_path()
+    cmd = [HIPCC, *HIP_FLAGS, "-shared", "-fvisibility=hidden", f"-I{ROOT}/include", f"-I{HERE}/csrc",
+           *LIB_SOURCES, "-o", out + ".tmp"]
+    _run(cmd)
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build_ext() -> str:
+    import torch
+    from torch.utils import cpp_extension as ce
+
+    incs = ce.include_paths(device_type="cuda")
+    libdirs = ce.library_paths(device_type="cuda")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    py_inc = sysconfig.get_paths()["include"]
+    out = ext_path()
+    cmd = [
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DUSE_ROCM=1", "-D__HIP_PLATFORM_AMD__=1",
+        "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        *[f"-I{p}" for p in incs], f"-I{py_inc}", f"-I{ROOT}/include", f"-I{ROCM}/include",
+        "csrc/torch_ops.cpp",
+        f"-L{os.path.join(HERE, '_lib')}", "-ldbs_hip",
+        *[f"-L{p}" for p in libdirs], "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+        "-Wl,-rpath,$ORIGIN/_lib",
+        "-o", out + ".tmp",
+    ]
+    _run(cmd)
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build() -> None:
+    build_lib()
+    build_ext()
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

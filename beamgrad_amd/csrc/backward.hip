@@ -1,0 +1,282 @@
+// SPDX-License-Identifier: MIT
+//
+// Backward kernels of libdbs_hip for gfx950: the surrogate gradient of the
+// decode's score outputs (each output differentiated along its own path with
+// the selection held fixed) and the backtrack of the final beams.
+//
+//  * path_walk: one workgroup per example walks the trace from its last step
+//    and produces, per selected slot, the gradient of the log-prob entry it
+//    used ("draws"). Per step every slot's draw is formed in the reference's
+//    operation order and each parent sums its children in slot order
+//    (reference src/decoder.cpp:565-624, 668-683).
+//  * dense_gradient: one workgroup per [V] row writes the row's gradient once.
+//    From logits, a row with entries g gets g_v - softmax(x_v) * S with S the
+//    entries summed in token order (reference src/decoder.hpp:212-242);
+//    otherwise only the entries are non-zero. The fresh mode stores 0 + value
+//    in float32, float16 or bfloat16, so no zero-fill pass and no cast pass
+//    are needed; the accumulate mode adds into a float32 buffer.
+#include <hip/hip_runtime.h>
+
+#include "dbs_cuda.h"
+#include "engine.hpp"
+
+namespace dbs_hip {
+
+namespace {
+
+constexpr int kWalkThreads = 256;
+constexpr int kDenseThreads = 256;
+
+__global__ __launch_bounds__(kWalkThreads) void path_walk_kernel(BackwardParams p) {
+    __shared__ float next[DBS_CUDA_MAX_BEAM];
+    __shared__ float prev[DBS_CUDA_MAX_BEAM];
+    __shared__ float draw[DBS_CUDA_MAX_BEAM];
+    __shared__ int32_t par[DBS_CUDA_MAX_BEAM];
+    const int b = static_cast<int>(blockIdx.x);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int K = p.K, T = p.T, V = p.V;
+    const int steps_b = p.steps ? p.steps[b] : T;
+    for (int k = tid; k < K; k += kWalkThreads) next[k] = 0.0f;
+    // steps the example did not decode carry no gradient
+    for (int64_t i = static_cast<int64_t>(steps_b) * K + tid; i < static_cast<int64_t>(T) * K; i += kWalkThreads)
+        p.draws[static_cast<int64_t>(b) * T * K + i] = 0.0f;
+    __syncthreads();
+    for (int t = steps_b - 1; t >= 0; --t) {
+        const bool last = t == steps_b - 1;
+        const int64_t base = (static_cast<int64_t>(b) * T + t) * K;
+        for (int k = tid; k < K; k += kWalkThreads) {
+            const int64_t slot = base + k;
+            const int parent = p.parents[slot];
+            const bool valid = parent >= 0 && parent < K;  // malformed slots carry nothing
+            float d = 0.0f;
+            if (valid) {
+                float drank = 0.0f;
+                if (p.g_scores) drank = drank + p.g_scores[slot];
+                if (last && p.g_final) drank = drank + p.g_final[static_cast<int64_t>(b) * K + k];
+                const float inv_pen = 1.0f / length_penalty(p.lengths[slot], p.alpha);
+                d = next[k] + drank * inv_pen;
+                if (p.g_raw) d = d + p.g_raw[slot];
+                if (last && p.g_final_raw) d = d + p.g_final_raw[static_cast<int64_t>(b) * K + k];
+            }
+            const bool flows = valid && d != 0.0f;
+            draw[k] = flows ? d : 0.0f;
+            par[k] = flows ? parent : -1;
+            const int tok = p.tokens[slot];
+            p.draws[slot] = (flows && p.from_logprob[slot] && tok >= 0 && tok < V) ? d : 0.0f;
+        }
+        __syncthreads();
+        // each parent sums its children's raw-score gradients in slot order
+        for (int q = tid; q < K; q += kWalkThreads) {
+            float s = 0.0f;
+            for (int k = 0; k < K; ++k)
+                if (par[k] == q) s = s + draw[k];
+            prev[q] = s;
+        }
+        __syncthreads();
+        for (int k = tid; k < K; k += kWalkThreads) next[k] = prev[k];
+        __syncthreads();
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float load_logit(const void* base, int64_t i) {
+    if constexpr (DT == 0) {
+        return static_cast<const float*>(base)[i];
+    } else if constexpr (DT == 1) {
+        return half_to_f32(static_cast<const uint16_t*>(base)[i]);
+    } else {
+        return bf16_to_f32(static_cast<const uint16_t*>(base)[i]);
+    }
+}
+
+template <int OT>
+__device__ __forceinline__ void store_out(void* out, int64_t i, float v, bool accumulate) {
+    if constexpr (OT == 0) {
+        float* o = static_cast<float*>(out);
+        o[i] = accumulate ? o[i] + v : 0.0f + v;
+    } else if constexpr (OT == 1) {
+        static_cast<uint16_t*>(out)[i] = f32_to_f16_rne(0.0f + v);
+    } else {
+        static_cast<uint16_t*>(out)[i] = f32_to_bf16_rne(0.0f + v);
+    }
+}
+
+// Stores zeros over [0, V) of a row (fresh mode), 4 elements per thread per pass.
+template <int OT>
+__device__ __forceinline__ void zero_row(void* out, int64_t row_off, int V) {
+    const int tid = static_cast<int>(threadIdx.x);
+    for (int v = tid; v < V; v += kDenseThreads) {
+        if constexpr (OT == 0) {
+            static_cast<float*>(out)[row_off + v] = 0.0f;
+        } else {
+            static_cast<uint16_t*>(out)[row_off + v] = 0;
+        }
+    }
+}
+
+template <int DT, int OT, bool LOGITS>
+__global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardParams p) {
+    __shared__ int32_t e_tok[DBS_CUDA_MAX_BEAM];
+    __shared__ float e_val[DBS_CUDA_MAX_BEAM];
+    __shared__ int32_t e_slot[DBS_CUDA_MAX_BEAM];
+    __shared__ int n_raw;
+    __shared__ int n_ent;
+    __shared__ float s_sum;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int K = p.K, T = p.T, V = p.V;
+    const int64_t r = blockIdx.x;  // row (b, t, q)
+    const int b = static_cast<int>(r / (static_cast<int64_t>(T) * K));
+    const int t = static_cast<int>((r / K) % T);
+    const int q = static_cast<int>(r % K);
+    const int steps_b = p.steps ? p.steps[b] : T;
+    const int64_t row_off = r * V;
+    const bool accumulate = p.accumulate != 0;
+
+    if (tid == 0) n_raw = 0;
+    __syncthreads();
+    if (t < steps_b) {
+        const int64_t base = (static_cast<int64_t>(b) * T + t) * K;
+        for (int k = tid; k < K; k += kDenseThreads) {
+            const float d = p.draws[base + k];
+            if (d != 0.0f && p.parents[base + k] == q) {
+                const int i = atomicAdd(&n_raw, 1);
+                e_tok[i] = p.tokens[base + k];
+                e_val[i] = d;
+                e_slot[i] = k;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        // order by (token, slot), merge equal tokens in slot order from 0, and
+        // sum the row's entries in token order (reference src/decoder.cpp:668-683)
+        const int n = n_raw;
+        for (int i = 1; i < n; ++i) {
+            const int32_t tk = e_tok[i], sl = e_slot[i];
+            const float vl = e_val[i];
+            int j = i - 1;
+            while (j >= 0 && (e_tok[j] > tk || (e_tok[j] == tk && e_slot[j] > sl))) {
+                e_tok[j + 1] = e_tok[j];
+                e_val[j + 1] = e_val[j];
+                e_slot[j + 1] = e_slot[j];
+                --j;
+            }
+            e_tok[j + 1] = tk;
+            e_val[j + 1] = vl;
+            e_slot[j + 1] = sl;
+        }
+        int w = 0;
+        float total = 0.0f;
+        for (int i = 0; i < n;) {
+            float v = 0.0f;
+            int j = i;
+            for (; j < n && e_tok[j] == e_tok[i]; ++j) v = v + e_val[j];
+            e_tok[w] = e_tok[i];
+            e_val[w] = v;
+            ++w;
+            total = total + v;
+            i = j;
+        }
+        n_ent = w;
+        s_sum = total;
+    }
+    __syncthreads();
+    const int ne = n_ent;
+
+    if (!LOGITS || ne == 0) {
+        if (!accumulate) zero_row<OT>(p.out, row_off, V);
+        if (ne > 0) {
+            __syncthreads();  // the entries land after the zeros of this workgroup
+            for (int i = tid; i < ne; i += kDenseThreads) store_out<OT>(p.out, row_off + e_tok[i], e_val[i], accumulate);
+        }
+        return;
+    }
+
+    // From logits: g_v - softmax(x_v) * S over the whole row.
+    const float S = s_sum;
+    const float lse = p.row_lse[r];
+    const size_t esz = DT == 0 ? 4 : 2;
+    const void* x = static_cast<const char*>(p.logits) + static_cast<size_t>(r) * static_cast<size_t>(V) * esz;
+    for (int v = tid; v < V; v += kDenseThreads) {
+        const float xv = load_logit<DT>(x, v);
+        const float pv = softmax_probability(xv, lse);
+        // entry value of token v, by binary search of the sorted entry tokens
+        int lo = 0, hi = ne;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (e_tok[mid] < v) lo = mid + 1;
+            else hi = mid;
+        }
+        const float g = (lo < ne && e_tok[lo] == v) ? e_val[lo] : 0.0f;
+        store_out<OT>(p.out, row_off + v, g - pv * S, accumulate);
+    }
+}
+
+template <int OT>
+hipError_t launch_dense_ot(const BackwardParams& p, hipStream_t stream) {
+    const int64_t rows = static_cast<int64_t>(p.B) * p.T * p.K;
+    if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>(rows));
+    KernelTimer timer(kKindDense, stream);
+    if (!p.logits) {
+        hipLaunchKernelGGL((dense_gradient_kernel<0, OT, false>), grid, dim3(kDenseThreads), 0, stream, p);
+    } else if (p.logits_type == 0) {
+        hipLaunchKernelGGL((dense_gradient_kernel<0, OT, true>), grid, dim3(kDenseThreads), 0, stream, p);
+    } else if (p.logits_type == 1) {
+        hipLaunchKernelGGL((dense_gradient_kernel<1, OT, true>), grid, dim3(kDenseThreads), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((dense_gradient_kernel<2, OT, true>), grid, dim3(kDenseThreads), 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
+__global__ void backtrack_kernel(const int32_t* tokens, const int32_t* parents, const int32_t* steps, int T, int K,
+                                 int64_t* seq) {
+    const int b = static_cast<int>(blockIdx.x);
+    const int steps_b = steps ? steps[b] : T;
+    for (int k = static_cast<int>(threadIdx.x); k < K; k += static_cast<int>(blockDim.x)) {
+        int beam = k;
+        int64_t* dst = seq + (static_cast<int64_t>(b) * K + k) * T;
+        for (int t = T - 1; t >= 0; --t) {
+            if (t >= steps_b || beam < 0) {
+                dst[t] = -1;
+                continue;
+            }
+            const int64_t slot = (static_cast<int64_t>(b) * T + t) * K + beam;
+            dst[t] = tokens[slot];
+            const int next = parents[slot];
+            beam = next < K ? next : -1;  // a malformed parent ends the path
+        }
+    }
+}
+
+}  // namespace
+
+size_t backward_workspace_bytes(int B, int T, int K) {
+    const size_t n = static_cast<size_t>(B) * T * K * sizeof(float);
+    return ((n + 255) / 256) * 256;
+}
+
+hipError_t launch_path_walk(const BackwardParams& p, hipStream_t stream) {
+    KernelTimer timer(kKindPathWalk, stream);
+    hipLaunchKernelGGL(path_walk_kernel, dim3(p.B), dim3(kWalkThreads), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_dense_gradient(const BackwardParams& p, hipStream_t stream) {
+    switch (p.out_type) {
+        case 0: return launch_dense_ot<0>(p, stream);
+        case 1: return launch_dense_ot<1>(p, stream);
+        default: return launch_dense_ot<2>(p, stream);
+    }
+}
+
+hipError_t launch_backtrack(const int32_t* tokens, const int32_t* parents, const int32_t* steps, int B, int T, int K,
+                            int64_t* seq, hipStream_t stream) {
+    const int threads = K < 256 ? ((K + 63) / 64) * 64 : 256;
+    KernelTimer timer(kKindBacktrack, stream);
+    hipLaunchKernelGGL(backtrack_kernel, dim3(B), dim3(threads), 0, stream, tokens, parents, steps, T, K, seq);
+    return hipGetLastError();
+}
+
+}  // namespace dbs_hip

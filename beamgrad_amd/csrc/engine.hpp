@@ -1,0 +1,147 @@
+// SPDX-License-Identifier: MIT
+//
+// Internal interface between the C ABI (api.hip) and the kernels of
+// libdbs_hip (decode.hip, backward.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "numerics.hpp"
+
+namespace dbs_hip {
+
+// Kernel kinds of the optional launch timer (dbs_hip_profile_* in dbs_hip.h).
+enum KernelKind : int { kKindRowPass = 0, kKindSelect = 1, kKindPathWalk = 2, kKindDense = 3, kKindBacktrack = 4,
+                        kKindCount = 5 };
+
+// Brackets the launches made in its scope with HIP events on `stream` when
+// profiling is on; the durations are read back by dbs_hip_profile_read.
+class KernelTimer {
+public:
+    KernelTimer(int kind, hipStream_t stream);
+    ~KernelTimer();
+    KernelTimer(const KernelTimer&) = delete;
+    KernelTimer& operator=(const KernelTimer&) = delete;
+
+private:
+    int kind_;
+    hipStream_t stream_;
+    hipEvent_t start_ = nullptr;
+    hipEvent_t stop_ = nullptr;
+};
+
+constexpr int kMaxEos = 17;          // eos_token + 16 extra EOS tokens
+constexpr int kRowThreads = 64;      // one wavefront per row in the row pass
+constexpr int kLanes = 256;          // lanes of the fixed logsumexp fold order
+constexpr int kSurvivorCap = 512;    // row-pass candidates kept per row before overflow
+constexpr int kSelectThreads = 256;  // one workgroup per example in the select pass
+constexpr int kRound = kSelectThreads;      // candidates offered per collector round (one per thread)
+
+// Per-row result of the row pass.
+struct RowInfo {
+    float lse;     // logsumexp of the row (from logits), else 0
+    float bound;   // upper bound on the log-prob of every allowed token not in the shortlist (-inf: none)
+    int32_t count; // shortlist entries; -1: no usable shortlist (the select pass rescans the row)
+    uint32_t invalid;  // the row holds NaN or +inf
+};
+
+struct ShortEntry {
+    float lp;
+    int32_t token;
+};
+
+// Everything the decode kernels read; passed by value.
+struct DecodeParams {
+    const void* x;            // [B, T, K, V] (decode) or [B, K, V] (step)
+    int dtype;
+    int from_logits;
+    int B, T, K, V;
+    int eos;                  // -1: no EOS handling
+    int n_eos;                // size of eos_set (0 when eos < 0)
+    int32_t eos_set[kMaxEos]; // every EOS token, sorted, distinct
+    int min_length;
+    float alpha;
+    int ngram;
+    int penalise;
+    float log_rep;            // logf(repetition_penalty) when penalise
+    int constrained;          // ngram > 0 || penalise
+    int M;                    // shortlist length; 0: every read row is rescanned
+    int use_tau;              // prefilter by the K-th shortlist candidate of each row
+    const int32_t* steps;     // device [B] or null
+    const uint8_t* banned;    // device [V] or null
+    const uint8_t* banned_pe; // device [B, V] or null
+    RowInfo* rowinfo;         // [rows]
+    ShortEntry* shortlist;    // [rows, M]
+    int32_t* prefix;          // [2, B, K, P] when constrained (P = prefix capacity)
+    int prefix_cap;
+    // outputs (any may be null except final_scores in decode mode)
+    float* final_scores;
+    float* final_raw;
+    int32_t* final_lengths;
+    int32_t* tokens;
+    int32_t* parents;
+    int32_t* lengths;
+    float* scores;
+    float* raw_scores;
+    uint8_t* from_logprob;
+    uint8_t* invalid;
+    float* row_lse;
+    // step mode: one step from an explicit state ([B, K] arrays, updated in place)
+    int step_mode;
+    float* st_raw;
+    int32_t* st_len;
+    uint8_t* st_fin;
+    const int32_t* st_prefix;  // [B, K, st_stride]
+    int st_stride;
+};
+
+struct DecodeLayout {
+    int M;
+    int use_tau;
+    int sort_cap;
+    size_t smem_bytes;
+    size_t off_rowinfo, off_short, off_prefix, total;
+    int prefix_cap;
+};
+
+DecodeLayout decode_layout(int B, int T, int K, int V, bool constrained, bool step_mode, int prefix_stride);
+
+// Queues the decode (or one step) on `stream`; returns a hipError_t.
+hipError_t launch_decode(const DecodeParams& p, const DecodeLayout& L, hipStream_t stream);
+
+// Elementwise helpers.
+hipError_t launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream);
+hipError_t launch_length_penalty(const int32_t* lengths, int64_t n, float alpha, float* out, hipStream_t stream);
+hipError_t launch_check_steps(const int32_t* steps, int B, int T, int32_t* status, hipStream_t stream);
+
+// Backward.
+struct BackwardParams {
+    int B, T, K, V;
+    float alpha;
+    const int32_t* steps;
+    const int32_t* parents;
+    const int32_t* tokens;
+    const int32_t* lengths;
+    const uint8_t* from_logprob;
+    const float* g_final;
+    const float* g_final_raw;
+    const float* g_scores;
+    const float* g_raw;
+    const void* logits;
+    int logits_type;
+    const float* row_lse;
+    float* draws;      // [B, T, K] per-slot entry gradients (workspace or caller output)
+    void* out;         // [B, T, K, V]
+    int out_type;      // 0 f32, 1 f16, 2 bf16
+    int accumulate;    // 1: out += g (f32 only); 0: out = 0 + g everywhere
+};
+
+size_t backward_workspace_bytes(int B, int T, int K);
+hipError_t launch_path_walk(const BackwardParams& p, hipStream_t stream);
+hipError_t launch_dense_gradient(const BackwardParams& p, hipStream_t stream);
+hipError_t launch_backtrack(const int32_t* tokens, const int32_t* parents, const int32_t* steps, int B, int T, int K,
+                            int64_t* seq, hipStream_t stream);
+
+}  // namespace dbs_hip

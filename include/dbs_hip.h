@@ -1,0 +1,81 @@
+/* SPDX-License-Identifier: MIT
+ *
+ * Additive entry points of libdbs_hip.so beyond the reference's device ABI
+ * (include/dbs_cuda.h). None changes an existing layout; each says which
+ * reference interface it extends.
+ */
+#pragma once
+
+#include "dbs_cuda.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dbs_cuda_decode_ex2 with a per-example banned-token mask: banned_per_example
+ * is device uint8 [B, V] (non-zero bans token v in example b), OR-ed with
+ * args->banned_tokens. The reference takes only one [V] mask on the device
+ * (reference include/dbs_cuda.h:86); its CPU path bans per example through
+ * separate dbs_decode_batch_into_ex calls (reference include/dbs.h:339-368). */
+DBS_CUDA_EXPORT int dbs_hip_decode_ex3(
+    const void* inputs,
+    int data_type,
+    int from_logits,
+    const DBSCudaDecodeArgs* args,
+    const DBSCudaSearchOptions* options,
+    const uint8_t* banned_per_example,
+    const DBSCudaDecodeOutputs* outputs,
+    float* row_lse,
+    void* workspace,
+    int64_t workspace_bytes,
+    void* stream);
+
+/* Output element types of dbs_hip_backward_dense. */
+#define DBS_HIP_GRAD_F32 0
+#define DBS_HIP_GRAD_F16 1
+#define DBS_HIP_GRAD_BF16 2
+
+/* The gradient of dbs_cuda_backward_ex written, not accumulated: every
+ * element of grad_out [B, T, K, V] is stored once, as 0 + g rounded to
+ * grad_type (round to nearest even), so the caller needs no zero-fill and no
+ * separate cast. Equals zero-filling a float32 buffer, calling
+ * dbs_cuda_backward_ex (reference include/dbs_cuda.h:262-268) and converting
+ * the result with a round-to-nearest-even cast (reference
+ * python/beamgrad/_torch.py:289). Workspace: dbs_cuda_backward_workspace_size. */
+DBS_CUDA_EXPORT int dbs_hip_backward_dense(
+    const DBSCudaDecodeArgs* args,
+    const DBSCudaBackwardInputs* inputs,
+    void* grad_out,
+    int grad_type,
+    void* workspace,
+    int64_t workspace_bytes,
+    void* stream);
+
+/* Token sequences of the final beams, following parent pointers from the last
+ * step: sequences [B, K, T] (int64); steps past steps_per_example[b] and dead
+ * beams hold -1. One launch; replaces the T-step torch loop of the reference's
+ * backtrack (reference python/beamgrad/_torch.py:582-606). tokens and parents
+ * are int32 [B, T, K]; steps_per_example is device int32 [B] or NULL. */
+DBS_CUDA_EXPORT int dbs_hip_backtrack(
+    const int32_t* tokens,
+    const int32_t* parents,
+    const int32_t* steps_per_example,
+    int batch_size,
+    int steps,
+    int beam_size,
+    int64_t* sequences,
+    void* stream);
+
+/* Launch timing for measurement tools (no counterpart in the reference).
+ * With profiling on, every kernel the library launches is bracketed by HIP
+ * events on the caller's stream, and its duration is summed per kernel kind:
+ * 0 row pass, 1 select, 2 path walk, 3 dense gradient, 4 backtrack.
+ * dbs_hip_profile_enable(on) clears the sums; dbs_hip_profile_read waits for
+ * the recorded events and returns the sum (milliseconds) and the number of
+ * launches of one kind. Off by default; costs two event records per launch. */
+DBS_CUDA_EXPORT int dbs_hip_profile_enable(int on);
+DBS_CUDA_EXPORT int dbs_hip_profile_read(int kernel, double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
