@@ -1,0 +1,222 @@
+# SPDX-License-Identifier: MIT
+"""Benchmark of the beam-search hot path on one MI355X.
+
+A step is one pass of the hot path over one batch of synthetic input already
+resident in HBM: for the headline workload that is
+``beamgrad_amd.decode(logits, from_logits=True)`` (final scores + trace) and
+``backtrack`` on bf16 logits [B=32, T=64, K=8, V=151936] with EOS 151643,
+length penalty 1.0 and min_length 4. ``value`` is candidate elements per
+second over the timed steps (rows read by the search x V, the reference's
+count); the dominant kernel's HBM roofline fraction and the reference CPU
+library's throughput on a bounded sample of the same workload are reported
+beside it.
+
+    python bench.py [--steps K] [--warmup W] [--config c1..c5] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, GB/s
+METRIC = "decode candidate elements/sec & % of HBM peak BW; fwd+bwd step latency (1 GPU)"
+
+CONFIGS = {
+    "c1": dict(B=8, T=32, K=4, V=32000, dtype="f32", from_logits=False, eos=2, alpha=0.6, min_length=0, seed=1001,
+               desc="decode()+backtrack() fp32 log-probs [8,32,4,32000], eos 2, alpha 0.6"),
+    "c2": dict(B=32, T=64, K=8, V=151936, dtype="bf16", from_logits=True, eos=151643, alpha=1.0, min_length=4,
+               seed=1002, desc="from_logits bf16 [32,64,8,151936] N(0,3^2)+Zipf(1.1) bias, eos 151643, "
+                               "length_penalty 1.0, min_length 4; final_scores+decode+backtrack"),
+    "c4": dict(B=16, T=64, K=64, V=32000, dtype="f32", from_logits=False, eos=2, alpha=0.6, min_length=0, seed=1004,
+               desc="wide-beam fp32 log-probs [16,64,64,32000] with 5% exact ties, eos 2, alpha 0.6; decode"),
+}
+
+
+def make_inputs(cfg: dict) -> torch.Tensor:
+    """Seeded synthetic rows generated on the GPU, one example at a time."""
+    B, T, K, V = cfg["B"], cfg["T"], cfg["K"], cfg["V"]
+    gen = torch.Generator(device="cuda").manual_seed(cfg["seed"])
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[cfg["dtype"]]
+    x = torch.empty(B, T, K, V, dtype=tdt, device="cuda")
+    if cfg is CONFIGS["c2"]:
+        rank = torch.randperm(V, generator=gen, device="cuda").to(torch.float32) + 1.0
+        bias = -1.1 * torch.log(rank)  # Zipf(s=1.1) bias shared across rows
+        for b in range(B):
+            x[b] = (torch.randn(T, K, V, generator=gen, device="cuda") * 3.0 + bias).to(tdt)
+    elif cfg is CONFIGS["c4"]:
+        for b in range(B):
+            lp = torch.log_softmax(torch.randn(T, K, V, generator=gen, device="cuda") * 1.5, dim=-1)
+            pool = lp.reshape(T, -1)[:, :64].clone()  # per-step pool of exact values
+            tie = torch.rand(T, K, V, generator=gen, device="cuda") < 0.05
+            pick = torch.randint(0, 64, (T, K, V), generator=gen, device="cuda")
+            lp = torch.where(tie, torch.gather(pool, 1, pick.reshape(T, -1)).reshape(T, K, V), lp)
+            x[b] = lp.to(tdt)
+    else:
+        for b in range(B):
+            x[b] = torch.log_softmax(torch.randn(T, K, V, generator=gen, device="cuda") * 2.0, dim=-1).to(tdt)
+    return x
+
+
+def rows_read(out, eos_set: tuple[int, ...]) -> int:
+    """Rows the reference reads: beam 0 at step 0, then every live beam that
+    has not emitted EOS, for t < steps (decoder.cpp:127-131)."""
+    raw = out.raw_scores  # [B, T, K]
+    live = torch.isfinite(raw[:, :-1])
+    if eos_set:
+        finished = torch.isin(out.tokens[:, :-1], torch.tensor(eos_set, device=raw.device))
+        live = live & ~finished
+    return int(raw.shape[0] + live.sum().item())
+
+
+def cpu_baseline(cfg: dict, x: torch.Tensor, rows_per_example: float, budget_s: float = 10.0) -> dict | None:
+    """The reference's CPU library (oracle/_ref) or, without it, the oracle,
+    timed on this host's cores over the same batch, repeated for about
+    `budget_s` seconds of CPU work."""
+    from oracle import oracle as orc
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    if x.dtype == torch.float32:
+        host = x.cpu().numpy()
+    else:
+        host = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    kw = dict(dtype=cfg["dtype"], from_logits=cfg["from_logits"], eos_token=cfg["eos"], min_length=cfg["min_length"],
+              alpha=cfg["alpha"])
+    if orc.reference_available():
+        impl, kind = orc.Reference(), "reference"
+    else:
+        impl, kind = orc.Oracle(), "port"
+    impl.decode(host, num_threads=threads, **kw)  # warm-up
+    reps, total = 0, 0.0
+    while total < budget_s:
+        t0 = time.perf_counter()
+        impl.decode(host, num_threads=threads, **kw)
+        total += time.perf_counter() - t0
+        reps += 1
+    cand = rows_per_example * cfg["B"] * cfg["V"] * reps
+    return {"value": cand / total, "unit": "candidate elements/s", "cores": threads, "kind": kind,
+            "sample": f"the whole batch ({cfg['B']} examples, T={cfg['T']}) decoded {reps} times "
+                      f"({total:.1f} s) with dbs_decode_batch_into_ex, {threads} threads, after a warm-up"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain device copy of 1 GiB (the PMC byte-counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build's hot path runs on a single MI355X "
+              "(examples shard over GPUs with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import beamgrad_amd as bg
+    from beamgrad_amd import _abi
+
+    cfg = CONFIGS[args.config]
+    B, T, K, V = cfg["B"], cfg["T"], cfg["K"], cfg["V"]
+    x = make_inputs(cfg)
+    opts = bg.BeamOptions(beam_size=K, eos_token=cfg["eos"], min_length=cfg["min_length"],
+                          length_penalty_alpha=cfg["alpha"])
+    eos_set = opts.eos_tokens
+    torch.cuda.synchronize()
+
+    def step():
+        out = bg.decode(x, opts, from_logits=cfg["from_logits"])
+        seq = bg.backtrack(out)
+        return out, seq
+
+    for _ in range(args.warmup):
+        out, _ = step()
+    torch.cuda.synchronize()
+    n_rows = rows_read(out, eos_set)
+
+    if args.copy_probe:
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    lib = _abi.load()
+    lib.dbs_hip_profile_enable(1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        out, seq = step()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(stop)
+    import ctypes as C
+
+    kernels = {}
+    for kind, name in enumerate(("row_pass", "select", "path_walk", "dense_gradient", "backtrack")):
+        ms, n = C.c_double(), C.c_int64()
+        lib.dbs_hip_profile_read(kind, C.byref(ms), C.byref(n))
+        if n.value:
+            kernels[name] = {"avg_ms": ms.value / n.value, "launches": n.value}
+    lib.dbs_hip_profile_enable(0)
+
+    ms_per_step = gpu_ms / args.steps
+    elem = 4 if cfg["dtype"] == "f32" else 2
+    cand_per_step = n_rows * V
+    value = cand_per_step / (ms_per_step / 1e3)
+    alg_bytes = cand_per_step * elem
+    rp = kernels["row_pass"]["avg_ms"]
+    achieved = alg_bytes / (rp / 1e3) / 1e9
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"row_pass_{args.config}_traffic.txt")
+    if os.path.exists(tfile):
+        for line in open(tfile):
+            if line.startswith("traffic_bytes_per_launch"):
+                traffic = float(line.split("=")[1])
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "candidate elements/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"],
+        "data": "synthetic (seeded, generated on the GPU)",
+        "config": {"workload": f"{args.config.upper()}: {cfg['desc']}", "B": B, "T": T, "K": K, "V": V,
+                   "from_logits": cfg["from_logits"], "rows_read_per_step": n_rows,
+                   "step_hbm_gbs": alg_bytes / (ms_per_step / 1e3) / 1e9,
+                   "step_hbm_frac": alg_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS,
+                   "kernels_ms": {k: round(v["avg_ms"], 4) for k, v in kernels.items()},
+                   "wall_s": round(wall, 3)},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": "row_pass",
+                     "algorithmic_bytes": alg_bytes},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        del out, seq
+        result["cpu_baseline"] = cpu_baseline(cfg, x, n_rows / B)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -74,6 +74,29 @@ def make_case(seed: int, *, big: bool = False, allow_invalid: bool = True) -> di
     return dict(seed=seed, B=B, T=T, K=K, V=V, dtype=dtype, x=x, xin=to_bits(x, dtype), kw=kw, invalid=invalid)
 
 
+def load_golden() -> list[dict]:
+    """The committed fixtures of tests/golden/cases.npz (reference outputs)."""
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "cases.npz")
+    z = np.load(path, allow_pickle=False)
+    cases = []
+    for n in range(int(z["n_cases"][0])):
+        p = f"c{n}_"
+        B, T, K, V, fl, eos, minlen, ngram, dt = (int(v) for v in z[p + "meta"])
+        alpha, rep = (float(v) for v in z[p + "fmeta"])
+        kw = dict(from_logits=bool(fl), eos_token=eos, extra_eos=[int(v) for v in z[p + "extra_eos"]],
+                  min_length=minlen, alpha=alpha, no_repeat_ngram_size=ngram, repetition_penalty=rep,
+                  steps=z[p + "steps"].tolist() if p + "steps" in z else None,
+                  banned=z[p + "banned"] if p + "banned" in z else None,
+                  banned_per_example=z[p + "banned_per_example"] if p + "banned_per_example" in z else None)
+        out = {k[len(p) + 4:]: z[k] for k in z.files if k.startswith(p + "out_")}
+        cases.append(dict(index=n, B=B, T=T, K=K, V=V, dtype=["f32", "f16", "bf16"][dt], xin=z[p + "x"], kw=kw,
+                          out=out, grad_final=z[p + "grad_final"], grad_scores=z[p + "grad_scores"],
+                          grad=z[p + "grad"]))
+    return cases
+
+
 TRACE_KEYS = ("final_scores", "final_raw_scores", "final_lengths", "tokens", "parents", "lengths", "scores",
               "raw_scores", "from_logprob", "row_lse", "invalid")
 

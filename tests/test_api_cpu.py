@@ -1,0 +1,70 @@
+# SPDX-License-Identifier: MIT
+"""CPU-side behaviour of the Python front end: option validation (the
+reference's rules, python/beamgrad/_options.py), the loud failure on CPU
+tensors, and the operators' fake implementations (shapes and dtypes)."""
+
+import numpy as np
+import pytest
+import torch
+
+import beamgrad_amd as bg
+
+
+def test_options_validation():
+    with pytest.raises(ValueError):
+        bg.BeamOptions(beam_size=0)
+    with pytest.raises(ValueError):
+        bg.BeamOptions(beam_size=True)
+    with pytest.raises(ValueError):
+        bg.BeamOptions(beam_size=2, eos_token=-2)
+    with pytest.raises(ValueError):
+        bg.BeamOptions(beam_size=2, length_penalty_alpha=-1.0)
+    with pytest.raises(ValueError):
+        bg.BeamOptions(beam_size=2, length_penalty_alpha=float("inf"))
+    with pytest.raises(ValueError):
+        bg.BeamOptions(beam_size=2, repetition_penalty=0.0)
+    with pytest.raises(ValueError):
+        bg.BeamOptions(beam_size=2, banned_tokens=[-1])
+    with pytest.raises(ValueError):
+        bg.BeamOptions(beam_size=2, validate_inputs=1)
+    o = bg.BeamOptions(beam_size=np.int64(3), eos_token=[5, 7, 5], banned_tokens=np.array([1, 2]))
+    assert o.beam_size == 3 and o.eos_token == (5, 7) and o.banned_tokens == (1, 2)
+    assert o.native_eos() == (5, [7])
+    assert bg.BeamOptions(beam_size=2, eos_token=[4]).eos_token == 4
+    with pytest.raises(ValueError):
+        o.eos_ids(6)
+    assert o.banned_mask(4) == [0, 1, 1, 0]
+
+
+def test_cpu_tensors_fail_loudly():
+    opts = bg.BeamOptions(beam_size=2)
+    with pytest.raises(RuntimeError, match="GPU"):
+        bg.decode(torch.zeros(1, 3, 2, 5), opts)
+    with pytest.raises(RuntimeError, match="GPU"):
+        bg.final_scores(torch.zeros(3, 2, 5), opts)
+    with pytest.raises(NotImplementedError):
+        # no CPU kernel is registered for the operators
+        torch.ops.beamgrad.decode_ex(torch.zeros(1, 3, 2, 5), False, None, -1, 0, 0.0, None, 0, 1.0, True, [])
+
+
+def test_shape_checks():
+    opts = bg.BeamOptions(beam_size=2)
+    with pytest.raises(ValueError, match="beams"):
+        bg.decode(torch.zeros(1, 3, 4, 5), opts)
+    with pytest.raises(ValueError, match="shape"):
+        bg.decode(torch.zeros(3, 5), opts)
+    with pytest.raises(TypeError):
+        bg.decode(torch.zeros(1, 3, 2, 5, dtype=torch.int32), opts)
+
+
+def test_fake_implementations_give_shapes():
+    x = torch.empty(2, 3, 4, 7, device="meta", dtype=torch.bfloat16)
+    out = torch.ops.beamgrad.decode_ex(x, True, None, -1, 0, 0.0, None, 0, 1.0, True, [])
+    assert [tuple(t.shape) for t in out] == [(2, 4), (2, 4), (2, 4)] + [(2, 3, 4)] * 7
+    assert out[0].dtype == torch.float32 and out[3].dtype == torch.int32 and out[8].dtype == torch.uint8
+    p = torch.empty(2, 3, 4, device="meta", dtype=torch.int32)
+    g = torch.ops.beamgrad.decode_backward_as(None, None, None, None, p, p, p, p.to(torch.uint8), None, 7, 0.0, None,
+                                              None, torch.bfloat16)
+    assert g.shape == (2, 3, 4, 7) and g.dtype == torch.bfloat16
+    seq = torch.ops.beamgrad.backtrack(p, p, None)
+    assert seq.shape == (2, 4, 3) and seq.dtype == torch.int64
