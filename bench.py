@@ -37,9 +37,35 @@ CONFIGS = {
     "c2": dict(B=32, T=64, K=8, V=151936, dtype="bf16", from_logits=True, eos=151643, alpha=1.0, min_length=4,
                seed=1002, desc="from_logits bf16 [32,64,8,151936] N(0,3^2)+Zipf(1.1) bias, eos 151643, "
                                "length_penalty 1.0, min_length 4; final_scores+decode+backtrack"),
+    "c3": dict(B=64, T=128, K=5, V=50257, dtype="f16", from_logits=False, eos=50256, alpha=0.0, min_length=8,
+               seed=1003, ngram=3, rep=1.2,
+               desc="constrained fp16 log-probs [64,128,5,50257], per-example 1% banned, no_repeat_ngram 3, "
+                    "repetition_penalty 1.2, min_length 8, steps U[64,128], eos 50256; decode"),
     "c4": dict(B=16, T=64, K=64, V=32000, dtype="f32", from_logits=False, eos=2, alpha=0.6, min_length=0, seed=1004,
                desc="wide-beam fp32 log-probs [16,64,64,32000] with 5% exact ties, eos 2, alpha 0.6; decode"),
+    "c5": dict(B=16, T=128, K=8, V=128256, dtype="bf16", from_logits=True, eos=-1, alpha=0.0, min_length=0,
+               seed=1005, desc="from_logits bf16 [16,128,8,128256] N(0,3^2); search + minimum_risk(costs U(0,1)) "
+                               "forward and backward into the logits"),
 }
+
+
+def workload(name: str) -> dict:
+    """Seeded inputs of a config, generated on the GPU: the rows, and the
+    per-example steps, banned mask and costs where the config has them."""
+    cfg = CONFIGS[name]
+    B, V = cfg["B"], cfg["V"]
+    gen = torch.Generator(device="cuda").manual_seed(cfg["seed"] + 7)
+    out = {"x": make_inputs(cfg), "steps": None, "banned": None, "costs": None}
+    if name == "c3":
+        out["steps"] = torch.randint(64, 129, (B,), generator=gen, device="cuda")
+        banned = torch.zeros(B, V, dtype=torch.uint8, device="cuda")
+        n_ban = V // 100
+        for b in range(B):
+            banned[b, torch.randperm(V, generator=gen, device="cuda")[:n_ban]] = 1
+        out["banned"] = banned
+    if name == "c5":
+        out["costs"] = torch.rand(B, cfg["K"], generator=gen, device="cuda")
+    return out
 
 
 def make_inputs(cfg: dict) -> torch.Tensor:
@@ -48,7 +74,13 @@ def make_inputs(cfg: dict) -> torch.Tensor:
     gen = torch.Generator(device="cuda").manual_seed(cfg["seed"])
     tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[cfg["dtype"]]
     x = torch.empty(B, T, K, V, dtype=tdt, device="cuda")
-    if cfg is CONFIGS["c2"]:
+    if cfg is CONFIGS["c3"]:
+        for b in range(B):
+            x[b] = torch.log_softmax(torch.randn(T, K, V, generator=gen, device="cuda") * 2.5, dim=-1).to(tdt)
+    elif cfg is CONFIGS["c5"]:
+        for b in range(B):
+            x[b] = (torch.randn(T, K, V, generator=gen, device="cuda") * 3.0).to(tdt)
+    elif cfg is CONFIGS["c2"]:
         rank = torch.randperm(V, generator=gen, device="cuda").to(torch.float32) + 1.0
         bias = -1.1 * torch.log(rank)  # Zipf(s=1.1) bias shared across rows
         for b in range(B):
@@ -78,34 +110,54 @@ def rows_read(out, eos_set: tuple[int, ...]) -> int:
     return int(raw.shape[0] + live.sum().item())
 
 
-def cpu_baseline(cfg: dict, x: torch.Tensor, rows_per_example: float, budget_s: float = 10.0) -> dict | None:
+def cpu_baseline(name: str, wl: dict, rows_per_example: float, budget_s: float = 10.0) -> dict | None:
     """The reference's CPU library (oracle/_ref) or, without it, the oracle,
-    timed on this host's cores over the same batch, repeated for about
-    `budget_s` seconds of CPU work."""
+    timed on this host's cores over the same batch (C5: decode + backward
+    with the same final-score gradient), repeated for about `budget_s`
+    seconds of CPU work."""
     from oracle import oracle as orc
 
+    cfg = CONFIGS[name]
     threads = min(16, len(os.sched_getaffinity(0)))
-    if x.dtype == torch.float32:
-        host = x.cpu().numpy()
-    else:
-        host = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    x = wl["x"].detach()
+    host = x.cpu().numpy() if x.dtype == torch.float32 else x.view(torch.int16).cpu().numpy().view(np.uint16)
     kw = dict(dtype=cfg["dtype"], from_logits=cfg["from_logits"], eos_token=cfg["eos"], min_length=cfg["min_length"],
-              alpha=cfg["alpha"])
+              alpha=cfg["alpha"], no_repeat_ngram_size=cfg.get("ngram", 0), repetition_penalty=cfg.get("rep", 1.0),
+              steps=None if wl["steps"] is None else wl["steps"].cpu().numpy(), num_threads=threads)
     if orc.reference_available():
         impl, kind = orc.Reference(), "reference"
     else:
         impl, kind = orc.Oracle(), "port"
-    impl.decode(host, num_threads=threads, **kw)  # warm-up
+    if wl["banned"] is not None:
+        banned = wl["banned"].cpu().numpy()
+        if kind == "reference":
+            run = lambda: impl.decode_per_example_banned(host, banned, **kw)  # noqa: E731
+        else:
+            run = lambda: impl.decode(host, banned_per_example=banned, **kw)  # noqa: E731
+        what = "per-example dbs_decode_batch_into_ex calls (one banned mask each)"
+    elif wl["costs"] is not None:
+        g_final = np.full((cfg["B"], cfg["K"]), 1.0 / cfg["B"], np.float32)
+
+        def run():
+            tr = impl.decode(host, **kw)
+            impl.backward(tr, cfg["V"], alpha=cfg["alpha"], grad_final=g_final, logits=host, logits_dtype=cfg["dtype"],
+                          row_lse=tr["row_lse"], num_threads=threads)
+        what = "dbs_decode_batch_into_ex + dbs_backward_batch_into_ex"
+    else:
+        run = lambda: impl.decode(host, **kw)  # noqa: E731
+        what = "dbs_decode_batch_into_ex"
+    run()  # warm-up
     reps, total = 0, 0.0
     while total < budget_s:
         t0 = time.perf_counter()
-        impl.decode(host, num_threads=threads, **kw)
+        run()
         total += time.perf_counter() - t0
         reps += 1
     cand = rows_per_example * cfg["B"] * cfg["V"] * reps
     return {"value": cand / total, "unit": "candidate elements/s", "cores": threads, "kind": kind,
-            "sample": f"the whole batch ({cfg['B']} examples, T={cfg['T']}) decoded {reps} times "
-                      f"({total:.1f} s) with dbs_decode_batch_into_ex, {threads} threads, after a warm-up"}
+            "ms_per_step": total / reps * 1e3,
+            "sample": f"the whole batch ({cfg['B']} examples, T={cfg['T']}) run {reps} times ({total:.1f} s) "
+                      f"through {what}, {threads} threads, after a warm-up"}
 
 
 def main() -> int:
@@ -128,16 +180,29 @@ def main() -> int:
 
     cfg = CONFIGS[args.config]
     B, T, K, V = cfg["B"], cfg["T"], cfg["K"], cfg["V"]
-    x = make_inputs(cfg)
+    wl = workload(args.config)
+    x = wl["x"]
     opts = bg.BeamOptions(beam_size=K, eos_token=cfg["eos"], min_length=cfg["min_length"],
-                          length_penalty_alpha=cfg["alpha"])
+                          length_penalty_alpha=cfg["alpha"], no_repeat_ngram_size=cfg.get("ngram", 0),
+                          repetition_penalty=cfg.get("rep", 1.0))
     eos_set = opts.eos_tokens
     torch.cuda.synchronize()
 
-    def step():
-        out = bg.decode(x, opts, from_logits=cfg["from_logits"])
-        seq = bg.backtrack(out)
-        return out, seq
+    if args.config == "c5":
+        x.requires_grad_(True)
+
+        def step():
+            # forward + minimum-risk loss + backward into the logits
+            x.grad = None
+            result = bg.search(x, opts, from_logits=True)
+            loss = bg.losses.minimum_risk(result, wl["costs"])
+            loss.backward()
+            return result.trace, result.sequences
+    else:
+        def step():
+            out = bg.decode(x, opts, wl["steps"], from_logits=cfg["from_logits"], banned_mask=wl["banned"])
+            seq = bg.backtrack(out)
+            return out, seq
 
     for _ in range(args.warmup):
         out, _ = step()
@@ -213,7 +278,7 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         del out, seq
-        result["cpu_baseline"] = cpu_baseline(cfg, x, n_rows / B)
+        result["cpu_baseline"] = cpu_baseline(args.config, wl, n_rows / B)
     print(json.dumps(result), flush=True)
     return 0
 

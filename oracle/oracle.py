@@ -382,12 +382,20 @@ class Reference:
             self.lib.dbs_destroy(h)
 
     def decode_per_example_banned(self, x: np.ndarray, banned_per_example: np.ndarray, *, steps=None, **kw) -> dict:
-        """B single-example calls, each with its own banned mask (the reference has no batched form for this)."""
+        """B single-example calls, each with its own banned mask (the reference
+        has no batched form for this), spread over a pool of `num_threads`
+        host threads (ctypes releases the GIL during each call)."""
+        from concurrent.futures import ThreadPoolExecutor
+
         B = x.shape[0]
-        parts = []
-        for b in range(B):
+        threads = kw.pop("num_threads", 0) or (os.cpu_count() or 1)
+
+        def one(b):
             st = None if steps is None else [int(np.asarray(steps)[b])]
-            parts.append(self.decode(x[b:b + 1], banned=banned_per_example[b], steps=st, **kw))
+            return self.decode(x[b:b + 1], banned=banned_per_example[b], steps=st, num_threads=1, **kw)
+
+        with ThreadPoolExecutor(max_workers=max(1, min(threads, B))) as pool:
+            parts = list(pool.map(one, range(B)))
         return {k: np.concatenate([p[k] for p in parts], 0) for k in parts[0]}
 
     def backward(self, trace: dict, vocab_size: int, *, alpha: float = 0.0, steps=None, grad_final=None,
