@@ -247,6 +247,7 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
     p.rowinfo = reinterpret_cast<RowInfo*>(ws + L.off_rowinfo);
     p.shortlist = reinterpret_cast<ShortEntry*>(ws + L.off_short);
     p.prefix = reinterpret_cast<int32_t*>(ws + L.off_prefix);
+    p.blocked = reinterpret_cast<int32_t*>(ws + L.off_blocked);
     p.prefix_cap = L.prefix_cap;
     p.final_scores = outputs->final_scores;
     p.final_raw = outputs->final_raw_scores;
@@ -309,6 +310,8 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
     p.banned = a.banned_tokens;
     p.rowinfo = reinterpret_cast<RowInfo*>(ws + L.off_rowinfo);
     p.shortlist = reinterpret_cast<ShortEntry*>(ws + L.off_short);
+    p.blocked = reinterpret_cast<int32_t*>(ws + L.off_blocked);
+    p.prefix_cap = L.prefix_cap;
     p.final_scores = outputs->final_scores;
     p.final_raw = outputs->final_scores ? outputs->final_raw_scores : nullptr;
     p.final_lengths = outputs->final_scores ? outputs->final_lengths : nullptr;
@@ -577,13 +580,25 @@ DBS_CUDA_EXPORT int dbs_hip_profile_enable(int on) {
         g_launches[i] = 0;
     }
     g_profile.store(on, std::memory_order_relaxed);
+    if (rescan_counter(1, nullptr) != hipSuccess) (void)hipGetLastError();
     return DBS_CUDA_STATUS_OK;
 }
 
 DBS_CUDA_EXPORT int dbs_hip_profile_read(int kernel, double* total_ms, int64_t* launches) {
-    if (kernel < 0 || kernel >= kKindCount || !total_ms || !launches) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    if (kernel < 0 || kernel > kKindCount || !total_ms || !launches) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lock(g_profile_mutex);
     drain_pending();
+    if (kernel == kKindCount) {
+        // rows the select pass had to rescan in full since profiling was enabled
+        unsigned long long n = 0;
+        if (rescan_counter(0, &n) != hipSuccess) {
+            (void)hipGetLastError();
+            return DBS_CUDA_STATUS_LAUNCH_FAILED;
+        }
+        *total_ms = 0.0;
+        *launches = static_cast<int64_t>(n);
+        return DBS_CUDA_STATUS_OK;
+    }
     *total_ms = g_total_ms[kernel];
     *launches = g_launches[kernel];
     return DBS_CUDA_STATUS_OK;

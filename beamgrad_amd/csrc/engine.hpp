@@ -74,7 +74,8 @@ struct DecodeParams {
     const uint8_t* banned_pe; // device [B, V] or null
     RowInfo* rowinfo;         // [rows]
     ShortEntry* shortlist;    // [rows, M]
-    int32_t* prefix;          // [2, B, K, P] when constrained (P = prefix capacity)
+    int32_t* prefix;          // [B, 2, K, P] when constrained and not kept in LDS (P = prefix capacity)
+    int32_t* blocked;         // [B, K, P] n-gram-blocked tokens when not kept in LDS
     int prefix_cap;
     // outputs (any may be null except final_scores in decode mode)
     float* final_scores;
@@ -97,19 +98,34 @@ struct DecodeParams {
     int st_stride;
 };
 
+// LDS plan of the select pass (byte offsets into its dynamic shared memory).
+struct SelectLayout {
+    int sort_cap;        // collector capacity (a power of two)
+    int pen_len;         // length-penalty table entries (T + 2; 0 in step mode)
+    size_t off_buf, off_rbuf, off_f32, off_i32, off_sl, off_prefix, off_blk;
+    int prefix_in_lds;   // the prefixes live in LDS (else in the workspace)
+    int blk_in_lds;      // the n-gram-blocked lists live in LDS (else in the workspace)
+    size_t smem;
+};
+
 struct DecodeLayout {
     int M;
     int use_tau;
-    int sort_cap;
-    size_t smem_bytes;
-    size_t off_rowinfo, off_short, off_prefix, total;
     int prefix_cap;
+    SelectLayout sel;
+    size_t off_rowinfo, off_short, off_prefix, off_blocked, total;
 };
 
 DecodeLayout decode_layout(int B, int T, int K, int V, bool constrained, bool step_mode, int prefix_stride);
+SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool step_mode, int prefix_cap);
 
 // Queues the decode (or one step) on `stream`; returns a hipError_t.
 hipError_t launch_decode(const DecodeParams& p, const DecodeLayout& L, hipStream_t stream);
+hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream);
+hipError_t launch_select(const DecodeParams& p, const SelectLayout& L, hipStream_t stream);
+
+// Rows the select pass rescanned in full (reset = 1 clears the count).
+hipError_t rescan_counter(int reset, unsigned long long* value);
 
 // Elementwise helpers.
 hipError_t launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream);

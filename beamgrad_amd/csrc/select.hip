@@ -1,0 +1,577 @@
+// SPDX-License-Identifier: MIT
+//
+// The select pass of the decode: one workgroup per example walks the T steps
+// (or the one step of the step API) over the row pass's shortlists.
+//
+// Per step it stages the step's row statistics and shortlists in LDS, builds
+// the candidates (EOS carry-forward; shortlist entries with n-gram blocking
+// and the repetition penalty), keeps the best K in an LDS collector under the
+// reference's total order (reference src/common.hpp:269-302), and then proves
+// the selection exact: a row whose bound could still beat the K-th selected
+// candidate is rescanned in full from HBM. The trace, the beam state and the
+// prefixes advance as in reference src/decoder.cpp:122-187, 314-350.
+#include <hip/hip_runtime.h>
+
+#include "device_common.hpp"
+
+namespace dbs_hip {
+
+namespace {
+
+// Rows rescanned since the last reset (read through dbs_hip_profile_read).
+__device__ unsigned long long g_rescanned_rows;
+
+constexpr int kRescanBuf = 512;   // candidates of one rescanned row kept before falling back
+constexpr int kRescanPerThread = 16;
+
+struct Lds {
+    Cand* buf;        // [sort_cap] the collector
+    Cand* rbuf;       // [kRescanBuf] one rescanned row's candidates
+    float* raw;       // [K] beams after the previous step
+    float* nraw;      // [K] beams after this step (also scratch)
+    float* rbound;    // [K]
+    float* pen;       // [pen_len] length penalty by length
+    float* inv;       // [pen_len] 1 / penalty
+    int32_t* len;
+    int32_t* nlen;
+    int32_t* last;
+    int32_t* nlast;
+    int32_t* ended;
+    int32_t* nended;
+    int32_t* rcount;  // [K] shortlist entries of the beam's row (-2 not read, -1 no shortlist, -3 failed check)
+    int32_t* plen;    // [2K] prefix lengths
+    int32_t* nblk;    // [K] n-gram-blocked tokens of each beam
+    ShortEntry* sl;   // [K * M] the step's shortlists
+    int32_t* prefix;  // [2, K, P] (LDS) or the example's slice of the workspace
+    int32_t* blk;     // [K, P] (LDS) or workspace
+};
+
+struct State {
+    int count;
+    int any_fail;
+    int rcount;
+    int overflow;
+    uint32_t invalid;
+    float tau;
+    Cand thr;
+};
+
+__device__ __forceinline__ float pen_of(const Lds& s, int pen_len, int l, float alpha) {
+    const int c = l > 1 ? l : 1;
+    return c < pen_len ? s.pen[c] : length_penalty(c, alpha);
+}
+
+__device__ __forceinline__ float inv_of(const Lds& s, int pen_len, int l, float alpha) {
+    const int c = l > 1 ? l : 1;
+    return c < pen_len ? s.inv[c] : 1.0f / length_penalty(c, alpha);
+}
+
+struct PrefixView {
+    const int32_t* tok;
+    int len;
+};
+
+__device__ __forceinline__ PrefixView prefix_of(const DecodeParams& p, const Lds& s, int b, int k, int cur) {
+    if (p.step_mode) {
+        const int l = s.len[k];
+        const int L = l < 0 ? 0 : (l < p.st_stride ? l : p.st_stride);
+        return PrefixView{p.st_prefix + (static_cast<int64_t>(b) * p.K + k) * p.st_stride, L};
+    }
+    return PrefixView{s.prefix + (static_cast<int64_t>(cur) * p.K + k) * p.prefix_cap, s.plen[cur * p.K + k]};
+}
+
+__device__ __forceinline__ bool in_list(const int32_t* a, int n, int v) {
+    for (int i = 0; i < n; ++i)
+        if (a[i] == v) return true;
+    return false;
+}
+
+// The candidate of token v (finite log-prob lp, statically allowed) in the
+// row of beam k; false when n-gram blocking removes it. A token of the prefix
+// pays the repetition penalty: raw = p + (lp - log(rep)) (reference
+// src/decoder.cpp:196-258).
+__device__ __forceinline__ bool make_cand(const DecodeParams& p, const Lds& s, const PrefixView& pre, int k,
+                                          float praw, float inv_pen, int v, int new_len, float lp, Cand& c) {
+    float value = lp;
+    if (p.constrained) {
+        if (p.ngram == 1) {
+            if (in_list(pre.tok, pre.len, v)) return false;
+        } else if (p.ngram > 1 && in_list(s.blk + static_cast<int64_t>(k) * p.prefix_cap, s.nblk[k], v)) {
+            return false;
+        }
+        if (p.penalise && in_list(pre.tok, pre.len, v)) value = lp - p.log_rep;
+    }
+    const float raw = praw + value;
+    c = Cand{raw * inv_pen, raw, k, v, new_len, 1};
+    return true;
+}
+
+__device__ void sort_cands(Cand* buf, int np) {
+    const int tid = static_cast<int>(threadIdx.x);
+    for (int kk = 2; kk <= np; kk <<= 1) {
+        for (int j = kk >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < np; i += kSelectThreads) {
+                const int partner = i ^ j;
+                if (partner > i) {
+                    const bool desc = (i & kk) == 0;
+                    const Cand a = buf[i], c = buf[partner];
+                    if (desc ? before(c, a) : before(a, c)) {
+                        buf[i] = c;
+                        buf[partner] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Sorts the collected candidates, keeps the best K, and raises the admission
+// threshold to the K-th kept one when that is better.
+__device__ void compact(Lds& s, State& st, int K) {
+    __syncthreads();
+    const int n = st.count;
+    int np = 1;
+    while (np < n) np <<= 1;
+    for (int i = n + static_cast<int>(threadIdx.x); i < np; i += kSelectThreads) s.buf[i] = dead_cand();
+    __syncthreads();
+    sort_cands(s.buf, np);
+    if (threadIdx.x == 0) {
+        st.count = n < K ? n : K;
+        if (st.count == K && before(s.buf[K - 1], st.thr)) st.thr = s.buf[K - 1];
+    }
+    __syncthreads();
+}
+
+// Admits c unless it ranks after the threshold (a candidate offered earlier,
+// or the dead sentinel). Equal admits: after a rescan removed the threshold's
+// own row from the collector, the threshold itself must come back.
+__device__ __forceinline__ void offer(Lds& s, State& st, const Cand& c) {
+    if (before(st.thr, c)) return;
+    const int slot = atomicAdd(&st.count, 1);
+    s.buf[slot] = c;
+}
+
+__device__ __forceinline__ void end_round(Lds& s, State& st, int K, int sort_cap) {
+    __syncthreads();
+    if (st.count > sort_cap - kSelectThreads) compact(s, st, K);
+}
+
+// Every candidate of row `row` (beam k) that does not rank after the
+// threshold: gathered into the rescan buffer in one sweep, then offered to the
+// collector. A buffer overflow (a row with very many candidates at the
+// threshold) falls back to offering round by round.
+template <int DT, bool LOGITS>
+__device__ void rescan_row(const DecodeParams& p, Lds& s, State& st, int b, int k, int64_t row, float lse,
+                           float praw, float inv_pen, int new_len, const PrefixView& pre, int sort_cap) {
+    const bool mask_eos = new_len < p.min_length;
+    const int V = p.V;
+    const int tid = static_cast<int>(threadIdx.x);
+    const size_t esz = DT == 0 ? 4 : 2;
+    const char* base = static_cast<const char*>(p.x) + static_cast<size_t>(row) * static_cast<size_t>(V) * esz;
+    if (tid == 0) {
+        st.rcount = 0;
+        st.overflow = 0;
+    }
+    __syncthreads();
+    const Cand thr = st.thr;
+    for (int v0 = 0; v0 < V; v0 += kSelectThreads * kRescanPerThread) {
+        float xs[kRescanPerThread];
+#pragma unroll
+        for (int j = 0; j < kRescanPerThread; ++j) {
+            const int v = v0 + j * kSelectThreads + tid;
+            xs[j] = v < V ? load_one<DT>(base, v) : -kInf;
+        }
+#pragma unroll
+        for (int j = 0; j < kRescanPerThread; ++j) {
+            const int v = v0 + j * kSelectThreads + tid;
+            const float lp = LOGITS ? xs[j] - lse : xs[j];
+            if (v >= V || !(lp < kInf) || lp == -kInf) continue;
+            const float raw0 = praw + lp;
+            const Cand c0{raw0 * inv_pen, raw0, k, v, new_len, 1};
+            if (before(thr, c0)) continue;  // penalties only lower a candidate
+            if (static_masked(p, b, v, mask_eos)) continue;
+            Cand c;
+            if (!make_cand(p, s, pre, k, praw, inv_pen, v, new_len, lp, c)) continue;
+            if (before(thr, c)) continue;
+            const int slot = atomicAdd(&st.rcount, 1);
+            if (slot < kRescanBuf) s.rbuf[slot] = c;
+            else st.overflow = 1;
+        }
+    }
+    __syncthreads();
+    if (!st.overflow) {
+        const int n = st.rcount;
+        for (int r0 = 0; r0 < n; r0 += kSelectThreads) {
+            if (r0 + tid < n) offer(s, st, s.rbuf[r0 + tid]);
+            end_round(s, st, p.K, sort_cap);
+        }
+        return;
+    }
+    // very many candidates at the threshold: offer the row round by round
+    for (int v0 = 0; v0 < V; v0 += kSelectThreads) {
+        const int v = v0 + tid;
+        if (v < V) {
+            const float x = load_one<DT>(base, v);
+            const float lp = LOGITS ? x - lse : x;
+            if ((lp < kInf) && lp != -kInf && !static_masked(p, b, v, mask_eos)) {
+                Cand c;
+                if (make_cand(p, s, pre, k, praw, inv_pen, v, new_len, lp, c)) offer(s, st, c);
+            }
+        }
+        end_round(s, st, p.K, sort_cap);
+    }
+}
+
+template <int DT, bool LOGITS>
+__global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, SelectLayout L) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ State st;
+    const int K = p.K, T = p.T, M = p.M;
+    const int b = static_cast<int>(blockIdx.x);
+    const int tid = static_cast<int>(threadIdx.x);
+
+    Lds s;
+    s.buf = reinterpret_cast<Cand*>(smem + L.off_buf);
+    s.rbuf = reinterpret_cast<Cand*>(smem + L.off_rbuf);
+    float* f = reinterpret_cast<float*>(smem + L.off_f32);
+    s.raw = f;
+    s.nraw = f + K;
+    s.rbound = f + 2 * K;
+    s.pen = f + 3 * K;
+    s.inv = f + 3 * K + L.pen_len;
+    int32_t* q = reinterpret_cast<int32_t*>(smem + L.off_i32);
+    s.len = q;
+    s.nlen = q + K;
+    s.last = q + 2 * K;
+    s.nlast = q + 3 * K;
+    s.ended = q + 4 * K;
+    s.nended = q + 5 * K;
+    s.rcount = q + 6 * K;
+    s.plen = q + 7 * K;
+    s.nblk = q + 9 * K;
+    s.sl = reinterpret_cast<ShortEntry*>(smem + L.off_sl);
+    s.prefix = L.prefix_in_lds ? reinterpret_cast<int32_t*>(smem + L.off_prefix)
+                               : p.prefix + static_cast<int64_t>(b) * 2 * K * p.prefix_cap;
+    s.blk = L.blk_in_lds ? reinterpret_cast<int32_t*>(smem + L.off_blk)
+                         : p.blocked + static_cast<int64_t>(b) * K * p.prefix_cap;
+
+    const int steps_b = p.step_mode ? 1 : example_steps(p, b);
+    const int T_loop = p.step_mode ? 1 : T;
+    const int pen_len = L.pen_len;
+    for (int l = tid; l < pen_len; l += kSelectThreads) {
+        const float pl = length_penalty(l, p.alpha);
+        s.pen[l] = pl;
+        s.inv[l] = 1.0f / pl;
+    }
+    // Initial state (reference src/decoder.cpp:46-56) or the caller's (:84-103).
+    for (int k = tid; k < K; k += kSelectThreads) {
+        if (p.step_mode) {
+            const int64_t i = static_cast<int64_t>(b) * K + k;
+            s.raw[k] = p.st_raw[i];
+            s.len[k] = p.st_len[i];
+            s.ended[k] = p.st_fin[i] != 0;
+            const int l = p.st_len[i];
+            s.last[k] = (p.st_prefix && l >= 1 && l <= p.st_stride) ? p.st_prefix[i * p.st_stride + (l - 1)] : -1;
+        } else {
+            s.raw[k] = k == 0 ? 0.0f : -kInf;
+            s.len[k] = 0;
+            s.ended[k] = 0;
+            s.last[k] = -1;
+        }
+        s.plen[k] = 0;
+        s.plen[K + k] = 0;
+    }
+    if (tid == 0) st.invalid = 0;
+    __syncthreads();
+
+    int cur = 0;
+    for (int t = 0; t < T_loop; ++t) {
+        const int64_t trace0 = (static_cast<int64_t>(b) * T + t) * K;  // step mode: T == 1
+        if (t >= steps_b) {
+            // padding step (reference src/c_api.cpp:764-781)
+            for (int k = tid; k < K; k += kSelectThreads) {
+                if (p.tokens) p.tokens[trace0 + k] = -1;
+                if (p.parents) p.parents[trace0 + k] = -1;
+                if (p.lengths) p.lengths[trace0 + k] = 0;
+                if (p.scores) p.scores[trace0 + k] = -kInf;
+                if (p.raw_scores) p.raw_scores[trace0 + k] = -kInf;
+                if (p.from_logprob) p.from_logprob[trace0 + k] = 0;
+            }
+            continue;
+        }
+        if (tid == 0) {
+            st.count = 0;
+            st.any_fail = 0;
+            st.tau = -kInf;
+            st.thr = dead_cand();
+        }
+        // Stage the step: row statistics of the rows read, the shortlists,
+        // and the n-gram-blocked tokens of each beam.
+        for (int k = tid; k < K; k += kSelectThreads) {
+            const float praw = s.raw[k];
+            const bool live = praw < kInf && praw > -kInf;
+            const bool carried = live && p.eos >= 0 && s.ended[k];
+            int cnt = -2;
+            float bound = -kInf;
+            if (live && !carried) {
+                const RowInfo info = p.rowinfo[trace0 + k];
+                if (info.invalid) atomicOr(&st.invalid, 1u);
+                if (p.row_lse && LOGITS) p.row_lse[trace0 + k] = info.lse;
+                cnt = M > 0 ? info.count : -1;
+                bound = info.bound;
+                s.nraw[k] = info.lse;  // the row's logsumexp, kept for a rescan
+                if (p.constrained && p.ngram > 1) {
+                    const PrefixView pre = prefix_of(p, s, b, k, cur);
+                    const int n = p.ngram;
+                    int nb = 0;
+                    int32_t* out = s.blk + static_cast<int64_t>(k) * p.prefix_cap;
+                    if (pre.len >= n - 1) {
+                        const int tail = pre.len - (n - 1);
+                        for (int i = 0; i + n <= pre.len; ++i) {
+                            bool same = true;
+                            for (int j = 0; j < n - 1 && same; ++j) same = pre.tok[i + j] == pre.tok[tail + j];
+                            if (same) out[nb++] = pre.tok[i + n - 1];
+                        }
+                    }
+                    s.nblk[k] = nb;
+                }
+            }
+            s.rcount[k] = cnt;
+            s.rbound[k] = bound;
+        }
+        if (M > 0) {
+            const ShortEntry* src = p.shortlist + trace0 * M;
+            for (int i = tid; i < K * M; i += kSelectThreads) s.sl[i] = src[i];
+        }
+        __syncthreads();
+        if (p.use_tau) {
+            // The first K entries of a shortlist are real candidates with raw
+            // >= fl(p + lp_K) (raw is monotone in lp): at least K expanded
+            // candidates reach the largest such value over the rows.
+            if (tid < 64) {
+                float best = -kInf;
+                for (int k = tid; k < K; k += 64)
+                    if (s.rcount[k] >= K) best = fmaxf(best, s.raw[k] + s.sl[k * M + (K - 1)].lp);
+                best = wave_max(best);
+                if (tid == 0) st.tau = best;
+            }
+            __syncthreads();
+        }
+
+        // Carried-forward beams (reference src/decoder.cpp:131-139).
+        for (int k = tid; k < K; k += kSelectThreads) {
+            const float praw = s.raw[k];
+            const bool live = praw < kInf && praw > -kInf;
+            if (live && p.eos >= 0 && s.ended[k]) {
+                const int l = s.len[k] > 1 ? s.len[k] : 1;
+                const int32_t last = s.last[k];
+                const Cand c{praw / pen_of(s, pen_len, l, p.alpha), praw, k, is_eos_tok(p, last) ? last : p.eos, l,
+                             0};
+                offer(s, st, c);
+            }
+        }
+        end_round(s, st, K, L.sort_cap);
+
+        // Shortlisted candidates.
+        if (M > 0) {
+            const float tau = st.tau;
+            for (int base = 0; base < K * M; base += kSelectThreads) {
+                const int item = base + tid;
+                if (item < K * M) {
+                    const int k = item / M;
+                    const int i = item - k * M;
+                    if (i < s.rcount[k]) {
+                        const ShortEntry e = s.sl[item];
+                        const float praw = s.raw[k];
+                        if (!(praw + e.lp < tau)) {
+                            const int new_len = s.len[k] + 1;
+                            const PrefixView pre = prefix_of(p, s, b, k, cur);
+                            Cand c;
+                            if (make_cand(p, s, pre, k, praw, inv_of(s, pen_len, new_len, p.alpha), e.token, new_len,
+                                          e.lp, c))
+                                offer(s, st, c);
+                        }
+                    }
+                }
+                end_round(s, st, K, L.sort_cap);
+            }
+        }
+        compact(s, st, K);
+
+        // Exactness: every candidate left out of a row's shortlist has raw <=
+        // fl(p + bound); a row passes when the K-th selected candidate ranks
+        // strictly before that bound's score and raw.
+        for (int k = tid; k < K; k += kSelectThreads) {
+            const int cnt = s.rcount[k];
+            if (cnt == -2) continue;
+            bool fail = cnt < 0;
+            if (!fail && s.rbound[k] > -kInf) {
+                const float X = s.raw[k] + s.rbound[k];
+                if (X > -kInf) {
+                    const float SX = X * inv_of(s, pen_len, s.len[k] + 1, p.alpha);
+                    const Cand kth = st.count >= K ? s.buf[K - 1] : dead_cand();
+                    fail = !((kth.score > SX) || (kth.score == SX && kth.raw > X));
+                }
+            }
+            if (fail) {
+                s.rcount[k] = -3;
+                atomicOr(&st.any_fail, 1);
+            }
+        }
+        __syncthreads();
+        if (st.any_fail) {
+            for (int k = 0; k < K; ++k) {
+                if (s.rcount[k] != -3) continue;
+                if (tid == 0) atomicAdd(&g_rescanned_rows, 1ull);
+                // drop the row's shortlisted candidates, then offer the whole row
+                for (int i = tid; i < st.count; i += kSelectThreads)
+                    if (s.buf[i].parent == k && s.buf[i].flp) s.buf[i] = dead_cand();
+                __syncthreads();
+                const float praw = s.raw[k];
+                const int new_len = s.len[k] + 1;
+                const int64_t row = p.step_mode ? static_cast<int64_t>(b) * K + k : trace0 + k;
+                const PrefixView pre = prefix_of(p, s, b, k, cur);
+                rescan_row<DT, LOGITS>(p, s, st, b, k, row, LOGITS ? s.nraw[k] : 0.0f, praw,
+                                       inv_of(s, pen_len, new_len, p.alpha), new_len, pre, L.sort_cap);
+            }
+            compact(s, st, K);
+        }
+
+        // Selection (reference src/decoder.cpp:314-350).
+        const int nsel = st.count;
+        for (int k = tid; k < K; k += kSelectThreads) {
+            const Cand c = k < nsel ? s.buf[k] : dead_cand();
+            const int64_t o = trace0 + k;
+            if (p.tokens) p.tokens[o] = c.token;
+            if (p.parents) p.parents[o] = c.parent;
+            if (p.lengths) p.lengths[o] = c.length;
+            if (p.scores) p.scores[o] = c.score;
+            if (p.raw_scores) p.raw_scores[o] = c.raw;
+            if (p.from_logprob) p.from_logprob[o] = static_cast<uint8_t>(c.flp);
+            s.nraw[k] = c.raw;
+            s.nlen[k] = c.length;
+            s.nlast[k] = c.token;
+            s.nended[k] = c.parent >= 0 ? (s.ended[c.parent] || is_eos_tok(p, c.token)) : 0;
+            if (p.constrained && !p.step_mode) {
+                const int nxt = cur ^ 1;
+                s.plen[nxt * K + k] =
+                    c.parent >= 0 ? s.plen[cur * K + c.parent] + ((c.flp && c.token >= 0) ? 1 : 0) : 0;
+            }
+        }
+        __syncthreads();
+        if (p.constrained && !p.step_mode) {
+            // each selected beam: its parent's prefix, then its token
+            const int nxt = cur ^ 1;
+            const int P = p.prefix_cap;
+            for (int k = 0; k < K; ++k) {
+                const Cand c = k < nsel ? s.buf[k] : dead_cand();
+                if (c.parent < 0) continue;
+                const int Lp = s.plen[cur * K + c.parent];
+                const int32_t* src = s.prefix + (static_cast<int64_t>(cur) * K + c.parent) * P;
+                int32_t* dst = s.prefix + (static_cast<int64_t>(nxt) * K + k) * P;
+                for (int i = tid; i < Lp; i += kSelectThreads) dst[i] = src[i];
+                if (tid == 0 && c.flp && c.token >= 0) dst[Lp] = c.token;
+            }
+            cur = nxt;
+        }
+        for (int k = tid; k < K; k += kSelectThreads) {
+            s.raw[k] = s.nraw[k];
+            s.len[k] = s.nlen[k];
+            s.last[k] = s.nlast[k];
+            s.ended[k] = s.nended[k];
+        }
+        __syncthreads();
+    }
+
+    // Final scores (reference src/decoder.cpp:179-187) and the state (step mode).
+    for (int k = tid; k < K; k += kSelectThreads) {
+        const int64_t i = static_cast<int64_t>(b) * K + k;
+        if (p.final_scores) p.final_scores[i] = s.raw[k] / pen_of(s, pen_len, s.len[k], p.alpha);
+        if (p.final_raw) p.final_raw[i] = s.raw[k];
+        if (p.final_lengths) p.final_lengths[i] = s.len[k];
+        if (p.step_mode) {
+            p.st_raw[i] = s.raw[k];
+            p.st_len[i] = s.len[k];
+            p.st_fin[i] = static_cast<uint8_t>(s.ended[k] != 0);
+        }
+    }
+    if (tid == 0 && p.invalid) p.invalid[b] = static_cast<uint8_t>(st.invalid != 0);
+}
+
+template <int DT, bool LOGITS>
+hipError_t launch_select_typed(const DecodeParams& p, const SelectLayout& L, hipStream_t stream) {
+    if (L.smem > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<DT, LOGITS>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L.smem));
+        if (e != hipSuccess) return e;
+    }
+    KernelTimer timer(kKindSelect, stream);
+    hipLaunchKernelGGL((select_kernel<DT, LOGITS>), dim3(p.B), dim3(kSelectThreads), L.smem, stream, p, L);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool step_mode, int prefix_cap) {
+    (void)B;
+    SelectLayout L{};
+    int sc = 1;
+    while (sc < K + 2 * kSelectThreads) sc <<= 1;
+    L.sort_cap = sc;
+    L.pen_len = step_mode ? 0 : T + 2;
+    auto align = [](size_t x) { return (x + 15) & ~static_cast<size_t>(15); };
+    size_t off = 0;
+    L.off_buf = off;
+    off = align(off + sizeof(Cand) * static_cast<size_t>(sc));
+    L.off_rbuf = off;
+    off = align(off + sizeof(Cand) * kRescanBuf);
+    L.off_f32 = off;
+    off = align(off + sizeof(float) * (3 * static_cast<size_t>(K) + 2 * static_cast<size_t>(L.pen_len)));
+    L.off_i32 = off;
+    off = align(off + sizeof(int32_t) * 10 * static_cast<size_t>(K));
+    L.off_sl = off;
+    off = align(off + sizeof(ShortEntry) * static_cast<size_t>(K) * static_cast<size_t>(M));
+    const size_t prefix_bytes = sizeof(int32_t) * 2 * static_cast<size_t>(K) * static_cast<size_t>(prefix_cap);
+    const size_t blk_bytes = sizeof(int32_t) * static_cast<size_t>(K) * static_cast<size_t>(prefix_cap);
+    const size_t budget = 150 * 1024;
+    L.prefix_in_lds = 0;
+    L.blk_in_lds = 0;
+    if (constrained && !step_mode && off + prefix_bytes <= budget) {
+        L.prefix_in_lds = 1;
+        L.off_prefix = off;
+        off = align(off + prefix_bytes);
+    }
+    if (constrained && off + blk_bytes <= budget) {
+        L.blk_in_lds = 1;
+        L.off_blk = off;
+        off = align(off + blk_bytes);
+    }
+    L.smem = off;
+    return L;
+}
+
+hipError_t launch_select(const DecodeParams& p, const SelectLayout& L, hipStream_t stream) {
+    if (p.from_logits) {
+        switch (p.dtype) {
+            case 0: return launch_select_typed<0, true>(p, L, stream);
+            case 1: return launch_select_typed<1, true>(p, L, stream);
+            default: return launch_select_typed<2, true>(p, L, stream);
+        }
+    }
+    switch (p.dtype) {
+        case 0: return launch_select_typed<0, false>(p, L, stream);
+        case 1: return launch_select_typed<1, false>(p, L, stream);
+        default: return launch_select_typed<2, false>(p, L, stream);
+    }
+}
+
+hipError_t rescan_counter(int reset, unsigned long long* value) {
+    if (reset) {
+        const unsigned long long zero = 0;
+        return hipMemcpyToSymbol(HIP_SYMBOL(g_rescanned_rows), &zero, sizeof(zero));
+    }
+    return hipMemcpyFromSymbol(value, HIP_SYMBOL(g_rescanned_rows), sizeof(*value));
+}
+
+}  // namespace dbs_hip

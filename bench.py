@@ -237,6 +237,9 @@ def main() -> int:
         lib.dbs_hip_profile_read(kind, C.byref(ms), C.byref(n))
         if n.value:
             kernels[name] = {"avg_ms": ms.value / n.value, "launches": n.value}
+    ms, n = C.c_double(), C.c_int64()
+    lib.dbs_hip_profile_read(5, C.byref(ms), C.byref(n))
+    rescans_per_step = n.value / args.steps
     lib.dbs_hip_profile_enable(0)
 
     ms_per_step = gpu_ms / args.steps
@@ -270,6 +273,7 @@ def main() -> int:
                    "step_hbm_gbs": alg_bytes / (ms_per_step / 1e3) / 1e9,
                    "step_hbm_frac": alg_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS,
                    "kernels_ms": {k: round(v["avg_ms"], 4) for k, v in kernels.items()},
+                   "rescanned_rows_per_step": rescans_per_step,
                    "wall_s": round(wall, 3)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": "row_pass",
