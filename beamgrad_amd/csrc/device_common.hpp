@@ -1,6 +1,6 @@
 // SPDX-License-Identifier: MIT
 //
-// Device helpers shared by the row pass and the select pass.
+// Device helpers shared by the row-pass kernels and the select pass.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -47,6 +47,175 @@ __device__ __forceinline__ int example_steps(const DecodeParams& p, int b) { ret
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;
+}
+
+// Orders the LDS accesses of one wavefront (its lanes run in lockstep and the
+// LDS serves a wavefront's requests in issue order).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Whether the search may read row r, with its example and the length a token
+// taken from it gives (decode: row (b, t, k) is read only for t < steps[b],
+// and at t = 0 only beam 0; step: live, unfinished beams).
+__device__ __forceinline__ bool row_is_read(const DecodeParams& p, int64_t r, int& b, int& new_len) {
+    const int K = p.K;
+    if (p.step_mode) {
+        b = static_cast<int>(r / K);
+        const float praw = p.st_raw[r];
+        if (!(praw < kInf && praw > -kInf)) return false;  // dead beam
+        if (p.eos >= 0 && p.st_fin[r]) return false;        // finished
+        new_len = p.st_len[r] + 1;
+        return true;
+    }
+    b = static_cast<int>(r / (static_cast<int64_t>(p.T) * K));
+    const int t = static_cast<int>((r / K) % p.T);
+    const int k = static_cast<int>(r % K);
+    if (t >= example_steps(p, b) || (t == 0 && k != 0)) return false;
+    new_len = t + 1;  // every unfinished live beam has length t at step t
+    return true;
+}
+
+// Bitonic sort (descending) of 256 values held 4 per lane (element i = 4 *
+// lane + e) across one wavefront.
+__device__ __forceinline__ void sort256_desc(float (&a)[4], int lane) {
+    for (int k = 2; k <= 256; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            if (j >= 4) {
+                const int lj = j >> 2;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float other = __shfl_xor(a[e], lj);
+                    const int i = 4 * lane + e;
+                    const bool desc = (i & k) == 0;
+                    const bool is_lo = (i & j) == 0;
+                    a[e] = (is_lo == desc) ? fmaxf(a[e], other) : fminf(a[e], other);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int i = 4 * lane + e;
+                    if ((i & j) == 0) {
+                        const int e2 = e + j;
+                        const bool desc = (i & k) == 0;
+                        const float lo = a[e], hi = a[e2];
+                        const bool swap = desc ? (hi > lo) : (lo > hi);
+                        if (swap) {
+                            a[e] = hi;
+                            a[e2] = lo;
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// The M-th largest of 256 lane maxima held 4 per lane (M <= 256): at least M
+// elements of the row are >= it.
+__device__ __forceinline__ float shortlist_threshold(float (&a)[4], int lane, int M) {
+    sort256_desc(a, lane);
+    const int idx = M - 1;
+    const float mine = a[idx & 3];
+    return __shfl(mine, idx >> 2);
+}
+
+// Combination of the 256 logsumexp lane sums held 4 per lane (lane j = 4 *
+// lane + e), pairwise with strides 128, 64, ..., 1: lane j += lane j + s
+// (reference src/kernels.hpp:196-202).
+__device__ __forceinline__ float lane_tree_sum(float (&acc)[4], int lane) {
+    for (int s = 128; s >= 4; s >>= 1) {
+        const int d = s >> 2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float other = __shfl_down(acc[e], d);
+            if (4 * lane + e < s) acc[e] = acc[e] + other;
+        }
+    }
+    acc[0] = acc[0] + acc[2];
+    acc[1] = acc[1] + acc[3];
+    acc[0] = acc[0] + acc[1];
+    return __shfl(acc[0], 0);
+}
+
+// Survivor key: value descending, then token ascending.
+__device__ __forceinline__ uint64_t survivor_key(float x, int v) {
+    return (static_cast<uint64_t>(ordered_key(x)) << 32) |
+           static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(v));
+}
+
+// One wavefront: sorts the n row survivors (finite x >= theta) kept in LDS
+// and writes the row's shortlist (the best M allowed tokens by value desc,
+// token asc, as log-probs) and RowInfo: the bound on every allowed token left
+// out is the (M+1)-th allowed survivor, else theta. FILTER: the survivors may
+// include statically masked tokens (banned, EOS below min_length of example
+// b), which are dropped here (key 0 sorts last).
+template <bool LOGITS, bool FILTER>
+__device__ void finish_row_wave(const DecodeParams& p, int64_t r, float lse, float theta, bool any_bad,
+                                uint64_t* s_key, float* s_x, int n, int lane, int b, bool mask_eos) {
+    const int M = p.M;
+    RowInfo info;
+    info.lse = lse;
+    info.invalid = any_bad ? 1u : 0u;
+    info.bound = -kInf;
+    info.count = 0;
+    if (M > 0 && !(LOGITS && lse == -kInf)) {
+        if (n > kSurvivorCap) {
+            info.count = -1;
+        } else {
+            int np = 1;
+            while (np < n) np <<= 1;
+            int dropped = 0;
+            if constexpr (FILTER) {
+                for (int i0 = 0; i0 < n; i0 += 64) {
+                    const int i = i0 + lane;
+                    bool drop = false;
+                    if (i < n) {
+                        const int v = static_cast<int>(0xffffffffu - static_cast<uint32_t>(s_key[i] & 0xffffffffu));
+                        drop = static_masked(p, b, v, mask_eos);
+                        if (drop) s_key[i] = 0;
+                    }
+                    dropped += __popcll(__ballot(drop));
+                }
+            }
+            for (int i = n + lane; i < np; i += 64) s_key[i] = 0;
+            wave_sync();
+            for (int kk = 2; kk <= np; kk <<= 1) {
+                for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+                    for (int i = lane; i < np; i += 64) {
+                        const int partner = i ^ jj;
+                        if (partner > i) {
+                            const bool desc = (i & kk) == 0;
+                            const uint64_t ki = s_key[i], kp = s_key[partner];
+                            if (desc ? (kp > ki) : (ki > kp)) {
+                                s_key[i] = kp;
+                                s_key[partner] = ki;
+                                const float xi = s_x[i];
+                                s_x[i] = s_x[partner];
+                                s_x[partner] = xi;
+                            }
+                        }
+                    }
+                    wave_sync();
+                }
+            }
+            n -= dropped;
+            const int cnt = n < M ? n : M;
+            ShortEntry* out = p.shortlist + r * M;
+            for (int i = lane; i < cnt; i += 64) {
+                const float x = s_x[i];
+                const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(s_key[i] & 0xffffffffu));
+                out[i].lp = LOGITS ? x - lse : x;
+                out[i].token = tok;
+            }
+            const float bx = n > M ? s_x[M] : theta;
+            info.count = cnt;
+            info.bound = (bx > -kInf) ? (LOGITS ? bx - lse : bx) : -kInf;
+        }
+    }
+    if (lane == 0) p.rowinfo[r] = info;
 }
 
 }  // namespace dbs_hip

@@ -122,6 +122,10 @@ SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool st
 // Queues the decode (or one step) on `stream`; returns a hipError_t.
 hipError_t launch_decode(const DecodeParams& p, const DecodeLayout& L, hipStream_t stream);
 hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream);
+// Row pass that keeps each row on chip (16-bit rows, V % 8 == 0, 16-byte
+// aligned, V <= 155648); launch_row_pass uses it when eligible.
+bool row_resident_eligible(const DecodeParams& p);
+hipError_t launch_row_resident(const DecodeParams& p, int64_t rows, hipStream_t stream);
 hipError_t launch_select(const DecodeParams& p, const SelectLayout& L, hipStream_t stream);
 
 // Rows the select pass rescanned in full (reset = 1 clears the count).

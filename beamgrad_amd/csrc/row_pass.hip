@@ -10,6 +10,8 @@
 // selection exact.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+
 #include "device_common.hpp"
 
 namespace dbs_hip {
@@ -53,42 +55,6 @@ __device__ __forceinline__ void load4(const void* row, int v, int V, float (&x)[
 // Row pass
 // ---------------------------------------------------------------------------
 
-// Bitonic sort (descending) of the 256 lane maxima held 4 per thread
-// (element i = 4 * lane + e) across one wavefront.
-__device__ __forceinline__ void sort256_desc(float (&a)[4], int lane) {
-    for (int k = 2; k <= 256; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            if (j >= 4) {
-                const int lj = j >> 2;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float other = __shfl_xor(a[e], lj);
-                    const int i = 4 * lane + e;
-                    const bool desc = (i & k) == 0;
-                    const bool is_lo = (i & j) == 0;
-                    a[e] = (is_lo == desc) ? fmaxf(a[e], other) : fminf(a[e], other);
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int i = 4 * lane + e;
-                    if ((i & j) == 0) {
-                        const int e2 = e + j;
-                        const bool desc = (i & k) == 0;
-                        const float lo = a[e], hi = a[e2];
-                        const bool swap = desc ? (hi > lo) : (lo > hi);
-                        if (swap) {
-                            a[e] = hi;
-                            a[e2] = lo;
-                        }
-                    }
-                }
-            }
-        }
-    }
-}
-
-
 template <int DT, bool LOGITS, bool VEC>
 __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
     __shared__ uint64_t s_key[kSurvivorCap];
@@ -97,23 +63,9 @@ __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
 
     const int lane = static_cast<int>(threadIdx.x);
     const int64_t r = blockIdx.x;
-    const int K = p.K, V = p.V;
-    int b, t, k, new_len;
-    if (p.step_mode) {
-        b = static_cast<int>(r / K);
-        k = static_cast<int>(r % K);
-        t = 0;
-        const float praw = p.st_raw[r];
-        if (!(praw < kInf && praw > -kInf)) return;           // dead beam: not read
-        if (p.eos >= 0 && p.st_fin[r]) return;               // finished: not read
-        new_len = p.st_len[r] + 1;
-    } else {
-        b = static_cast<int>(r / (static_cast<int64_t>(p.T) * K));
-        t = static_cast<int>((r / K) % p.T);
-        k = static_cast<int>(r % K);
-        if (t >= example_steps(p, b) || (t == 0 && k != 0)) return;  // never read
-        new_len = t + 1;  // every unfinished live beam has length t at step t
-    }
+    const int V = p.V;
+    int b, new_len;
+    if (!row_is_read(p, r, b, new_len)) return;
     const bool mask_eos = new_len < p.min_length;
     const size_t esz = DT == 0 ? 4 : 2;
     const char* row = static_cast<const char*>(p.x) + static_cast<size_t>(r) * static_cast<size_t>(V) * esz;
@@ -143,10 +95,7 @@ __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
     float theta = -kInf;
     if (M > 0) {
         float a[4] = {lmax[0], lmax[1], lmax[2], lmax[3]};
-        sort256_desc(a, lane);
-        const int idx = M - 1;
-        const float mine = a[idx & 3];
-        theta = __shfl(mine, idx >> 2);
+        theta = shortlist_threshold(a, lane, M);
     }
     if (lane == 0) s_count = 0;
     __syncthreads();
@@ -169,8 +118,7 @@ __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
                 if (M > 0 && finite && x[e] >= theta && !static_masked(p, b, v + e, mask_eos)) {
                     const int slot = atomicAdd(&s_count, 1);
                     if (slot < kSurvivorCap) {
-                        s_key[slot] = (static_cast<uint64_t>(ordered_key(x[e])) << 32) |
-                                      static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(v + e));
+                        s_key[slot] = survivor_key(x[e], v + e);
                         s_x[slot] = x[e];
                     }
                 }
@@ -181,74 +129,14 @@ __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
     float lse = 0.0f;
     if (LOGITS) {
         if (do_lse) {
-            // pairwise tree over the 256 lanes: lane j += lane j + s, s = 128 .. 1
-            for (int s = 128; s >= 4; s >>= 1) {
-                const int d = s >> 2;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float other = __shfl_down(acc[e], d);
-                    if (4 * lane + e < s) acc[e] = acc[e] + other;
-                }
-            }
-            acc[0] = acc[0] + acc[2];
-            acc[1] = acc[1] + acc[3];
-            acc[0] = acc[0] + acc[1];
-            const float sum = __shfl(acc[0], 0);
-            lse = logsumexp_from(rmax, sum);
+            lse = logsumexp_from(rmax, lane_tree_sum(acc, lane));
         } else {
             lse = -kInf;
         }
     }
     __syncthreads();
 
-    RowInfo info;
-    info.lse = lse;
-    info.invalid = any_bad ? 1u : 0u;
-    info.bound = -kInf;
-    info.count = 0;
-    if (M > 0 && !(LOGITS && lse == -kInf)) {
-        const int n = s_count;
-        if (n > kSurvivorCap) {
-            info.count = -1;
-        } else {
-            int np = 1;
-            while (np < n) np <<= 1;
-            for (int i = n + lane; i < np; i += kRowThreads) s_key[i] = 0;
-            __syncthreads();
-            // bitonic sort of (key, x) descending
-            for (int kk = 2; kk <= np; kk <<= 1) {
-                for (int j = kk >> 1; j > 0; j >>= 1) {
-                    for (int i = lane; i < np; i += kRowThreads) {
-                        const int partner = i ^ j;
-                        if (partner > i) {
-                            const bool desc = (i & kk) == 0;
-                            const uint64_t ki = s_key[i], kp = s_key[partner];
-                            if (desc ? (kp > ki) : (ki > kp)) {
-                                s_key[i] = kp;
-                                s_key[partner] = ki;
-                                const float xi = s_x[i];
-                                s_x[i] = s_x[partner];
-                                s_x[partner] = xi;
-                            }
-                        }
-                    }
-                    __syncthreads();
-                }
-            }
-            const int cnt = n < M ? n : M;
-            ShortEntry* out = p.shortlist + r * M;
-            for (int i = lane; i < cnt; i += kRowThreads) {
-                const float x = s_x[i];
-                const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(s_key[i] & 0xffffffffu));
-                out[i].lp = LOGITS ? x - lse : x;
-                out[i].token = tok;
-            }
-            float bx = n > M ? s_x[M] : theta;
-            info.count = cnt;
-            info.bound = (bx > -kInf) ? (LOGITS ? bx - lse : bx) : -kInf;
-        }
-    }
-    if (lane == 0) p.rowinfo[r] = info;
+    finish_row_wave<LOGITS, false>(p, r, lse, theta, any_bad, s_key, s_x, s_count, lane, b, mask_eos);
 }
 
 
@@ -259,8 +147,13 @@ hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream) {
     if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
     const size_t esz = p.dtype == 0 ? 4 : 2;
     const bool vec = (p.V % 4 == 0) && (reinterpret_cast<uintptr_t>(p.x) % (4 * esz) == 0);
-    const dim3 grid(static_cast<unsigned>(rows));
     KernelTimer timer(kKindRowPass, stream);
+    static const bool resident_off = [] {
+        const char* env = std::getenv("DBS_HIP_RESIDENT");  // testing knob: 0 keeps the two-pass kernel
+        return env != nullptr && env[0] == '0';
+    }();
+    if (!resident_off && row_resident_eligible(p)) return launch_row_resident(p, rows, stream);
+    const dim3 grid(static_cast<unsigned>(rows));
 #define DBS_ROW_PASS(DT, LG)                                                                                 \
     do {                                                                                                     \
         if (vec) hipLaunchKernelGGL((row_pass_kernel<DT, LG, true>), grid, dim3(kRowThreads), 0, stream, p); \

@@ -30,15 +30,19 @@ def log_softmax(x: np.ndarray) -> np.ndarray:
     return (x - m - np.log(np.exp(x - m).sum(-1, keepdims=True))).astype(np.float32)
 
 
-def make_case(seed: int, *, big: bool = False, allow_invalid: bool = True) -> dict:
+def make_case(seed: int, *, big: bool = False, allow_invalid: bool = True, dtypes=None, vocabs=None,
+              scales=None) -> dict:
     rng = np.random.default_rng(seed)
     B = int(rng.integers(1, 5))
     T = int(rng.integers(1, 9))
     K = int(rng.choice([1, 2, 3, 4, 5, 8, 9, 16] + ([33, 64, 100] if big else [])))
-    V = int(rng.choice([2, 3, 7, 40, 255, 256, 257, 1000, 1001, 3000] + ([32000, 50257] if big else [])))
-    dtype = str(rng.choice(["f32", "f16", "bf16"]))
+    vocab_pool = vocabs if vocabs is not None else [2, 3, 7, 40, 255, 256, 257, 1000, 1001, 3000] + (
+        [32000, 50257] if big else [])
+    V = int(rng.choice(vocab_pool))
+    dtype = str(rng.choice(dtypes if dtypes is not None else ["f32", "f16", "bf16"]))
     from_logits = bool(rng.integers(0, 2))
-    x = rng.normal(0.0, float(rng.choice([0.5, 2.0, 3.0])), size=(B, T, K, V)).astype(np.float32)
+    scale = float(rng.choice(scales if scales is not None else [0.5, 2.0, 3.0]))
+    x = rng.normal(0.0, scale, size=(B, T, K, V)).astype(np.float32)
     if not from_logits:
         x = log_softmax(x)
     # exact ties inside rows and across rows

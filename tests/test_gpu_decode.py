@@ -83,3 +83,92 @@ def test_invalid_rows_flagged_only_when_read(hip, oracle):
     out = hip.decode(x, "f32")
     want = oracle.decode(x)
     assert out["invalid"].tolist() == want["invalid"].tolist() == [0, 1, 1]
+
+
+# 16-bit rows with V % 8 == 0 take the row pass that keeps each row on chip
+# (one workgroup per CU); DBS_HIP_RESIDENT=0 selects the two-pass kernel on
+# the same inputs.
+_RESIDENT_VOCABS = [8, 40, 256, 1000, 2048, 3000, 4104, 8200]
+
+
+@pytest.mark.parametrize("resident", ["1", "0"])
+@pytest.mark.parametrize("seed", range(0, 30))
+def test_decode_16bit_row_passes(hip, oracle, seed, resident, monkeypatch):
+    monkeypatch.setenv("DBS_HIP_RESIDENT", resident)
+    case = make_case(9000 + seed, dtypes=["bf16", "f16"], vocabs=_RESIDENT_VOCABS, scales=[0.05, 0.5, 2.0, 3.0, 8.0])
+    _check(hip, oracle, case)
+
+
+@pytest.mark.parametrize("seed", range(0, 6))
+def test_decode_16bit_wide_beams(hip, oracle, seed):
+    """K > 64: no shortlist (every read row is rescanned); the row pass still
+    gives the logsumexp and the flags."""
+    case = make_case(9500 + seed, big=True, dtypes=["bf16"], vocabs=[1000, 4104])
+    _check(hip, oracle, case)
+
+
+def _bf16_exact(values):
+    """float32 values that bfloat16 represents exactly (checked)."""
+    from tests.cases import to_bits
+
+    v = np.asarray(values, np.float32)
+    bits = to_bits(v, "bf16")
+    back = (bits.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(back.view(np.uint32), v.view(np.uint32)), "not exact in bfloat16"
+    return v
+
+
+@pytest.mark.parametrize("m", [1.0, 1.5, 2.0, 4.0, 0.98828125, 0.5, 7.5, 2.0 ** 20, 1.5 * 2.0 ** 99,
+                               (2.0 - 2.0 ** -7) * 2.0 ** 127])
+def test_logsumexp_table_edges(hip, oracle, m):
+    """Rows whose terms sit at the edges of the per-row bfloat16 term table:
+    magnitudes around 2^(E-25) (where fl(x - max) stops depending on x), +-0,
+    subnormals, terms at exp(-87) and just past it, -inf, and maxima at and
+    below 1 (the Cephes fallback)."""
+    rng = np.random.default_rng(int(abs(np.log2(m)) * 1000) + 7)
+    V = 4104
+    m = float(_bf16_exact([m])[0])
+    E = int(np.floor(np.log2(m)))
+    specials = []
+    for k in range(-28, -20):
+        t = 2.0 ** (E + k)
+        specials += [t, -t, t * 1.0078125, -t * 1.0078125, t * 0.9921875, -t * 0.9921875]
+    specials += [0.0, -0.0, 1e-40, -1e-40, 2.0 ** -133, -(2.0 ** -133), -np.inf]
+    for d in (86.0, 86.5, 87.0, 87.5, 88.0, 120.0, 127.0, 128.0, 130.0):
+        specials += [m - d]
+    specials = [s for s in specials if not (s > m)]
+    rows = []
+    for r in range(6):
+        base = rng.normal(0.0, 1.0, V).astype(np.float32) * np.float32(min(m, 3.0)) * 0.3
+        base = np.minimum(base, np.float32(m))
+        idx = rng.choice(V, size=len(specials) + 1, replace=False)
+        base[idx[:-1]] = np.asarray(specials, np.float32)
+        base[idx[-1]] = m
+        rows.append(base)
+    x = np.stack(rows).reshape(1, 3, 2, V).astype(np.float32)
+    from tests.cases import to_bits
+
+    xin = to_bits(x, "bf16")
+    kw = dict(from_logits=True, eos_token=3, min_length=2, alpha=1.0)
+    want = oracle.decode(xin, dtype="bf16", **kw)
+    got = hip.decode(xin, "bf16", **kw)
+    diff = first_difference(got, want)
+    assert diff is None, f"m={m}: {diff}"
+
+
+@pytest.mark.parametrize("V,dtype", [(151936, "bf16"), (128256, "bf16"), (155648, "bf16"), (155656, "bf16"),
+                                     (151936, "f16")])
+def test_decode_large_vocab_16bit(hip, oracle, V, dtype):
+    """Full-size vocabularies around the on-chip limit (155648 entries; one
+    more stripe falls back to the two-pass kernel)."""
+    rng = np.random.default_rng(V % 1000 + 11)
+    x = rng.normal(0.0, 3.0, size=(1, 3, 4, V)).astype(np.float32)
+    x += (-1.1 * np.log(rng.permutation(V) + 1.0)).astype(np.float32)
+    from tests.cases import to_bits
+
+    xin = to_bits(x, dtype)
+    kw = dict(from_logits=True, eos_token=V - 7, min_length=2, alpha=1.0)
+    want = oracle.decode(xin, dtype=dtype, **kw)
+    got = hip.decode(xin, dtype, **kw)
+    diff = first_difference(got, want)
+    assert diff is None, f"V={V} {dtype}: {diff}"
