@@ -12,10 +12,10 @@
 //
 //   * thread (seg, j) owns lane j of the stripes [seg*P, seg*P + P) of the row
 //     (stripe s = elements 256 s .. 256 s + 255), packed two stripes per VGPR;
-//   * each wavefront streams its 64 lanes in chunks of 8 stripes: one 16-byte
-//     global->LDS load per lane moves a chunk (1 KB) into a ring of LDS slots,
-//     kRing chunks in flight per wavefront, and the lanes read their own
-//     elements back transposed;
+//   * each wavefront loads its 64 lanes in chunks of 8 stripes, all in flight
+//     at once: one 16-byte buffer load per lane brings a chunk (1 KB) into the
+//     registers it will occupy; a pass through a 1 KB LDS slot (one write, two
+//     transposing reads) gives each lane its own elements of the chunk;
 //   * packed 16-bit integer max/min over the raw patterns give the row
 //     maximum, the NaN/+inf flag and per-register-group maxima;
 //   * from logits (bfloat16), exp(fl(x - max)) is a function of x's 16-bit
@@ -44,20 +44,12 @@ constexpr int kResRegs = 152;                    // packed element pairs per thr
 constexpr int kResChunks = kResRegs / 4;         // 8-stripe chunks per thread
 constexpr int kResGroups = 4;                    // register groups with their own maxima
 constexpr int kResGroupRegs = kResRegs / kResGroups;
-constexpr int kRing = 8;                         // 1 KB staging slots per wavefront
 constexpr int kLutHalf = 4096;                   // table slots per sign
 constexpr int kMaxStripes = 2 * 8 * kResChunks;  // 608 stripes: V <= 155648
 
-// LDS layout (bytes). The table sits at 0 so its reads use the immediate offset.
-constexpr int kOffLut = 0;
-constexpr int kOffRing = kOffLut + 2 * kLutHalf * 4;
-constexpr int kOffLaneMax = kOffRing + 8 * kRing * 1024;
-constexpr int kOffAcc = kOffLaneMax + 2 * 256 * 4;
-constexpr int kOffKey = kOffAcc + 256 * 4;
-constexpr int kOffX = kOffKey + kSurvivorCap * 8;
-constexpr int kOffWave = kOffX + kSurvivorCap * 4;
-constexpr int kOffMisc = kOffWave + 8 * 8;
-constexpr int kResLds = kOffMisc + 16;
+// LDS, as separate arrays.
+constexpr int kResLds = 2 * kLutHalf * 4 + 8 * 1024 + 256 * 4 + kSurvivorCap * 12 + 2 * 256 * 4 + 64 + 16;
+static_assert(kResLds <= 160 * 1024, "LDS of the resident row pass");
 
 typedef short v2i16 __attribute__((ext_vector_type(2)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
@@ -89,39 +81,58 @@ __device__ __forceinline__ uint32_t pk_shl2_u16(uint32_t a) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, a) << two);
 }
 
-// Waits until at most N vector-memory operations of the wavefront are
-// outstanding (the global->LDS loads complete in issue order) / until its
-// LDS reads have returned. The memory clobber keeps the compiler from moving
-// LDS accesses across the wait.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+// Buffer view of one row (bytes [0, nbytes)): loads past its end return
+// zeros instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const uint16_t* row, int nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(row), 0, nbytes, 0x00020000);
 }
-__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-__device__ __forceinline__ void load_chunk_lds(const uint16_t* src, unsigned char* dst) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dst), 16, 0, 0);
+typedef unsigned int v2u32 __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u32 __attribute__((ext_vector_type(4)));
+
+// Workgroup barrier for LDS data only: the wavefront's LDS operations have
+// completed; its global loads may still be in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Transposes one chunk: lane L holds 16 bytes = lanes 8 (L % 8) .. + 7 of
+// stripe L / 8; it gets back its own lane L of the 8 stripes, packed two
+// stripes per register (lower stripe in the low half). The chunk goes through
+// the wavefront's 1 KB slot, (stripe i, lane L) at byte 128 i + 2 L, read back
+// with two transposing reads: within each 16-lane group, lane i receives
+// element i % 4 of the 8 bytes addressed by lanes 4 k + i / 4 (k = 0..3), so
+// lane L = 16 G + a addresses (stripe 4 h + a / 4, lanes 16 G + 4 (a % 4) ..).
+// The write, the reads and their wait are one asm block (the LDS serves a
+// wavefront's operations in order).
+__device__ __forceinline__ void transpose_chunk(unsigned char* slot, int L, uint32_t x0, uint32_t x1, uint32_t x2,
+                                                uint32_t x3, uint32_t (&R)[4]) {
+    const int G = L >> 4, a = L & 15;
+    const uint32_t base = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)slot));
+    const uint32_t waddr = base + 16 * L;
+    const uint32_t raddr = base + 128 * (a >> 2) + 32 * G + 8 * (a & 3);
+    const v4u32 w = {x0, x1, x2, x3};
+    v2u32 t0, t1;
+    asm volatile(
+        "ds_write_b128 %2, %3\n\t"
+        "ds_read_b64_tr_b16 %0, %4\n\t"
+        "ds_read_b64_tr_b16 %1, %4 offset:512\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(t0), "=&v"(t1)
+        : "v"(waddr), "v"(w), "v"(raddr)
+        : "memory");
+    R[0] = t0.x;
+    R[1] = t0.y;
+    R[2] = t1.x;
+    R[3] = t1.y;
 }
 
 template <int DT>
 __device__ __forceinline__ float pattern_value(uint32_t h) {
     return DT == 1 ? half_to_f32(static_cast<uint16_t>(h)) : bf16_to_f32(static_cast<uint16_t>(h));
-}
-
-// Largest value of a register group from its packed signed maxima and minima:
-// per half, the largest non-negative pattern, else (all negative) the
-// smallest magnitude, which is the smallest signed pattern.
-template <int DT>
-__device__ __forceinline__ float group_value(uint32_t gmax, uint32_t gmin) {
-    float best = -kInf;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int16_t smax = static_cast<int16_t>(gmax >> (16 * h));
-        const int16_t smin = static_cast<int16_t>(gmin >> (16 * h));
-        const uint32_t pat = static_cast<uint16_t>(smax >= 0 ? smax : smin);
-        best = fmaxf(best, pattern_value<DT>(pat));
-    }
-    return best;
 }
 
 // Signed 16-bit key of a sign-magnitude pattern, monotone in its value (-0
@@ -149,18 +160,59 @@ __device__ __forceinline__ bool table_fits(float m, int& ulo) {
     return !(d >= -87.0f);
 }
 
+// Inverse of key16.
+__device__ __forceinline__ uint32_t key_pattern(int key) {
+    return static_cast<uint16_t>(key < 0 ? (key ^ 0x7fff) : key);
+}
+
+// Over 256 bins taken in descending order, the bin holding the target-th
+// largest count-weighted key (1-based; the bins hold at least target keys),
+// and how many keys lie in the bins above it. One wavefront, every lane gets
+// the answer.
+__device__ __forceinline__ void hist_select(const int* hist, int target, int lane, int& bin, int& above) {
+    const int4 h = *reinterpret_cast<const int4*>(hist + 252 - 4 * lane);  // bins 252-4l .. 255-4l
+    const int c0 = h.w, c1 = h.z, c2 = h.y, c3 = h.x;                     // descending
+    const int sum = c0 + c1 + c2 + c3;
+    int incl = sum;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off);
+        if (lane >= off) incl += t;
+    }
+    const int excl = incl - sum;
+    const uint64_t mine = __ballot(excl < target && target <= incl);
+    const int src = __ffsll(static_cast<long long>(mine)) - 1;
+    int b = 255 - 4 * lane, a = excl;
+    if (a + c0 < target) {
+        a += c0;
+        --b;
+        if (a + c1 < target) {
+            a += c1;
+            --b;
+            if (a + c2 < target) {
+                a += c2;
+                --b;
+            }
+        }
+    }
+    bin = __shfl(b, src);
+    above = __shfl(a, src);
+}
+
 template <int DT, bool LOGITS>
 __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams p, int64_t rows) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    float* lut = reinterpret_cast<float*>(lds + kOffLut);
-    float* s_lane_max = reinterpret_cast<float*>(lds + kOffLaneMax);
-    float* s_acc = reinterpret_cast<float*>(lds + kOffAcc);
-    uint64_t* s_key = reinterpret_cast<uint64_t*>(lds + kOffKey);
-    float* s_x = reinterpret_cast<float*>(lds + kOffX);
-    float* s_wmax = reinterpret_cast<float*>(lds + kOffWave);
-    int* s_wbad = reinterpret_cast<int*>(lds + kOffWave + 32);
-    int* s_count = reinterpret_cast<int*>(lds + kOffMisc);
-    float* s_theta = reinterpret_cast<float*>(lds + kOffMisc + 4);
+    __shared__ __attribute__((aligned(16))) float lut[2 * kLutHalf];
+    __shared__ __attribute__((aligned(16))) unsigned char s_stage[8 * 1024];
+    __shared__ float s_acc[256];
+    __shared__ uint64_t s_key[kSurvivorCap];
+    __shared__ float s_x[kSurvivorCap];
+    __shared__ __attribute__((aligned(16))) int s_hist[2 * 256];
+    __shared__ int s_wave[16];
+    __shared__ int s_count_arr[1];
+    int* s_hist1 = s_hist;
+    int* s_hist2 = s_hist + 256;
+    int* s_wkey = s_wave;
+    int* s_wbad = s_wave + 8;
+    int* s_count = s_count_arr;
 
     const int tid = static_cast<int>(threadIdx.x);
     const int j = tid & 255, l = tid & 63;
@@ -177,14 +229,70 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
     constexpr uint32_t kPad = DT == 2 ? 0xff80u : 0xfc00u;    // -inf
     constexpr int kPosInf = DT == 2 ? 0x7f80 : 0x7c00;
     constexpr uint32_t kNegInf = kPad;
-    unsigned char* ring = lds + kOffRing + wave * (kRing * 1024);
+    unsigned char* stage = s_stage + wave * 1024;
 
     if (tid == 0) *s_count = 0;
+    if (tid < 256) {
+        s_hist1[tid] = 0;
+        s_hist2[tid] = 0;
+    }
     __syncthreads();
 
-    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
-        int b, new_len;
-        if (!row_is_read(p, r, b, new_len)) continue;
+    // Wavefront 0 finishes row r (lane tree, shortlist, RowInfo) after it has
+    // queued the first loads of the next row, so the loads cover it.
+    bool pend = false;
+    int64_t pend_r = 0;
+    float pend_m = 0.0f, pend_theta = 0.0f;
+    bool pend_bad = false, pend_lse = false, pend_mask = false, pend_full = false;
+    int pend_b = 0;
+    auto finish_pending = [&]() {
+        float lse = 0.0f;
+        if (LOGITS) {
+            if (pend_lse) {
+                float a[4];
+#pragma unroll
+                for (int e2 = 0; e2 < 4; ++e2) a[e2] = s_acc[4 * l + e2];
+                lse = logsumexp_from(pend_m, lane_tree_sum(a, l));
+            } else {
+                lse = -kInf;
+            }
+        }
+        const int n = pend_full ? kSurvivorCap + 1 : *s_count;
+        finish_row_wave<LOGITS, true>(p, pend_r, lse, pend_theta, pend_bad, s_key, s_x, n, l, pend_b, pend_mask);
+        wave_sync();
+        if (l == 0) *s_count = 0;
+        pend = false;
+    };
+
+    // (the row index and what derives from it are the same in every lane:
+    // readfirstlane lets the compiler keep them, and the row's buffer view,
+    // in scalar registers)
+    auto next_read_row = [&](int64_t rr, int& b_out, int& len_out) -> int64_t {
+        while (rr < rows && !row_is_read(p, rr, b_out, len_out)) rr += gridDim.x;
+        b_out = __builtin_amdgcn_readfirstlane(b_out);
+        len_out = __builtin_amdgcn_readfirstlane(len_out);
+        const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(rr));
+        const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(rr) >> 32));
+        return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+    };
+    // byte offset in the segment of this lane's 16 bytes of chunk 0 (stripe
+    // l/8 of the segment, lanes 64 wv + 8 (l % 8) ..); chunk c adds the
+    // scalar 4096 c
+    auto lane_offset = [&]() -> int {
+        int lr = l;
+        asm volatile("" : "+v"(lr));
+        return 2 * (256 * (lr >> 3) + 64 * wv + 8 * (lr & 7));
+    };
+
+    // Workgroups start a quarter of a row's time apart (blockIdx mod 4), so
+    // the CUs' load phases interleave instead of all hitting memory at once.
+    for (int z = 0; z < 2 * static_cast<int>(blockIdx.x & 3); ++z) __builtin_amdgcn_s_sleep(127);
+
+    int b = 0, new_len = 0;
+    int64_t r = next_read_row(blockIdx.x, b, new_len);
+    while (r < rows) {
+        int bn = 0, lenn = 0;
+        const int64_t rn = next_read_row(r + gridDim.x, bn, lenn);
         const bool mask_eos = new_len < p.min_length;
         const uint16_t* row = static_cast<const uint16_t*>(p.x) + r * V;
         // Opaque copies per row: everything the unrolled load derives from
@@ -194,12 +302,10 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
         asm volatile("" : "+s"(nch_r), "+s"(V_r));
         asm volatile("" : "+v"(jr), "+v"(lr));
 
-        // ---- load: ring of 1 KB chunks per wavefront, transposed to lanes ----
+        // ---- load the row's segment into registers, transposed to lanes ----
         // registers past the segment's chunks hold -inf pairs (term 0, never
         // a survivor), so the chain below runs over all of them unguarded
         uint32_t reg[kResRegs];
-#pragma unroll
-        for (int k = 0; k < kResRegs; ++k) reg[k] = kPad | (kPad << 16);
         uint32_t gmax[kResGroups], gmin[kResGroups];
         uint32_t umax = 0;
 #pragma unroll
@@ -207,81 +313,101 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             gmax[g] = 0x80008000u;
             gmin[g] = kPad | (kPad << 16);
         }
-        // lane l of the wavefront moves 8 elements: stripe 8c + l/8 of the
-        // segment, lanes 64 wv + 8 (l % 8) ...; a group past the row end
-        // reads the row start instead (V % 8 == 0: groups are whole) and is
-        // replaced by padding below.
-        const int v_lane = 256 * (s_begin + (lr >> 3)) + 64 * wv + 8 * (lr & 7);
-        auto chunk_src = [&](int c) -> const uint16_t* {
-            const int v = v_lane + 2048 * c;
-            return row + (v < V_r ? v : 0);
-        };
+        // Chunk c (8 stripes x this wavefront's 64 lanes): lane l loads the 16
+        // bytes of stripe 8c + l/8, lanes 64 wv + 8 (l % 8) .. into the four
+        // registers the chunk will occupy. Every chunk is in flight at once;
+        // the buffer view covers exactly the segment's stripes inside the
+        // row, so groups past it read zeros without touching memory, and are
+        // replaced by padding. Consuming a chunk writes its 1 KB to the
+        // wavefront's staging slot and reads it back transposed, each lane its
+        // own lane's 8 stripes.
+        const int seg_bytes = max(0, 2 * min(V_r, 256 * (s_begin + per)) - 512 * s_begin);
+        const __amdgpu_buffer_rsrc_t rs = row_buffer(row + 256 * s_begin, seg_bytes);
+        const int voff = lane_offset();
 #pragma unroll
-        for (int c = 0; c < kRing; ++c)
-            if (c < nch_r) load_chunk_lds(chunk_src(c), ring + c * 1024);
+        for (int c = 0; c < kResChunks; ++c) {
+            const v4u32 q = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 4096 * c, 0);
+            reg[4 * c] = q.x;
+            reg[4 * c + 1] = q.y;
+            reg[4 * c + 2] = q.z;
+            reg[4 * c + 3] = q.w;
+        }
+        if (wave == 0 && pend) finish_pending();
 #pragma unroll
         for (int c = 0; c < kResChunks; ++c) {
             if (c < nch_r) {
-                if (c + kRing < nch_r) wait_vm<kRing - 1>();
-                else wait_vm<0>();
-                const unsigned char* slot = ring + (c % kRing) * 1024;
-                uint32_t e[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) e[i] = *reinterpret_cast<const uint16_t*>(slot + 128 * i + 2 * lr);
+                uint32_t R4[4];
+                transpose_chunk(stage, lr, reg[4 * c], reg[4 * c + 1], reg[4 * c + 2], reg[4 * c + 3], R4);
                 const int sb = s_begin + 8 * c;
                 if (256 * (sb + 8) > V_r) {
 #pragma unroll
-                    for (int i = 0; i < 8; ++i)
-                        if (256 * (sb + i) + jr >= V_r) e[i] = kPad;
+                    for (int q = 0; q < 4; ++q) {
+                        const bool lo_out = 256 * (sb + 2 * q) + jr >= V_r;
+                        const bool hi_out = 256 * (sb + 2 * q + 1) + jr >= V_r;
+                        R4[q] = (lo_out ? kPad : (R4[q] & 0xffffu)) | (hi_out ? (kPad << 16) : (R4[q] & 0xffff0000u));
+                    }
                 }
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int k = 4 * c + q;
-                    const uint32_t R = e[2 * q] | (e[2 * q + 1] << 16);
+                    const uint32_t R = R4[q];
                     reg[k] = R;
                     const int g = k / kResGroupRegs;
                     gmax[g] = pk_max_i16(gmax[g], R);
                     gmin[g] = pk_min_i16(gmin[g], R);
                     umax = pk_max_u16(umax, R);
                 }
-                wait_lds();
-                if (c + kRing < nch_r) load_chunk_lds(chunk_src(c + kRing), ring + (c % kRing) * 1024);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) reg[4 * c + q] = kPad | (kPad << 16);
             }
         }
 
-        // ---- row maximum, flag, lane maxima ----
-        float gval[kResGroups];
-        float tmax = -kInf;
+        // ---- row maximum, flag, group keys; the key histogram for theta ----
+        // (keys: key16 of the largest pattern of a group, per half the largest
+        // non-negative pattern, else the smallest signed one)
+        int gkey[kResGroups];
+        int tkey = -32768;
         uint32_t allmax = 0x80008000u;
 #pragma unroll
         for (int g = 0; g < kResGroups; ++g) {
-            gval[g] = group_value<DT>(gmax[g], gmin[g]);
-            tmax = fmaxf(tmax, gval[g]);
+            int best = -32768;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int16_t smax = static_cast<int16_t>(gmax[g] >> (16 * h));
+                const int16_t smin = static_cast<int16_t>(gmin[g] >> (16 * h));
+                const int kk = key16(static_cast<uint16_t>(smax >= 0 ? smax : smin));
+                best = max(best, kk);
+            }
+            gkey[g] = best;
+            tkey = max(tkey, best);
             allmax = pk_max_i16(allmax, gmax[g]);
         }
         const bool bad = static_cast<int16_t>(allmax & 0xffffu) >= kPosInf ||
                          static_cast<int16_t>(allmax >> 16) >= kPosInf || (umax & 0xffffu) > kNegInf ||
                          (umax >> 16) > kNegInf;
-        s_lane_max[seg * 256 + j] = tmax;
-        const float wmax = wave_max(tmax);
+        if (M > 0) atomicAdd(&s_hist1[(tkey + 32768) >> 8], 1);
+        int wkey = tkey;
+        for (int off = 32; off > 0; off >>= 1) wkey = max(wkey, __shfl_xor(wkey, off));
         const bool wbad = __any(bad);
         if (l == 0) {
-            s_wmax[wave] = wmax;
+            s_wkey[wave] = wkey;
             s_wbad[wave] = wbad ? 1 : 0;
         }
-        __syncthreads();
+        lds_barrier();
 
-        float m = -kInf;
+        int mkey = -32768;
         bool any_bad = false;
 #pragma unroll
         for (int w = 0; w < kResThreads / 64; ++w) {
-            m = fmaxf(m, s_wmax[w]);
+            mkey = max(mkey, s_wkey[w]);
             any_bad = any_bad || s_wbad[w] != 0;
         }
+        float m = pattern_value<DT>(key_pattern(mkey));
         if (any_bad) {
-            // NaN or +inf in the row: the maxima are over x < +inf (reference
-            // src/kernels_scalar.cpp:48-56), so re-read the segment for them;
-            // every group is scanned for survivors.
+            // NaN or +inf in the row: the maximum is over x < +inf (reference
+            // src/kernels_scalar.cpp:48-56), so re-read the segment for it.
+            // No shortlist is kept for such a row.
             float lm = -kInf;
             for (int s = s_begin; s < s_begin + 8 * nch; s += 8) {
                 float xs[8];
@@ -294,23 +420,22 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
                 for (int u = 0; u < 8; ++u)
                     if (xs[u] < kInf && xs[u] > lm) lm = xs[u];
             }
-            __syncthreads();  // every read of the wavefront maxima above is done
-            s_lane_max[seg * 256 + j] = lm;
+            lds_barrier();  // every read of the wavefront keys above is done
             const float wm = wave_max(lm);
-            if (l == 0) s_wmax[wave] = wm;
-            __syncthreads();
+            if (l == 0) s_wkey[wave] = static_cast<int>(f32_bits(wm));
+            lds_barrier();
             m = -kInf;
 #pragma unroll
-            for (int w = 0; w < kResThreads / 64; ++w) m = fmaxf(m, s_wmax[w]);
-#pragma unroll
-            for (int g = 0; g < kResGroups; ++g) gval[g] = kInf;
+            for (int w = 0; w < kResThreads / 64; ++w) m = fmaxf(m, bits_f32(static_cast<uint32_t>(s_wkey[w])));
         }
-        if (M > 0 && wave == 0) {
-            float a[4];
-#pragma unroll
-            for (int e2 = 0; e2 < 4; ++e2) a[e2] = fmaxf(s_lane_max[4 * l + e2], s_lane_max[256 + 4 * l + e2]);
-            const float th = shortlist_threshold(a, l, M);
-            if (l == 0) *s_theta = th;
+
+        // theta: the M-th largest of the 512 thread maxima (at least M
+        // elements are >= it), radix-selected on the 16-bit keys
+        const bool select = M > 0 && !any_bad;
+        int b1 = 0, above1 = 0;
+        if (select) {
+            hist_select(s_hist1, M, l, b1, above1);
+            if (((tkey + 32768) >> 8) == b1) atomicAdd(&s_hist2[(tkey + 32768) & 255], 1);
         }
         int ulo = 0;
         const bool do_lse = LOGITS && m > -kInf;
@@ -331,21 +456,28 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
                 lut[s] = term;
             }
         }
-        __syncthreads();
-        const float theta = M > 0 ? *s_theta : kInf;
+        lds_barrier();
+        int tk = -32768;  // key(theta)
+        if (select) {
+            int b2 = 0, above2 = 0;
+            hist_select(s_hist2, M - above1, l, b2, above2);
+            tk = ((b1 << 8) | b2) - 32768;
+        }
+        if (tid < 256) s_hist1[tid] = 0;  // every wavefront has its b1
+        const float theta = M > 0 ? (select ? pattern_value<DT>(key_pattern(tk)) : -kInf) : kInf;
+        const bool full = M > 0 && !(theta > -kInf);  // no shortlist: every element would survive
 
         // ---- registers holding x >= theta (groups whose maximum reaches it) ----
         // A packed key test marks them (a superset: keys >= key(theta) - 1, so
         // -0 and +0 both pass); their elements are re-read from the row, which
         // is still in cache, while the other segment folds its lanes.
         uint32_t hm[(kResRegs + 31) / 32] = {};
-        if (M > 0) {
-            int tk = key16(value_pattern<DT>(theta)) - 1;
-            if (tk < -32768) tk = -32768;
-            const uint32_t tk2 = static_cast<uint32_t>(static_cast<uint16_t>(tk)) * 0x10001u;
+        if (M > 0 && !full) {
+            const int tk1 = tk > -32768 ? tk - 1 : tk;
+            const uint32_t tk2 = static_cast<uint32_t>(static_cast<uint16_t>(tk1)) * 0x10001u;
 #pragma unroll
             for (int g = 0; g < kResGroups; ++g) {
-                if (gval[g] >= theta) {
+                if (gkey[g] >= tk1) {
 #pragma unroll
                     for (int q = 0; q < kResGroupRegs; ++q) {
                         const int k = g * kResGroupRegs + q;
@@ -387,7 +519,7 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
         // same two barriers.
         if (seg == 1) {
             push_hits();
-            __syncthreads();
+            lds_barrier();
         }
         if (do_lse) {
             float acc = seg == 0 ? 0.0f : s_acc[j];
@@ -402,8 +534,8 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
                     idx = pk_min_u16(idx, 0x0fff0fffu);
                     idx |= (R >> 3) & 0x10001000u;
                     const uint32_t addr = pk_shl2_u16(idx);
-                    lo = *reinterpret_cast<const float*>(lds + kOffLut + (addr & 0xffffu));
-                    hi = *reinterpret_cast<const float*>(lds + kOffLut + (addr >> 16));
+                    lo = lut[(addr & 0xffffu) >> 2];
+                    hi = lut[addr >> 18];
                 };
                 // blocks of kBlk registers; the lookups of block b + 1 are in
                 // flight while block b is added in order
@@ -441,46 +573,37 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             s_acc[j] = acc;
         }
         if (seg == 0) {
-            __syncthreads();
+            lds_barrier();
+            s_hist2[tid] = 0;  // every wavefront has read its b2
             push_hits();
         }
-        __syncthreads();
+        lds_barrier();
 
-        // ---- finish: lane tree, shortlist, RowInfo ----
         if (wave == 0) {
-            float lse = 0.0f;
-            if (LOGITS) {
-                if (do_lse) {
-                    float a[4];
-#pragma unroll
-                    for (int e2 = 0; e2 < 4; ++e2) a[e2] = s_acc[4 * l + e2];
-                    lse = logsumexp_from(m, lane_tree_sum(a, l));
-                } else {
-                    lse = -kInf;
-                }
-            }
-            const int n = *s_count;
-            finish_row_wave<LOGITS, true>(p, r, lse, theta, any_bad, s_key, s_x, n, l, b, mask_eos);
-            wave_sync();
-            if (l == 0) *s_count = 0;
+            pend = true;
+            pend_r = r;
+            pend_m = m;
+            pend_theta = theta;
+            pend_bad = any_bad;
+            pend_lse = do_lse;
+            pend_mask = mask_eos;
+            pend_full = full;
+            pend_b = b;
         }
+        r = rn;
+        b = bn;
+        new_len = lenn;
     }
+    if (wave == 0 && pend) finish_pending();
 }
 
 int g_cu_count[64];
 
 template <int DT, bool LOGITS>
 hipError_t launch_resident(const DecodeParams& p, int64_t rows, int device, hipStream_t stream) {
-    static bool attr_set[64] = {};
-    if (!attr_set[device]) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&row_resident_kernel<DT, LOGITS>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kResLds);
-        if (e != hipSuccess) return e;
-        attr_set[device] = true;
-    }
     const int64_t grid = rows < g_cu_count[device] ? rows : g_cu_count[device];
-    hipLaunchKernelGGL((row_resident_kernel<DT, LOGITS>), dim3(static_cast<unsigned>(grid)), dim3(kResThreads),
-                       kResLds, stream, p, rows);
+    hipLaunchKernelGGL((row_resident_kernel<DT, LOGITS>), dim3(static_cast<unsigned>(grid)), dim3(kResThreads), 0,
+                       stream, p, rows);
     return hipGetLastError();
 }
 
