@@ -284,10 +284,6 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
         return 2 * (256 * (lr >> 3) + 64 * wv + 8 * (lr & 7));
     };
 
-    // Workgroups start a quarter of a row's time apart (blockIdx mod 4), so
-    // the CUs' load phases interleave instead of all hitting memory at once.
-    for (int z = 0; z < 2 * static_cast<int>(blockIdx.x & 3); ++z) __builtin_amdgcn_s_sleep(127);
-
     int b = 0, new_len = 0;
     int64_t r = next_read_row(blockIdx.x, b, new_len);
     while (r < rows) {

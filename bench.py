@@ -2,7 +2,7 @@
 """Benchmark of the beam-search hot path on one MI355X.
 
 A step is one pass of the hot path over one batch of synthetic input already
-resident in HBM: for the headline workload that is
+resident in HBM: for the headline workload (config C2) that is
 ``beamgrad_amd.decode(logits, from_logits=True)`` (final scores + trace) and
 ``backtrack`` on bf16 logits [B=32, T=64, K=8, V=151936] with EOS 151643,
 length penalty 1.0 and min_length 4. ``value`` is candidate elements per

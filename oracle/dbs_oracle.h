@@ -5,8 +5,24 @@
  * __graft_entry__.smoke() and by bench.py's cpu_baseline leg. Nothing in the
  * product (beamgrad_amd/) links, loads or calls it.
  *
- * Every function names the reference file:line it restates. Parity status of
- * each function is listed in oracle/README.md.
+ * Every function names the reference file:line it restates. How each is
+ * pinned (tests/test_oracle.py; "_ref" = the reference's own CPU library built
+ * from its sources by oracle/Makefile):
+ *   orc_f16_to_f32, orc_bf16_to_f32  all 65536 patterns vs the closed form
+ *   orc_log_ge1, orc_exp_ge0         vs math.log / math.exp (series error)
+ *   orc_length_penalty               <= 1 ulp of pow, integer-alpha squaring,
+ *                                    saturation; _ref decodes
+ *   orc_exp_nonpositive              vs math.exp; _ref from-logits decodes
+ *   orc_row_stats                    vs a float64 logsumexp; _ref row_lse bits
+ *   orc_softmax_probability          _ref logits backward bits; finite differences
+ *   orc_decode                       _ref bits on random cases (ties, -inf,
+ *                                    NaN flags, EOS, n-gram, banned), committed
+ *                                    golden fixtures, known answers, exhaustive
+ *                                    beams, greedy K = 1
+ *   orc_backward                     _ref bits, golden fixtures, finite differences
+ *   orc_path_gradient                draws scattered == _ref dense gradient
+ *   orc_backtrack                    the reference's path property test
+ * No function is left unpinned.
  */
 #ifndef DBS_ORACLE_H
 #define DBS_ORACLE_H

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from oracle.oracle import Oracle, Reference, reference_available
-from tests.cases import first_difference, load_golden, make_case
+from tests.cases import first_difference, load_golden, log_softmax, make_case
 
 KEYS = ("final_scores", "final_raw_scores", "final_lengths", "tokens", "parents", "lengths", "scores",
         "raw_scores", "from_logprob", "row_lse")
@@ -292,3 +292,61 @@ def test_single_beam_is_greedy(oracle):
     out = oracle.decode(x)
     assert out["tokens"][0, :, 0].tolist() == [int(np.argmax(x[0, t, 0])) for t in range(6)]
     assert out["tokens"][0, 2, 0] == 3
+
+
+# ---------------------------------------------------------------------------
+# path gradient and backtrack, pinned by the reference library and by the
+# reference's own property test
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("seed", range(0, 20))
+def test_path_gradient_scatters_to_reference_dense_backward(oracle, seed):
+    """The per-slot draws, scattered to (t, parent, token) of the slots that
+    took a log-prob, are the reference library's dense final-scores gradient
+    (at a step the log-prob slots have distinct (parent, token) pairs)."""
+    if not reference_available():
+        pytest.skip("reference library not built")
+    case = make_case(2300 + seed, allow_invalid=False)
+    kw = dict(case["kw"])
+    kw.pop("banned_per_example")
+    tr = oracle.decode(case["xin"], dtype=case["dtype"], **kw)
+    B, T, K = tr["parents"].shape
+    V = case["V"]
+    gf = np.random.default_rng(seed).normal(size=(B, K)).astype(np.float32)
+    draws = oracle.path_gradient(tr, V, gf, alpha=kw["alpha"], steps=kw["steps"])
+    dense = np.zeros((B, T, K, V), np.float32)
+    b_i, t_i, k_i = np.nonzero(draws)
+    assert np.all(tr["from_logprob"][b_i, t_i, k_i] == 1)
+    dense[b_i, t_i, tr["parents"][b_i, t_i, k_i], tr["tokens"][b_i, t_i, k_i]] += draws[b_i, t_i, k_i]
+    want = Reference().backward(tr, V, alpha=kw["alpha"], steps=kw["steps"], grad_final=gf)
+    assert np.array_equal(dense.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("seed", range(0, 10))
+def test_backtracked_paths_reproduce_raw_scores(oracle, seed):
+    """Restates the reference's python/tests/test_api.py:118-133 on the
+    oracle: following parents back from each final beam gives the tokens of
+    the backtracked sequence, the log-probs taken on the way sum to the final
+    raw score, and every path starts from beam 0; steps past an example's
+    length hold -1 (python/beamgrad/_torch.py:582-606)."""
+    rng = np.random.default_rng(4100 + seed)
+    B, T, K, V = 3, 6, 4, 13
+    x = log_softmax(rng.normal(size=(B, T, K, V)).astype(np.float32))
+    steps = [6, 4, 1] if seed % 2 else None
+    out = oracle.decode(x, eos_token=3, alpha=0.5, steps=steps)
+    paths = oracle.backtrack(out["tokens"], out["parents"], steps)
+    for b in range(B):
+        n = T if steps is None else steps[b]
+        for k in range(K):
+            total, beam = 0.0, k
+            for t in range(T - 1, -1, -1):
+                if t >= n:
+                    assert paths[b, k, t] == -1
+                    continue
+                if out["from_logprob"][b, t, beam]:
+                    total += float(x[b, t, out["parents"][b, t, beam], out["tokens"][b, t, beam]])
+                assert paths[b, k, t] == out["tokens"][b, t, beam]
+                beam = int(out["parents"][b, t, beam])
+            assert abs(total - float(out["final_raw_scores"][b, k])) <= 1e-5 * max(1.0, abs(total))
+            assert beam == 0
