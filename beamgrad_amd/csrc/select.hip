@@ -106,7 +106,7 @@ __device__ __forceinline__ bool make_cand(const DecodeParams& p, const Lds& s, c
     return true;
 }
 
-__device__ void sort_cands(Cand* buf, int np) {
+__device__ __forceinline__ void sort_cands(Cand* buf, int np) {
     const int tid = static_cast<int>(threadIdx.x);
     for (int kk = 2; kk <= np; kk <<= 1) {
         for (int j = kk >> 1; j > 0; j >>= 1) {
@@ -128,7 +128,7 @@ __device__ void sort_cands(Cand* buf, int np) {
 
 // Sorts the collected candidates, keeps the best K, and raises the admission
 // threshold to the K-th kept one when that is better.
-__device__ void compact(Lds& s, State& st, int K) {
+__device__ __forceinline__ void compact(Lds& s, State& st, int K) {
     __syncthreads();
     const int n = st.count;
     int np = 1;
@@ -162,7 +162,7 @@ __device__ __forceinline__ void end_round(Lds& s, State& st, int K, int sort_cap
 // collector. A buffer overflow (a row with very many candidates at the
 // threshold) falls back to offering round by round.
 template <int DT, bool LOGITS>
-__device__ void rescan_row(const DecodeParams& p, Lds& s, State& st, int b, int k, int64_t row, float lse,
+__device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State& st, int b, int k, int64_t row, float lse,
                            float praw, float inv_pen, int new_len, const PrefixView& pre, int sort_cap) {
     const bool mask_eos = new_len < p.min_length;
     const int V = p.V;
