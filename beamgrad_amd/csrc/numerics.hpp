@@ -150,13 +150,15 @@ struct Cand {
     int32_t flp;
 };
 
+// Branch-free: each level is "strictly before, or equal and the next level
+// decides", with non-short-circuit operators so the device code stays
+// straight-line.
 DBS_HD bool before(const Cand& a, const Cand& b) {
-    if (a.score != b.score) return a.score > b.score;
-    if (a.raw != b.raw) return a.raw > b.raw;
-    if (a.parent != b.parent) return a.parent < b.parent;
-    if (a.token != b.token) return a.token < b.token;
-    if (a.length != b.length) return a.length < b.length;
-    return a.flp > b.flp;
+    const bool by_length = (a.length < b.length) | ((a.length == b.length) & (a.flp > b.flp));
+    const bool by_token = (a.token < b.token) | ((a.token == b.token) & by_length);
+    const bool by_parent = (a.parent < b.parent) | ((a.parent == b.parent) & by_token);
+    const bool by_raw = (a.raw > b.raw) | ((a.raw == b.raw) & by_parent);
+    return (a.score > b.score) | ((a.score == b.score) & by_raw);
 }
 
 DBS_HD Cand dead_cand() { return Cand{-kInf, -kInf, -1, -1, 0, 0}; }

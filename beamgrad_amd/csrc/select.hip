@@ -27,6 +27,8 @@ constexpr int kRescanPerThread = 16;
 struct Lds {
     Cand* buf;        // [sort_cap] the collector
     Cand* rbuf;       // [kRescanBuf] one rescanned row's candidates
+    uint4* key;       // [2 * kRankMax] candidate keys of a rank compaction
+    int32_t* part;    // [kSelectThreads] partial ranks
     float* raw;       // [K] beams after the previous step
     float* nraw;      // [K] beams after this step (also scratch)
     float* rbound;    // [K]
@@ -126,11 +128,110 @@ __device__ __forceinline__ void sort_cands(Cand* buf, int np) {
     }
 }
 
+// Collector sizes up to this are compacted by a parallel rank (larger ones by
+// the bitonic sort).
+constexpr int kRankMax = kSelectThreads;
+
+// Order-preserving unsigned image of a float (-0 and +0 map together, as they
+// compare equal; no NaN reaches the collector).
+__device__ __forceinline__ uint32_t order_bits(float f) {
+    const uint32_t u = __float_as_uint(f) & (f == 0.0f ? 0u : 0xffffffffu);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// The candidate at collector index idx as a 224-bit integer that is larger
+// exactly when the candidate comes earlier in the total order, least
+// significant word first: index (lower first; it decides only between
+// candidates that compare equal, i.e. dead sentinels), flp (desc), length,
+// token, parent (asc as signed integers), raw, score (desc).
+__device__ __forceinline__ void store_key(uint4* dst, const Cand& c, int idx) {
+    dst[0] = make_uint4(0xffffffffu - static_cast<uint32_t>(idx), static_cast<uint32_t>(c.flp) ^ 0x80000000u,
+                        0x7fffffffu - static_cast<uint32_t>(c.length), 0x7fffffffu - static_cast<uint32_t>(c.token));
+    dst[1] = make_uint4(0x7fffffffu - static_cast<uint32_t>(c.parent), order_bits(c.raw), order_bits(c.score), 0u);
+}
+
+// rank += (key j > key i): the borrow out of key i - key j, kept in VCC
+// through the whole subtraction.
+__device__ __forceinline__ void count_before(int& rank, const uint4& ilo, const uint4& ihi, const uint4& jlo,
+                                             const uint4& jhi) {
+    uint32_t t;
+    asm("v_sub_co_u32 %0, vcc, %2, %9\n\t"
+        "v_subb_co_u32 %0, vcc, %3, %10, vcc\n\t"
+        "v_subb_co_u32 %0, vcc, %4, %11, vcc\n\t"
+        "v_subb_co_u32 %0, vcc, %5, %12, vcc\n\t"
+        "v_subb_co_u32 %0, vcc, %6, %13, vcc\n\t"
+        "v_subb_co_u32 %0, vcc, %7, %14, vcc\n\t"
+        "v_subb_co_u32 %0, vcc, %8, %15, vcc\n\t"
+        "v_addc_co_u32 %1, vcc, 0, %1, vcc"
+        : "=&v"(t), "+v"(rank)
+        : "v"(ilo.x), "v"(ilo.y), "v"(ilo.z), "v"(ilo.w), "v"(ihi.x), "v"(ihi.y), "v"(ihi.z), "v"(jlo.x),
+          "v"(jlo.y), "v"(jlo.z), "v"(jlo.w), "v"(jhi.x), "v"(jhi.y), "v"(jhi.z)
+        : "vcc");
+}
+
+// Keeps the best K of n <= kRankMax collected candidates, in order: every
+// candidate's rank is the number of keys above its own, counted by up to four
+// waves per candidate over disjoint ranges of the others, and the candidates
+// of rank < K move to their rank.
+__device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n) {
+    const int tid = static_cast<int>(threadIdx.x);
+    const int n4 = (n + 3) & ~3;
+    Cand c = dead_cand();
+    if (tid < n4) {
+        if (tid < n) {
+            c = s.buf[tid];
+            store_key(s.key + 2 * tid, c, tid);
+        } else {
+            s.key[2 * tid] = make_uint4(0u, 0u, 0u, 0u);  // below every key
+            s.key[2 * tid + 1] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    __syncthreads();
+    // wave w counts for candidates 64 gi + lane over the gj-th part of the others
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int groups = (n + 63) >> 6;
+    const int parts = groups == 1 ? 4 : (groups == 2 ? 2 : 1);
+    const int gi = w / parts, gj = w - gi * parts;
+    int part = 0;
+    if (gi < groups) {
+        const int i = 64 * gi + lane;
+        const uint4 ilo = s.key[2 * i], ihi = s.key[2 * i + 1];
+        const int span = ((n4 / parts) + 3) & ~3;
+        const int j0 = gj * span;
+        const int j1 = j0 + span < n4 ? j0 + span : n4;
+        for (int j = j0; j < j1; j += 4) {
+            const uint4 a0 = s.key[2 * j], a1 = s.key[2 * j + 1];
+            const uint4 b0 = s.key[2 * j + 2], b1 = s.key[2 * j + 3];
+            const uint4 c0 = s.key[2 * j + 4], c1 = s.key[2 * j + 5];
+            const uint4 d0 = s.key[2 * j + 6], d1 = s.key[2 * j + 7];
+            count_before(part, ilo, ihi, a0, a1);
+            count_before(part, ilo, ihi, b0, b1);
+            count_before(part, ilo, ihi, c0, c1);
+            count_before(part, ilo, ihi, d0, d1);
+        }
+    }
+    s.part[tid] = part;
+    __syncthreads();
+    if (tid < n) {
+        const int gi_t = tid >> 6;
+        int rank = 0;
+        for (int g = 0; g < parts; ++g) rank += s.part[(gi_t * parts + g) * 64 + (tid & 63)];
+        if (rank < K) s.buf[rank] = c;
+        if (rank == K - 1 && before(c, st.thr)) st.thr = c;
+    }
+    if (tid == 0) st.count = n < K ? n : K;
+    __syncthreads();
+}
+
 // Sorts the collected candidates, keeps the best K, and raises the admission
 // threshold to the K-th kept one when that is better.
 __device__ __forceinline__ void compact(Lds& s, State& st, int K) {
     __syncthreads();
-    const int n = st.count;
+    const int n = __builtin_amdgcn_readfirstlane(st.count);
+    if (n <= kRankMax) {
+        compact_by_rank(s, st, K, n);
+        return;
+    }
     int np = 1;
     while (np < n) np <<= 1;
     for (int i = n + static_cast<int>(threadIdx.x); i < np; i += kSelectThreads) s.buf[i] = dead_cand();
@@ -234,6 +335,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     Lds s;
     s.buf = reinterpret_cast<Cand*>(smem + L.off_buf);
     s.rbuf = reinterpret_cast<Cand*>(smem + L.off_rbuf);
+    s.key = reinterpret_cast<uint4*>(smem + L.off_key);
+    s.part = reinterpret_cast<int32_t*>(smem + L.off_key + sizeof(uint4) * 2 * kRankMax);
     float* f = reinterpret_cast<float*>(smem + L.off_f32);
     s.raw = f;
     s.nraw = f + K;
@@ -526,6 +629,8 @@ SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool st
     off = align(off + sizeof(Cand) * static_cast<size_t>(sc));
     L.off_rbuf = off;
     off = align(off + sizeof(Cand) * kRescanBuf);
+    L.off_key = off;
+    off = align(off + sizeof(uint4) * 2 * kRankMax + sizeof(int32_t) * kSelectThreads);
     L.off_f32 = off;
     off = align(off + sizeof(float) * (3 * static_cast<size_t>(K) + 2 * static_cast<size_t>(L.pen_len)));
     L.off_i32 = off;
