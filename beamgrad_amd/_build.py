@@ -26,7 +26,7 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
     "-ffp-contract=off",
     "-fno-fast-math",
@@ -35,7 +35,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-LIB_SOURCES = ["csrc/api.hip", "csrc/decode.hip", "csrc/row_pass.hip", "csrc/row_resident.hip", "csrc/select.hip", "csrc/backward.hip"]
+LIB_SOURCES = ["csrc/api.hip", "csrc/decode.hip", "csrc/row_pass.hip", "csrc/row_resident.hip", "csrc/row_pipe.hip", "csrc/select.hip", "csrc/backward.hip"]
 
 
 def lib_path() -> str:

@@ -5,6 +5,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -126,6 +128,9 @@ hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream);
 // aligned, V <= 155648); launch_row_pass uses it when eligible.
 bool row_resident_eligible(const DecodeParams& p);
 hipError_t launch_row_resident(const DecodeParams& p, int64_t rows, hipStream_t stream);
+bool row_pipe_eligible(const DecodeParams& p);
+extern std::atomic<int> g_row_pass_kind;  // dbs_hip_set_row_pass
+hipError_t launch_row_pipe(const DecodeParams& p, int64_t rows, hipStream_t stream);
 hipError_t launch_select(const DecodeParams& p, const SelectLayout& L, hipStream_t stream);
 
 // Rows the select pass rescanned in full (reset = 1 clears the count).

@@ -10,7 +10,7 @@
 // selection exact.
 #include <hip/hip_runtime.h>
 
-#include <cstdlib>
+#include <atomic>
 
 #include "device_common.hpp"
 
@@ -142,17 +142,17 @@ __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
 
 }  // namespace
 
+std::atomic<int> g_row_pass_kind{-1};
+
 hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream) {
     const int64_t rows = p.step_mode ? static_cast<int64_t>(p.B) * p.K : static_cast<int64_t>(p.B) * p.T * p.K;
     if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
     const size_t esz = p.dtype == 0 ? 4 : 2;
     const bool vec = (p.V % 4 == 0) && (reinterpret_cast<uintptr_t>(p.x) % (4 * esz) == 0);
     KernelTimer timer(kKindRowPass, stream);
-    static const bool resident_off = [] {
-        const char* env = std::getenv("DBS_HIP_RESIDENT");  // testing knob: 0 keeps the two-pass kernel
-        return env != nullptr && env[0] == '0';
-    }();
-    if (!resident_off && row_resident_eligible(p)) return launch_row_resident(p, rows, stream);
+    const int kind = g_row_pass_kind.load(std::memory_order_relaxed);
+    if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return launch_row_resident(p, rows, stream);
+    if ((kind == -1 || kind == 2) && row_pipe_eligible(p)) return launch_row_pipe(p, rows, stream);
     const dim3 grid(static_cast<unsigned>(rows));
 #define DBS_ROW_PASS(DT, LG)                                                                                 \
     do {                                                                                                     \

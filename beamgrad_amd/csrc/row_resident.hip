@@ -33,7 +33,7 @@
 // does not hold fold with the Cephes evaluation instead.
 #include <hip/hip_runtime.h>
 
-#include "device_common.hpp"
+#include "row_helpers.hpp"
 
 namespace dbs_hip {
 
@@ -44,59 +44,11 @@ constexpr int kResRegs = 152;                    // packed element pairs per thr
 constexpr int kResChunks = kResRegs / 4;         // 8-stripe chunks per thread
 constexpr int kResGroups = 4;                    // register groups with their own maxima
 constexpr int kResGroupRegs = kResRegs / kResGroups;
-constexpr int kLutHalf = 4096;                   // table slots per sign
 constexpr int kMaxStripes = 2 * 8 * kResChunks;  // 608 stripes: V <= 155648
 
 // LDS, as separate arrays.
 constexpr int kResLds = 2 * kLutHalf * 4 + 8 * 1024 + 256 * 4 + kSurvivorCap * 12 + 2 * 256 * 4 + 64 + 16;
 static_assert(kResLds <= 160 * 1024, "LDS of the resident row pass");
-
-typedef short v2i16 __attribute__((ext_vector_type(2)));
-typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t pk_max_i16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(v2i16, a), __builtin_bit_cast(v2i16, b)));
-}
-__device__ __forceinline__ uint32_t pk_min_i16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(v2i16, a), __builtin_bit_cast(v2i16, b)));
-}
-__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(v2u16, a), __builtin_bit_cast(v2u16, b)));
-}
-__device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(v2u16, a), __builtin_bit_cast(v2u16, b)));
-}
-__device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(__builtin_bit_cast(v2u16, a), __builtin_bit_cast(v2u16, b)));
-}
-__device__ __forceinline__ uint32_t pk_sub_sat_i16(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(__builtin_bit_cast(v2i16, a), __builtin_bit_cast(v2i16, b)));
-}
-__device__ __forceinline__ uint32_t pk_sign_fill_i16(uint32_t a) {
-    const v2i16 fifteen = {15, 15};
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2i16, a) >> fifteen);
-}
-__device__ __forceinline__ uint32_t pk_shl2_u16(uint32_t a) {
-    const v2u16 two = {2, 2};
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, a) << two);
-}
-
-// Buffer view of one row (bytes [0, nbytes)): loads past its end return
-// zeros instead of touching memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const uint16_t* row, int nbytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(row), 0, nbytes, 0x00020000);
-}
-
-typedef unsigned int v2u32 __attribute__((ext_vector_type(2)));
-typedef unsigned int v4u32 __attribute__((ext_vector_type(4)));
-
-// Workgroup barrier for LDS data only: the wavefront's LDS operations have
-// completed; its global loads may still be in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
 
 // Transposes one chunk: lane L holds 16 bytes = lanes 8 (L % 8) .. + 7 of
 // stripe L / 8; it gets back its own lane L of the 8 stripes, packed two
@@ -128,74 +80,6 @@ __device__ __forceinline__ void transpose_chunk(unsigned char* slot, int L, uint
     R[1] = t0.y;
     R[2] = t1.x;
     R[3] = t1.y;
-}
-
-template <int DT>
-__device__ __forceinline__ float pattern_value(uint32_t h) {
-    return DT == 1 ? half_to_f32(static_cast<uint16_t>(h)) : bf16_to_f32(static_cast<uint16_t>(h));
-}
-
-// Signed 16-bit key of a sign-magnitude pattern, monotone in its value (-0
-// one below +0).
-__device__ __forceinline__ int key16(uint32_t h) {
-    const int s = static_cast<int16_t>(h);
-    return s < 0 ? (s ^ 0x7fff) : s;
-}
-
-// The 16-bit pattern of theta (a value of the row, or -inf).
-template <int DT>
-__device__ __forceinline__ uint32_t value_pattern(float x) {
-    return DT == 2 ? (f32_bits(x) >> 16) : f32_to_f16_rne(x);
-}
-
-// Whether the bfloat16 term table covers a row with maximum m; u_lo out.
-__device__ __forceinline__ bool table_fits(float m, int& ulo) {
-    if (!(m >= 1.0f && m < kInf)) return false;
-    const uint32_t mp = f32_bits(m) >> 16;
-    const int E = static_cast<int>((mp >> 7) & 0xffu) - 127;
-    ulo = (E + 102) << 7;
-    const int ucap = ulo - 1 + (kLutHalf - 1);
-    if (ucap >= 0x7f80) return true;  // the clamp slot is -inf/NaN: term 0
-    const float d = bf16_to_f32(static_cast<uint16_t>(0x8000 | ucap)) - m;
-    return !(d >= -87.0f);
-}
-
-// Inverse of key16.
-__device__ __forceinline__ uint32_t key_pattern(int key) {
-    return static_cast<uint16_t>(key < 0 ? (key ^ 0x7fff) : key);
-}
-
-// Over 256 bins taken in descending order, the bin holding the target-th
-// largest count-weighted key (1-based; the bins hold at least target keys),
-// and how many keys lie in the bins above it. One wavefront, every lane gets
-// the answer.
-__device__ __forceinline__ void hist_select(const int* hist, int target, int lane, int& bin, int& above) {
-    const int4 h = *reinterpret_cast<const int4*>(hist + 252 - 4 * lane);  // bins 252-4l .. 255-4l
-    const int c0 = h.w, c1 = h.z, c2 = h.y, c3 = h.x;                     // descending
-    const int sum = c0 + c1 + c2 + c3;
-    int incl = sum;
-    for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(incl, off);
-        if (lane >= off) incl += t;
-    }
-    const int excl = incl - sum;
-    const uint64_t mine = __ballot(excl < target && target <= incl);
-    const int src = __ffsll(static_cast<long long>(mine)) - 1;
-    int b = 255 - 4 * lane, a = excl;
-    if (a + c0 < target) {
-        a += c0;
-        --b;
-        if (a + c1 < target) {
-            a += c1;
-            --b;
-            if (a + c2 < target) {
-                a += c2;
-                --b;
-            }
-        }
-    }
-    bin = __shfl(b, src);
-    above = __shfl(a, src);
 }
 
 template <int DT, bool LOGITS>

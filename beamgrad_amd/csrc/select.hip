@@ -132,22 +132,16 @@ __device__ __forceinline__ void sort_cands(Cand* buf, int np) {
 // the bitonic sort).
 constexpr int kRankMax = kSelectThreads;
 
-// Order-preserving unsigned image of a float (-0 and +0 map together, as they
-// compare equal; no NaN reaches the collector).
-__device__ __forceinline__ uint32_t order_bits(float f) {
-    const uint32_t u = __float_as_uint(f) & (f == 0.0f ? 0u : 0xffffffffu);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
 // The candidate at collector index idx as a 224-bit integer that is larger
 // exactly when the candidate comes earlier in the total order, least
 // significant word first: index (lower first; it decides only between
 // candidates that compare equal, i.e. dead sentinels), flp (desc), length,
-// token, parent (asc as signed integers), raw, score (desc).
+// token, parent (asc as signed integers), raw, score (desc; no NaN reaches
+// the collector).
 __device__ __forceinline__ void store_key(uint4* dst, const Cand& c, int idx) {
     dst[0] = make_uint4(0xffffffffu - static_cast<uint32_t>(idx), static_cast<uint32_t>(c.flp) ^ 0x80000000u,
                         0x7fffffffu - static_cast<uint32_t>(c.length), 0x7fffffffu - static_cast<uint32_t>(c.token));
-    dst[1] = make_uint4(0x7fffffffu - static_cast<uint32_t>(c.parent), order_bits(c.raw), order_bits(c.score), 0u);
+    dst[1] = make_uint4(0x7fffffffu - static_cast<uint32_t>(c.parent), ordered_key(c.raw), ordered_key(c.score), 0u);
 }
 
 // rank += (key j > key i): the borrow out of key i - key j, kept in VCC

@@ -76,6 +76,15 @@ DBS_CUDA_EXPORT int dbs_hip_backtrack(
 DBS_CUDA_EXPORT int dbs_hip_profile_enable(int on);
 DBS_CUDA_EXPORT int dbs_hip_profile_read(int kernel, double* total_ms, int64_t* launches);
 
+/* Row-pass kernel choice for tests and measurements (no counterpart in the
+ * reference; every choice gives the same results): -1 automatic (the
+ * default: the resident 16-bit kernel where it applies, else the pipelined
+ * 16-bit kernel, else the two-pass kernel), 0 two-pass, 1 resident 16-bit
+ * (V % 8 == 0, 16-byte aligned rows), 2 pipelined 16-bit (any V).
+ * A kernel that does not apply to a decode falls back to the two-pass one.
+ * Returns the previous choice, or -2 for an invalid argument. */
+DBS_CUDA_EXPORT int dbs_hip_set_row_pass(int kind);
+
 #ifdef __cplusplus
 }
 #endif

@@ -85,17 +85,26 @@ def test_invalid_rows_flagged_only_when_read(hip, oracle):
     assert out["invalid"].tolist() == want["invalid"].tolist() == [0, 1, 1]
 
 
-# 16-bit rows with V % 8 == 0 take the row pass that keeps each row on chip
-# (one workgroup per CU); DBS_HIP_RESIDENT=0 selects the two-pass kernel on
-# the same inputs.
-_RESIDENT_VOCABS = [8, 40, 256, 1000, 2048, 3000, 4104, 8200]
+# 16-bit rows have three row-pass kernels with identical results: the
+# pipelined one (the default; any V, rows at any 2-byte offset), the resident
+# one (V % 8 == 0) and the two-pass one. Each runs on the same inputs.
+_ROW_PASS_VOCABS = [8, 40, 255, 256, 257, 1000, 2047, 2048, 3000, 4104, 8200, 8201]
 
 
-@pytest.mark.parametrize("resident", ["1", "0"])
+@pytest.fixture
+def row_pass(hip):
+    def select(kind):
+        hip.lib.dbs_hip_set_row_pass(kind)
+
+    yield select
+    hip.lib.dbs_hip_set_row_pass(-1)
+
+
+@pytest.mark.parametrize("kind", [2, 1, 0])
 @pytest.mark.parametrize("seed", range(0, 30))
-def test_decode_16bit_row_passes(hip, oracle, seed, resident, monkeypatch):
-    monkeypatch.setenv("DBS_HIP_RESIDENT", resident)
-    case = make_case(9000 + seed, dtypes=["bf16", "f16"], vocabs=_RESIDENT_VOCABS, scales=[0.05, 0.5, 2.0, 3.0, 8.0])
+def test_decode_16bit_row_passes(hip, oracle, row_pass, seed, kind):
+    row_pass(kind)
+    case = make_case(9000 + seed, dtypes=["bf16", "f16"], vocabs=_ROW_PASS_VOCABS, scales=[0.05, 0.5, 2.0, 3.0, 8.0])
     _check(hip, oracle, case)
 
 
