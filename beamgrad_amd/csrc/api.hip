@@ -264,7 +264,7 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
         e = launch_fill_f32(row_lse, 0.0f, static_cast<int64_t>(a.batch_size) * a.steps * a.beam_size, stream);
         if (e != hipSuccess) return finish(stream, e);
     }
-    e = launch_decode(p, L, stream);
+    e = launch_decode(p, L, stream, ws);
     return finish(stream, e);
 }
 
@@ -333,7 +333,7 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
         e = launch_fill_f32(row_lse, 0.0f, static_cast<int64_t>(a.batch_size) * a.beam_size, stream);
         if (e != hipSuccess) return finish(stream, e);
     }
-    e = launch_decode(p, L, stream);
+    e = launch_decode(p, L, stream, ws);
     return finish(stream, e);
 }
 
@@ -571,6 +571,11 @@ DBS_CUDA_EXPORT int dbs_cuda_path_gradient(const DBSCudaDecodeArgs* args, const 
     return finish(stream, launch_path_walk(p, stream));
 }
 
+DBS_CUDA_EXPORT int dbs_hip_set_decode_overlap(int on) {
+    if (on < -1 || on > 1) return -2;
+    return dbs_hip::g_overlap.exchange(on);
+}
+
 DBS_CUDA_EXPORT int dbs_hip_set_row_pass(int kind) {
     if (kind < -1 || kind > 2) return -2;
     return dbs_hip::g_row_pass_kind.exchange(kind);
@@ -586,17 +591,20 @@ DBS_CUDA_EXPORT int dbs_hip_profile_enable(int on) {
     }
     g_profile.store(on, std::memory_order_relaxed);
     if (rescan_counter(1, nullptr) != hipSuccess) (void)hipGetLastError();
+    if (wait_timeout_counter(1, nullptr) != hipSuccess) (void)hipGetLastError();
     return DBS_CUDA_STATUS_OK;
 }
 
 DBS_CUDA_EXPORT int dbs_hip_profile_read(int kernel, double* total_ms, int64_t* launches) {
-    if (kernel < 0 || kernel > kKindCount || !total_ms || !launches) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    if (kernel < 0 || kernel > kKindCount + 1 || !total_ms || !launches) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lock(g_profile_mutex);
     drain_pending();
-    if (kernel == kKindCount) {
-        // rows the select pass had to rescan in full since profiling was enabled
+    if (kernel >= kKindCount) {
+        // rows the select pass had to rescan in full / overlapped-decode waits
+        // that gave up, since profiling was enabled
         unsigned long long n = 0;
-        if (rescan_counter(0, &n) != hipSuccess) {
+        const hipError_t e = kernel == kKindCount ? rescan_counter(0, &n) : wait_timeout_counter(0, &n);
+        if (e != hipSuccess) {
             (void)hipGetLastError();
             return DBS_CUDA_STATUS_LAUNCH_FAILED;
         }

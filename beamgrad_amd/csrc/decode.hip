@@ -15,7 +15,9 @@
 // elementwise helpers of the C ABI.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdlib>
+#include <mutex>
 
 #include "engine.hpp"
 
@@ -74,15 +76,88 @@ DecodeLayout decode_layout(int B, int T, int K, int V, bool constrained, bool st
     L.off_blocked = off;
     if (constrained && !L.sel.blk_in_lds)
         off = align(off + sizeof(int32_t) * static_cast<size_t>(B) * K * (L.prefix_cap > 0 ? L.prefix_cap : 1));
+    L.off_sync = off;
+    if (!step_mode) off = align(off + sync_bytes(B, T));
     L.total = off == 0 ? 256 : off;
     (void)V;
     return L;
 }
 
-hipError_t launch_decode(const DecodeParams& p, const DecodeLayout& L, hipStream_t stream) {
-    hipError_t e = launch_row_pass(p, stream);
+std::atomic<int> g_overlap{-1};
+
+namespace {
+
+// The second stream of the overlapped decode and its two events, per device
+// (default priority; created on first use, kept until the process ends).
+struct Aux {
+    hipStream_t stream = nullptr;
+    hipEvent_t start = nullptr, done = nullptr;
+    int cus = 0;
+};
+Aux g_aux[64];
+std::mutex g_aux_mutex;
+
+hipError_t aux_for(int device, Aux*& out) {
+    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+    Aux& a = g_aux[device];
+    if (!a.stream) {
+        hipError_t e = hipDeviceGetAttribute(&a.cus, hipDeviceAttributeMultiprocessorCount, device);
+        if (e == hipSuccess) e = hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&a.start, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&a.done, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            a.stream = nullptr;
+            return e;
+        }
+    }
+    out = &a;
+    return hipSuccess;
+}
+
+}  // namespace
+
+size_t sync_bytes(int B, int T) {
+    return ((sizeof(int32_t) * static_cast<size_t>(B) * static_cast<size_t>(T) + 7) & ~static_cast<size_t>(7)) +
+           sizeof(unsigned long long);
+}
+
+// The row pass, then the select pass. With several steps and at most half
+// the CUs taken by the select pass's workgroups (one per example), the select
+// pass can run alongside on a second stream, following the row pass step by
+// step: the row pass is queued first and never waits on the select pass, and
+// its rows are handed out by ticket, so it always progresses on the CUs left.
+// By default only constrained decodes (n-gram blocking, repetition penalty)
+// do: their select pass is as long as the row pass, while elsewhere the CUs
+// the row pass loses cost more than the overlap saves (measured on MI355X).
+hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStream_t stream, char* ws) {
+    DecodeParams p = p0;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess) return e;
-    return launch_select(p, L.sel, stream);
+    std::lock_guard<std::mutex> lock(g_aux_mutex);
+    Aux* aux = nullptr;
+    const int mode = g_overlap.load(std::memory_order_relaxed);
+    const bool want = !p.step_mode && p.T > 1 && (mode == 1 || (mode == -1 && p.constrained));
+    if (want) {
+        e = aux_for(device, aux);
+        if (e != hipSuccess) return e;
+    }
+    if (!want || 2 * p.B > aux->cus) {
+        e = launch_row_pass(p, stream);
+        if (e != hipSuccess) return e;
+        return launch_select(p, L.sel, stream);
+    }
+    char* sync = ws + L.off_sync;
+    p.step_done = reinterpret_cast<int32_t*>(sync);
+    p.row_ticket = reinterpret_cast<unsigned long long*>(sync + sync_bytes(p.B, p.T) - sizeof(unsigned long long));
+    e = launch_fill_f32(reinterpret_cast<float*>(sync), 0.0f, static_cast<int64_t>(sync_bytes(p.B, p.T) / 4), stream);
+    if (e == hipSuccess) e = hipEventRecord(aux->start, stream);
+    if (e == hipSuccess) e = launch_row_pass(p, stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(aux->stream, aux->start, 0);
+    if (e == hipSuccess) e = launch_select(p, L.sel, aux->stream);
+    if (e == hipSuccess) e = hipEventRecord(aux->done, aux->stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(stream, aux->done, 0);
+    return e;
 }
 
 hipError_t launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream) {

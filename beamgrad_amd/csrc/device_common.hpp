@@ -78,6 +78,48 @@ __device__ __forceinline__ bool row_is_read(const DecodeParams& p, int64_t r, in
     return true;
 }
 
+// The row a processing index stands for: step-major (every example's step t
+// before step t + 1) in the overlapped decode, so the select pass can follow
+// the row pass step by step; the index itself otherwise.
+__device__ __forceinline__ int64_t row_of_ticket(const DecodeParams& p, int64_t q) {
+    if (!p.step_done) return q;
+    const int64_t K = p.K, B = p.B;
+    const int64_t k = q % K, bt = q / K;
+    const int64_t b = bt % B, t = bt / B;
+    return (b * p.T + t) * K + k;
+}
+
+// The next processing index of a persistent row-pass workgroup: its own
+// stride without tickets, else the next ticket (thread-uniform; call from one
+// thread and share).
+__device__ __forceinline__ int64_t take_ticket(const DecodeParams& p, int64_t after, int64_t stride) {
+    if (!p.row_ticket) return after + stride;
+    return static_cast<int64_t>(__hip_atomic_fetch_add(p.row_ticket, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// Shared words of the overlapped decode (the row pass's RowInfo and
+// shortlists, read by the select pass while the row pass still runs) are
+// stored and loaded as device-scope atomics: coherent across the XCDs' L2
+// caches word by word, without whole-cache write-backs or invalidations.
+__device__ __forceinline__ void store_shared(uint32_t* dst, uint32_t v, bool coherent) {
+    if (coherent) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *dst = v;
+}
+__device__ __forceinline__ uint32_t load_shared(const uint32_t* src, bool coherent) {
+    return coherent ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *src;
+}
+
+// Row r's RowInfo and shortlist are stored (device-scope words): once they
+// have completed, count the row for its step. One wavefront.
+__device__ __forceinline__ void signal_row_done(const DecodeParams& p, int64_t r, int lane) {
+    if (!p.step_done) return;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0) {
+        const int64_t bt = r / p.K;  // b * T + t
+        __hip_atomic_fetch_add(p.step_done + bt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // Bitonic sort (descending) of 256 values held 4 per lane (element i = 4 *
 // lane + e) across one wavefront.
 __device__ __forceinline__ void sort256_desc(float (&a)[4], int lane) {
@@ -156,6 +198,7 @@ template <bool LOGITS, bool FILTER>
 __device__ void finish_row_wave(const DecodeParams& p, int64_t r, float lse, float theta, bool any_bad,
                                 uint64_t* s_key, float* s_x, int n, int lane, int b, bool mask_eos) {
     const int M = p.M;
+    const bool coherent = p.step_done != nullptr;
     RowInfo info;
     info.lse = lse;
     info.invalid = any_bad ? 1u : 0u;
@@ -207,15 +250,23 @@ __device__ void finish_row_wave(const DecodeParams& p, int64_t r, float lse, flo
             for (int i = lane; i < cnt; i += 64) {
                 const float x = s_x[i];
                 const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(s_key[i] & 0xffffffffu));
-                out[i].lp = LOGITS ? x - lse : x;
-                out[i].token = tok;
+                store_shared(reinterpret_cast<uint32_t*>(&out[i].lp), f32_bits(LOGITS ? x - lse : x), coherent);
+                store_shared(reinterpret_cast<uint32_t*>(&out[i].token), static_cast<uint32_t>(tok), coherent);
             }
             const float bx = n > M ? s_x[M] : theta;
             info.count = cnt;
             info.bound = (bx > -kInf) ? (LOGITS ? bx - lse : bx) : -kInf;
         }
     }
-    if (lane == 0) p.rowinfo[r] = info;
+    if (lane == 0) {
+        static_assert(sizeof(RowInfo) == 16, "RowInfo words");
+        uint32_t w[4];
+        __builtin_memcpy(w, &info, sizeof(w));
+        uint32_t* dst = reinterpret_cast<uint32_t*>(p.rowinfo + r);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_shared(dst + i, w[i], coherent);
+    }
+    signal_row_done(p, r, lane);
 }
 
 }  // namespace dbs_hip

@@ -98,6 +98,12 @@ struct DecodeParams {
     uint8_t* st_fin;
     const int32_t* st_prefix;  // [B, K, st_stride]
     int st_stride;
+    // Overlapped decode (null: the select pass runs after the row pass): the
+    // row pass hands out rows step-major through row_ticket and counts the
+    // finished rows of each (example, step) in step_done [B, T]; the select
+    // pass waits for a step's count before it reads that step.
+    int32_t* step_done;
+    unsigned long long* row_ticket;
 };
 
 // LDS plan of the select pass (byte offsets into its dynamic shared memory).
@@ -115,14 +121,17 @@ struct DecodeLayout {
     int use_tau;
     int prefix_cap;
     SelectLayout sel;
-    size_t off_rowinfo, off_short, off_prefix, off_blocked, total;
+    size_t off_rowinfo, off_short, off_prefix, off_blocked, off_sync, total;
 };
 
 DecodeLayout decode_layout(int B, int T, int K, int V, bool constrained, bool step_mode, int prefix_stride);
 SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool step_mode, int prefix_cap);
 
-// Queues the decode (or one step) on `stream`; returns a hipError_t.
-hipError_t launch_decode(const DecodeParams& p, const DecodeLayout& L, hipStream_t stream);
+// Queues the decode (or one step) on `stream` with workspace ws; returns a
+// hipError_t.
+hipError_t launch_decode(const DecodeParams& p, const DecodeLayout& L, hipStream_t stream, char* ws);
+size_t sync_bytes(int B, int T);           // overlapped-decode counters in the workspace
+extern std::atomic<int> g_overlap;         // dbs_hip_set_decode_overlap
 hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream);
 // Row pass that keeps each row on chip (16-bit rows, V % 8 == 0, 16-byte
 // aligned, V <= 155648); launch_row_pass uses it when eligible.
@@ -135,6 +144,9 @@ hipError_t launch_select(const DecodeParams& p, const SelectLayout& L, hipStream
 
 // Rows the select pass rescanned in full (reset = 1 clears the count).
 hipError_t rescan_counter(int reset, unsigned long long* value);
+// Select-pass waits for a step that gave up (the overlapped decode's bounded
+// wait; nonzero means results may be wrong). reset / read like rescan_counter.
+hipError_t wait_timeout_counter(int reset, unsigned long long* value);
 
 // Elementwise helpers.
 hipError_t launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream);

@@ -128,4 +128,50 @@ __device__ __forceinline__ void hist_select(const int* hist, int target, int lan
     above = __shfl(a, src);
 }
 
+// Row sequence of a persistent row-pass workgroup. Thread 0 finds the rows
+// (the workgroup's stride, or tickets in the overlapped decode) and publishes
+// them in LDS slots; every wavefront reads a slot after a barrier.
+struct RowSlot {
+    long long r;
+    int b, len;
+};
+
+__device__ __forceinline__ int64_t first_ticket(const DecodeParams& p) {
+    return p.row_ticket ? take_ticket(p, 0, 0) : static_cast<int64_t>(blockIdx.x);
+}
+
+// From processing index q on, the first row the search reads (q is left at
+// it), or rows when none is left.
+__device__ __forceinline__ int64_t find_read_row(const DecodeParams& p, int64_t rows, int64_t& q, int& b, int& len) {
+    while (q < rows) {
+        const int64_t rr = row_of_ticket(p, q);
+        if (row_is_read(p, rr, b, len)) return rr;
+        q = take_ticket(p, q, gridDim.x);
+    }
+    return rows;
+}
+
+// Thread 0: the row after processing index q (advanced) into slot.
+__device__ __forceinline__ void publish_next_row(const DecodeParams& p, int64_t rows, int64_t& q, RowSlot& slot) {
+    int b = 0, len = 0;
+    int64_t rr = rows;
+    if (q < rows) {
+        q = take_ticket(p, q, gridDim.x);
+        rr = find_read_row(p, rows, q, b, len);
+    }
+    slot.r = rr;
+    slot.b = b;
+    slot.len = len;
+}
+
+// Every lane: a published row (kept in scalar registers).
+__device__ __forceinline__ int64_t read_row_slot(const RowSlot& slot, int& b, int& len) {
+    const long long rr = slot.r;
+    b = __builtin_amdgcn_readfirstlane(slot.b);
+    len = __builtin_amdgcn_readfirstlane(slot.len);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(rr));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<unsigned long long>(rr) >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 }  // namespace dbs_hip

@@ -62,7 +62,7 @@ __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
     __shared__ int s_count;
 
     const int lane = static_cast<int>(threadIdx.x);
-    const int64_t r = blockIdx.x;
+    const int64_t r = row_of_ticket(p, blockIdx.x);
     const int V = p.V;
     int b, new_len;
     if (!row_is_read(p, r, b, new_len)) return;

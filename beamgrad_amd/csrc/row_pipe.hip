@@ -141,17 +141,6 @@ __global__ __launch_bounds__(kPipeThreads) void row_pipe_kernel(DecodeParams p, 
         pend = false;
     };
 
-    // (the row index and what derives from it are the same in every lane:
-    // readfirstlane keeps them, and the buffer views, in scalar registers)
-    auto next_read_row = [&](int64_t rr, int& b_out, int& len_out) -> int64_t {
-        while (rr < rows && !row_is_read(p, rr, b_out, len_out)) rr += gridDim.x;
-        b_out = __builtin_amdgcn_readfirstlane(b_out);
-        len_out = __builtin_amdgcn_readfirstlane(len_out);
-        const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(rr));
-        const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(rr) >> 32));
-        return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-    };
-
     uint32_t reg[kWin];
     // The segment's windows of row rr, straight into the registers (the
     // compiler waits for each before its first use).
@@ -174,17 +163,29 @@ __global__ __launch_bounds__(kPipeThreads) void row_pipe_kernel(DecodeParams p, 
                 sv.rs, (__attribute__((address_space(3))) void*)(stage + 256 * q), 16, voff, 2048 * q, 0, 0);
     };
 
-    int b = 0, new_len = 0, par = 0;
-    int64_t r = next_read_row(blockIdx.x, b, new_len);
+    // the row sequence (thread 0 finds it two rows ahead; three slots in turn)
+    __shared__ RowSlot s_rows[3];
+    int64_t q_next = 0;  // thread 0's processing index
+    if (tid == 0) {
+        q_next = first_ticket(p);
+        int b0 = 0, len0 = 0;
+        s_rows[0].r = find_read_row(p, rows, q_next, b0, len0);
+        s_rows[0].b = b0;
+        s_rows[0].len = len0;
+        publish_next_row(p, rows, q_next, s_rows[1]);
+    }
+    __syncthreads();
+    int b = 0, new_len = 0, par = 0, rslot = 0;
+    int64_t r = read_row_slot(s_rows[0], b, new_len);
     int bn = 0, lenn = 0;
-    int64_t rn = r < rows ? next_read_row(r + gridDim.x, bn, lenn) : rows;
+    int64_t rn = read_row_slot(s_rows[1], bn, lenn);
     if (r < rows) {
         load_windows(r);
         if (seg == 0 && rn < rows) stage_windows(rn);
     }
     while (r < rows) {
-        int bnn = 0, lennn = 0;
-        const int64_t rnn = rn < rows ? next_read_row(rn + gridDim.x, bnn, lennn) : rows;
+        const int slot2 = rslot == 0 ? 2 : rslot - 1;  // (rslot + 2) % 3
+        if (tid == 0) publish_next_row(p, rows, q_next, s_rows[slot2]);
         const bool mask_eos = new_len < p.min_length;
         const uint16_t* row = static_cast<const uint16_t*>(p.x) + r * V;
         const int sh = static_cast<int>((r * static_cast<int64_t>(V)) & 1);
@@ -255,6 +256,8 @@ __global__ __launch_bounds__(kPipeThreads) void row_pipe_kernel(DecodeParams p, 
             s_wbad[wave] = wbad ? 1 : 0;
         }
         lds_barrier();
+        int bnn = 0, lennn = 0;
+        const int64_t rnn = read_row_slot(s_rows[slot2], bnn, lennn);  // published before the barrier
 
         int mkey = -32768;
         bool any_bad = false;
@@ -468,6 +471,7 @@ __global__ __launch_bounds__(kPipeThreads) void row_pipe_kernel(DecodeParams p, 
             pend_par = par;
         }
         par ^= 1;
+        rslot = rslot == 2 ? 0 : rslot + 1;
         r = rn;
         b = bn;
         new_len = lenn;

@@ -148,17 +148,6 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
         pend = false;
     };
 
-    // (the row index and what derives from it are the same in every lane:
-    // readfirstlane lets the compiler keep them, and the row's buffer view,
-    // in scalar registers)
-    auto next_read_row = [&](int64_t rr, int& b_out, int& len_out) -> int64_t {
-        while (rr < rows && !row_is_read(p, rr, b_out, len_out)) rr += gridDim.x;
-        b_out = __builtin_amdgcn_readfirstlane(b_out);
-        len_out = __builtin_amdgcn_readfirstlane(len_out);
-        const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(rr));
-        const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(rr) >> 32));
-        return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-    };
     // byte offset in the segment of this lane's 16 bytes of chunk 0 (stripe
     // l/8 of the segment, lanes 64 wv + 8 (l % 8) ..); chunk c adds the
     // scalar 4096 c
@@ -168,11 +157,43 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
         return 2 * (256 * (lr >> 3) + 64 * wv + 8 * (lr & 7));
     };
 
-    int b = 0, new_len = 0;
-    int64_t r = next_read_row(blockIdx.x, b, new_len);
+    // The row sequence: every wavefront steps through its workgroup's rows
+    // by itself (in scalar registers); with tickets, thread 0 takes them and
+    // publishes them in LDS slots by row parity.
+    __shared__ RowSlot s_rows[2];
+    const bool tickets = p.row_ticket != nullptr;
+    auto next_read_row = [&](int64_t rr, int& b_out, int& len_out) -> int64_t {
+        while (rr < rows && !row_is_read(p, rr, b_out, len_out)) rr += gridDim.x;
+        b_out = __builtin_amdgcn_readfirstlane(b_out);
+        len_out = __builtin_amdgcn_readfirstlane(len_out);
+        const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(rr));
+        const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(rr) >> 32));
+        return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+    };
+    int64_t q_next = 0;  // thread 0's processing index (tickets)
+    int b = 0, new_len = 0, par = 0;
+    int64_t r = rows;
+    if (tickets) {
+        if (tid == 0) {
+            q_next = first_ticket(p);
+            int b0 = 0, len0 = 0;
+            s_rows[0].r = find_read_row(p, rows, q_next, b0, len0);
+            s_rows[0].b = b0;
+            s_rows[0].len = len0;
+        }
+        __syncthreads();
+        r = read_row_slot(s_rows[0], b, new_len);
+    } else {
+        r = next_read_row(blockIdx.x, b, new_len);
+    }
     while (r < rows) {
         int bn = 0, lenn = 0;
-        const int64_t rn = next_read_row(r + gridDim.x, bn, lenn);
+        int64_t rn = rows;
+        if (tickets) {
+            if (tid == 0) publish_next_row(p, rows, q_next, s_rows[par ^ 1]);
+        } else {
+            rn = next_read_row(r + gridDim.x, bn, lenn);
+        }
         const bool mask_eos = new_len < p.min_length;
         const uint16_t* row = static_cast<const uint16_t*>(p.x) + r * V;
         // Opaque copies per row: everything the unrolled load derives from
@@ -470,9 +491,14 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             pend_full = full;
             pend_b = b;
         }
-        r = rn;
-        b = bn;
-        new_len = lenn;
+        if (tickets) {
+            r = read_row_slot(s_rows[par ^ 1], b, new_len);  // published before this row's first barrier
+            par ^= 1;
+        } else {
+            r = rn;
+            b = bn;
+            new_len = lenn;
+        }
     }
     if (wave == 0 && pend) finish_pending();
 }

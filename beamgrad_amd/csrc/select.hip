@@ -20,6 +20,33 @@ namespace {
 
 // Rows rescanned since the last reset (read through dbs_hip_profile_read).
 __device__ unsigned long long g_rescanned_rows;
+// Waits for a step of the overlapped decode that gave up (should stay 0).
+__device__ unsigned long long g_wait_timeouts;
+
+// Upper bound of one wait for a step's rows: 2 s of the 100 MHz real-time
+// counter (a whole row pass takes milliseconds). The row pass never waits on
+// the select pass, so the bound only keeps a fault elsewhere from hanging the
+// workgroup; after one wait gives up, the workgroup waits no more.
+constexpr unsigned long long kWaitTicks = 200000000ull;
+
+// Overlapped decode: waits until the row pass has finished every row of
+// example b's step t (one at step 0, else K). Their RowInfo and shortlist
+// words were stored, and are read, as device-scope atomics, and the count
+// follows their completion. One thread; false when the wait gave up.
+__device__ __forceinline__ bool wait_step_rows(const DecodeParams& p, int b, int t) {
+    const int need = t == 0 ? 1 : p.K;
+    const int32_t* cnt = p.step_done + static_cast<int64_t>(b) * p.T + t;
+    if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= need) return true;
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+        __builtin_amdgcn_s_sleep(4);
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kWaitTicks) {
+            atomicAdd(&g_wait_timeouts, 1ull);
+            return false;
+        }
+    }
+    return true;
+}
 
 constexpr int kRescanBuf = 512;   // candidates of one rescanned row kept before falling back
 constexpr int kRescanPerThread = 16;
@@ -49,6 +76,7 @@ struct Lds {
 };
 
 struct State {
+    int gave_up;  // a wait of the overlapped decode gave up
     int count;
     int any_fail;
     int rcount;
@@ -379,7 +407,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         s.plen[k] = 0;
         s.plen[K + k] = 0;
     }
-    if (tid == 0) st.invalid = 0;
+    if (tid == 0) {
+        st.invalid = 0;
+        st.gave_up = 0;
+    }
     __syncthreads();
 
     int cur = 0;
@@ -403,6 +434,12 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             st.tau = -kInf;
             st.thr = dead_cand();
         }
+        if (p.step_done && !st.gave_up) {
+            // the row pass runs alongside: wait for this step's rows
+            if (tid == 0 && !wait_step_rows(p, b, t)) st.gave_up = 1;
+            __syncthreads();
+        }
+        const bool coherent = p.step_done != nullptr;
         // Stage the step: row statistics of the rows read, the shortlists,
         // and the n-gram-blocked tokens of each beam.
         for (int k = tid; k < K; k += kSelectThreads) {
@@ -412,7 +449,14 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             int cnt = -2;
             float bound = -kInf;
             if (live && !carried) {
-                const RowInfo info = p.rowinfo[trace0 + k];
+                RowInfo info;
+                {
+                    uint32_t w[4];
+                    const uint32_t* src = reinterpret_cast<const uint32_t*>(p.rowinfo + trace0 + k);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) w[i] = load_shared(src + i, coherent);
+                    __builtin_memcpy(&info, w, sizeof(info));
+                }
                 if (info.invalid) atomicOr(&st.invalid, 1u);
                 if (p.row_lse && LOGITS) p.row_lse[trace0 + k] = info.lse;
                 cnt = M > 0 ? info.count : -1;
@@ -439,7 +483,13 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         }
         if (M > 0) {
             const ShortEntry* src = p.shortlist + trace0 * M;
-            for (int i = tid; i < K * M; i += kSelectThreads) s.sl[i] = src[i];
+            const uint32_t* src32 = reinterpret_cast<const uint32_t*>(src);
+            for (int i = tid; i < K * M; i += kSelectThreads) {
+                ShortEntry e;
+                e.lp = bits_f32(load_shared(src32 + 2 * i, coherent));
+                e.token = static_cast<int32_t>(load_shared(src32 + 2 * i + 1, coherent));
+                s.sl[i] = e;
+            }
         }
         __syncthreads();
         if (p.use_tau) {
@@ -663,6 +713,14 @@ hipError_t launch_select(const DecodeParams& p, const SelectLayout& L, hipStream
         case 1: return launch_select_typed<1, false>(p, L, stream);
         default: return launch_select_typed<2, false>(p, L, stream);
     }
+}
+
+hipError_t wait_timeout_counter(int reset, unsigned long long* value) {
+    if (reset) {
+        const unsigned long long zero = 0;
+        return hipMemcpyToSymbol(HIP_SYMBOL(g_wait_timeouts), &zero, sizeof(zero));
+    }
+    return hipMemcpyFromSymbol(value, HIP_SYMBOL(g_wait_timeouts), sizeof(*value));
 }
 
 hipError_t rescan_counter(int reset, unsigned long long* value) {

@@ -69,7 +69,10 @@ DBS_CUDA_EXPORT int dbs_hip_backtrack(
 /* Launch timing for measurement tools (no counterpart in the reference).
  * With profiling on, every kernel the library launches is bracketed by HIP
  * events on the caller's stream, and its duration is summed per kernel kind:
- * 0 row pass, 1 select, 2 path walk, 3 dense gradient, 4 backtrack.
+ * 0 row pass, 1 select, 2 path walk, 3 dense gradient, 4 backtrack; kind 5
+ * returns (in launches) the rows the select pass rescanned in full and kind 6
+ * the overlapped-decode waits that gave up (always 0 unless something else
+ * failed).
  * dbs_hip_profile_enable(on) clears the sums; dbs_hip_profile_read waits for
  * the recorded events and returns the sum (milliseconds) and the number of
  * launches of one kind. Off by default; costs two event records per launch. */
@@ -84,6 +87,16 @@ DBS_CUDA_EXPORT int dbs_hip_profile_read(int kernel, double* total_ms, int64_t* 
  * A kernel that does not apply to a decode falls back to the two-pass one.
  * Returns the previous choice, or -2 for an invalid argument. */
 DBS_CUDA_EXPORT int dbs_hip_set_row_pass(int kind);
+
+/* Whether a multi-step decode runs its select pass alongside the row pass, on
+ * a second stream that the caller's stream then waits for (no counterpart in
+ * the reference; the results are the same either way): -1 automatic (the
+ * default: constrained decodes, whose select pass is as long as the row
+ * pass), 1 always, 0 never (the select pass after the row pass on the
+ * caller's stream). Applies when at most half the CUs would hold the select
+ * pass's workgroups (one per example). Returns the previous setting, or -2
+ * for an invalid argument. */
+DBS_CUDA_EXPORT int dbs_hip_set_decode_overlap(int on);
 
 #ifdef __cplusplus
 }

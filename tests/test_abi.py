@@ -37,7 +37,7 @@ def lib():
 
 def test_every_declared_symbol_is_exported(lib):
     names = declared_symbols()
-    assert len(names) == 23  # 17 reference entry points + 6 additions
+    assert len(names) == 24  # 17 reference entry points + 7 additions
     out = subprocess.run(["nm", "-D", "--defined-only", _build.lib_path()], capture_output=True, text=True,
                          check=True).stdout
     exported = set(re.findall(r" T (dbs_\w+)", out))
@@ -144,3 +144,5 @@ def test_host_entry_points(lib):
     assert lib.dbs_hip_set_row_pass(3) == -2
     assert lib.dbs_hip_set_row_pass(-1) == -1  # automatic is the default
     assert lib.dbs_hip_set_row_pass(-1) == -1
+    assert lib.dbs_hip_set_decode_overlap(2) == -2
+    assert lib.dbs_hip_set_decode_overlap(-1) == -1  # automatic by default

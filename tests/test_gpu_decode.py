@@ -181,3 +181,28 @@ def test_decode_large_vocab_16bit(hip, oracle, V, dtype):
     got = hip.decode(xin, dtype, **kw)
     diff = first_difference(got, want)
     assert diff is None, f"V={V} {dtype}: {diff}"
+
+
+# A multi-step decode can run its select pass alongside the row pass (a second
+# stream that follows the row pass step by step; dbs_hip_set_decode_overlap:
+# 1 always, 0 never, -1 constrained decodes only). Every order gives the
+# oracle's bits, with every row-pass kernel, and no wait for a step gives up.
+@pytest.mark.parametrize("kind", [-1, 2, 0])
+@pytest.mark.parametrize("overlap", [1, 0, -1])
+@pytest.mark.parametrize("seed", range(0, 10))
+def test_decode_overlapped_select(hip, oracle, row_pass, seed, overlap, kind):
+    import ctypes as C
+
+    lib = hip.lib
+    row_pass(kind)
+    prev = lib.dbs_hip_set_decode_overlap(overlap)
+    try:
+        lib.dbs_hip_profile_enable(1)  # clears the counters
+        case = make_case(9700 + seed, dtypes=["bf16", "f16", "f32"], vocabs=[40, 1000, 4104, 8201])
+        _check(hip, oracle, case)
+        ms, n = C.c_double(), C.c_int64()
+        assert lib.dbs_hip_profile_read(6, C.byref(ms), C.byref(n)) == 0
+        assert n.value == 0, "a wait of the overlapped decode gave up"
+    finally:
+        lib.dbs_hip_profile_enable(0)
+        lib.dbs_hip_set_decode_overlap(prev)
