@@ -150,6 +150,7 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     char* sync = ws + L.off_sync;
     p.step_done = reinterpret_cast<int32_t*>(sync);
     p.row_ticket = reinterpret_cast<unsigned long long*>(sync + sync_bytes(p.B, p.T) - sizeof(unsigned long long));
+    p.reserve_cus = p.B;  // a persistent row pass would otherwise hold every CU until it ends
     e = launch_fill_f32(reinterpret_cast<float*>(sync), 0.0f, static_cast<int64_t>(sync_bytes(p.B, p.T) / 4), stream);
     if (e == hipSuccess) e = hipEventRecord(aux->start, stream);
     if (e == hipSuccess) e = launch_row_pass(p, stream);

@@ -44,6 +44,11 @@ __device__ __forceinline__ bool static_masked(const DecodeParams& p, int b, int 
 
 __device__ __forceinline__ int example_steps(const DecodeParams& p, int b) { return p.steps ? p.steps[b] : p.T; }
 
+__device__ __forceinline__ int wave_sum(int v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;

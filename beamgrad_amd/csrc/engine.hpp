@@ -104,6 +104,7 @@ struct DecodeParams {
     // pass waits for a step's count before it reads that step.
     int32_t* step_done;
     unsigned long long* row_ticket;
+    int reserve_cus;  // CUs the persistent row-pass kernels leave free (the select pass's workgroups)
 };
 
 // LDS plan of the select pass (byte offsets into its dynamic shared memory).

@@ -489,7 +489,9 @@ int pipe_windows(int V) { return ((V + 256) / 256 + kSegs - 1) / kSegs; }
 
 template <int DT, bool LOGITS>
 hipError_t launch_pipe(const DecodeParams& p, int64_t rows, int device, hipStream_t stream) {
-    const int64_t grid = rows < g_pipe_cu_count[device] ? rows : g_pipe_cu_count[device];
+    // one workgroup per CU, less the CUs left to an overlapped select pass
+    const int64_t cus = g_pipe_cu_count[device] - p.reserve_cus > 0 ? g_pipe_cu_count[device] - p.reserve_cus : 1;
+    const int64_t grid = rows < cus ? rows : cus;
     const dim3 g(static_cast<unsigned>(grid)), blk(kPipeThreads);
     const int P = pipe_windows(p.V);
     if (P <= 64) hipLaunchKernelGGL((row_pipe_kernel<DT, LOGITS, 64>), g, blk, 0, stream, p, rows);

@@ -507,7 +507,9 @@ int g_cu_count[64];
 
 template <int DT, bool LOGITS>
 hipError_t launch_resident(const DecodeParams& p, int64_t rows, int device, hipStream_t stream) {
-    const int64_t grid = rows < g_cu_count[device] ? rows : g_cu_count[device];
+    // one workgroup per CU, less the CUs left to an overlapped select pass
+    const int64_t cus = g_cu_count[device] - p.reserve_cus > 0 ? g_cu_count[device] - p.reserve_cus : 1;
+    const int64_t grid = rows < cus ? rows : cus;
     hipLaunchKernelGGL((row_resident_kernel<DT, LOGITS>), dim3(static_cast<unsigned>(grid)), dim3(kResThreads), 0,
                        stream, p, rows);
     return hipGetLastError();

@@ -50,6 +50,8 @@ __device__ __forceinline__ bool wait_step_rows(const DecodeParams& p, int b, int
 
 constexpr int kRescanBuf = 512;   // candidates of one rescanned row kept before falling back
 constexpr int kRescanPerThread = 16;
+constexpr int kTauHead = 2;       // entries per row behind the second tau bound
+constexpr int kWideBeam = 16;     // beams from which the wide-beam paths pay off
 
 struct Lds {
     Cand* buf;        // [sort_cap] the collector
@@ -70,7 +72,7 @@ struct Lds {
     int32_t* rcount;  // [K] shortlist entries of the beam's row (-2 not read, -1 no shortlist, -3 failed check)
     int32_t* plen;    // [2K] prefix lengths
     int32_t* nblk;    // [K] n-gram-blocked tokens of each beam
-    ShortEntry* sl;   // [K * M] the step's shortlists
+    ShortEntry* sl;   // [K, M + 1] the step's shortlists (see sl_at)
     int32_t* prefix;  // [2, K, P] (LDS) or the example's slice of the workspace
     int32_t* blk;     // [K, P] (LDS) or workspace
 };
@@ -85,6 +87,12 @@ struct State {
     float tau;
     Cand thr;
 };
+
+// Entry i of beam k's shortlist in LDS. Wide beams pad the rows to M + 1
+// entries, so the lanes of a wavefront reading entry i of consecutive beams
+// spread over the banks.
+__device__ __forceinline__ int sl_stride(int K, int M) { return K >= kWideBeam ? M + 1 : M; }
+__device__ __forceinline__ int sl_at(int k, int i, int S) { return k * S + i; }
 
 __device__ __forceinline__ float pen_of(const Lds& s, int pen_len, int l, float alpha) {
     const int c = l > 1 ? l : 1;
@@ -191,6 +199,17 @@ __device__ __forceinline__ void count_before(int& rank, const uint4& ilo, const 
         : "vcc");
 }
 
+// rank += (64-bit key (hi, lo) j > key i): the borrow out of i - j.
+__device__ __forceinline__ void count_above64(int& rank, uint32_t ilo, uint32_t ihi, uint32_t jlo, uint32_t jhi) {
+    uint32_t t;
+    asm("v_sub_co_u32 %0, vcc, %2, %4\n\t"
+        "v_subb_co_u32 %0, vcc, %3, %5, vcc\n\t"
+        "v_addc_co_u32 %1, vcc, 0, %1, vcc"
+        : "=&v"(t), "+v"(rank)
+        : "v"(ilo), "v"(ihi), "v"(jlo), "v"(jhi)
+        : "vcc");
+}
+
 // Keeps the best K of n <= kRankMax collected candidates, in order: every
 // candidate's rank is the number of keys above its own, counted by up to four
 // waves per candidate over disjoint ranges of the others, and the candidates
@@ -221,7 +240,15 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
         const int span = ((n4 / parts) + 3) & ~3;
         const int j0 = gj * span;
         const int j1 = j0 + span < n4 ? j0 + span : n4;
-        for (int j = j0; j < j1; j += 4) {
+        int j = j0;
+        for (; j + 8 <= j1; j += 8) {  // eight keys in flight
+            uint4 w[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) w[u] = s.key[2 * j + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) count_before(part, ilo, ihi, w[2 * u], w[2 * u + 1]);
+        }
+        for (; j < j1; j += 4) {
             const uint4 a0 = s.key[2 * j], a1 = s.key[2 * j + 1];
             const uint4 b0 = s.key[2 * j + 2], b1 = s.key[2 * j + 3];
             const uint4 c0 = s.key[2 * j + 4], c1 = s.key[2 * j + 5];
@@ -351,6 +378,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ State st;
     const int K = p.K, T = p.T, M = p.M;
+    const int SL = sl_stride(K, M);
     const int b = static_cast<int>(blockIdx.x);
     const int tid = static_cast<int>(threadIdx.x);
 
@@ -450,11 +478,13 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             float bound = -kInf;
             if (live && !carried) {
                 RowInfo info;
-                {
+                if (!coherent) {
+                    info = p.rowinfo[trace0 + k];
+                } else {
                     uint32_t w[4];
                     const uint32_t* src = reinterpret_cast<const uint32_t*>(p.rowinfo + trace0 + k);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) w[i] = load_shared(src + i, coherent);
+                    for (int i = 0; i < 4; ++i) w[i] = load_shared(src + i, true);
                     __builtin_memcpy(&info, w, sizeof(info));
                 }
                 if (info.invalid) atomicOr(&st.invalid, 1u);
@@ -483,25 +513,90 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         }
         if (M > 0) {
             const ShortEntry* src = p.shortlist + trace0 * M;
-            const uint32_t* src32 = reinterpret_cast<const uint32_t*>(src);
-            for (int i = tid; i < K * M; i += kSelectThreads) {
-                ShortEntry e;
-                e.lp = bits_f32(load_shared(src32 + 2 * i, coherent));
-                e.token = static_cast<int32_t>(load_shared(src32 + 2 * i + 1, coherent));
-                s.sl[i] = e;
+            if (!coherent && (M & 1) == 0 && K * M >= kWideBeam * 16) {
+                // 16-byte loads (two entries of one row: with M even the rows'
+                // shortlists start 16-byte aligned), eight in flight per
+                // thread
+                const uint4* src4 = reinterpret_cast<const uint4*>(src);
+                const int n4 = K * M / 2;
+                for (int i0 = tid; i0 < n4; i0 += 8 * kSelectThreads) {
+                    uint4 v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        if (i0 + u * kSelectThreads < n4) v[u] = src4[i0 + u * kSelectThreads];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int q = i0 + u * kSelectThreads;
+                        if (q < n4) {
+                            const int k = (2 * q) / M, i = 2 * q - k * M;
+                            uint2* dst = reinterpret_cast<uint2*>(s.sl + sl_at(k, i, SL));
+                            dst[0] = make_uint2(v[u].x, v[u].y);
+                            dst[1] = make_uint2(v[u].z, v[u].w);
+                        }
+                    }
+                }
+            } else {
+                const uint32_t* src32 = reinterpret_cast<const uint32_t*>(src);
+                for (int i = tid; i < K * M; i += kSelectThreads) {
+                    ShortEntry e;
+                    if (!coherent) {
+                        e = src[i];
+                    } else {
+                        e.lp = bits_f32(load_shared(src32 + 2 * i, true));
+                        e.token = static_cast<int32_t>(load_shared(src32 + 2 * i + 1, true));
+                    }
+                    s.sl[SL == M ? i : sl_at(i / M, i % M, SL)] = e;
+                }
             }
         }
         __syncthreads();
         if (p.use_tau) {
-            // The first K entries of a shortlist are real candidates with raw
-            // >= fl(p + lp_K) (raw is monotone in lp): at least K expanded
-            // candidates reach the largest such value over the rows.
+            // Lower bounds of the K-th best expanded raw (unconstrained: raw =
+            // fl(p + lp), monotone in lp; every beam expanded has the same
+            // length, so this step's shortlisted candidates rank by raw).
+            // (a) The first K entries of a shortlist are real candidates with
+            // raw >= fl(p + lp_K): at least K reach the largest such value.
             if (tid < 64) {
                 float best = -kInf;
                 for (int k = tid; k < K; k += 64)
-                    if (s.rcount[k] >= K) best = fmaxf(best, s.raw[k] + s.sl[k * M + (K - 1)].lp);
+                    if (s.rcount[k] >= K) best = fmaxf(best, s.raw[k] + s.sl[sl_at(k, K - 1, SL)].lp);
                 best = wave_max(best);
                 if (tid == 0) st.tau = best;
+            }
+            // (b) Wide beams: the K-th largest raw among the first kTauHead
+            // entries of every row: at least K real candidates reach it.
+            // Ranked as 64-bit keys (ordered value bits, then the lower index
+            // first), two per broadcast read.
+            const int nv = K * kTauHead;  // <= 128 (K <= 64 with a shortlist), even
+            uint2* vk = reinterpret_cast<uint2*>(s.key);
+            float v = -kInf;
+            if (K >= kWideBeam && tid < nv) {
+                const int k = tid / kTauHead, i = tid - k * kTauHead;
+                v = i < s.rcount[k] ? s.raw[k] + s.sl[sl_at(k, i, SL)].lp : -kInf;
+                vk[tid] = make_uint2(0xffffffffu - static_cast<uint32_t>(tid), ordered_key(v));
+            }
+            if (K >= kWideBeam) __syncthreads();  // (a) and the keys are in
+            if (K >= kWideBeam && tid < nv) {
+                const uint32_t mlo = 0xffffffffu - static_cast<uint32_t>(tid), mhi = ordered_key(v);
+                const uint4* w4 = reinterpret_cast<const uint4*>(vk);
+                int rank = 0;
+                int j2 = 0;
+                for (; j2 + 4 <= nv / 2; j2 += 4) {  // four reads in flight
+                    uint4 w[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) w[u] = w4[j2 + u];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        count_above64(rank, mlo, mhi, w[u].x, w[u].y);
+                        count_above64(rank, mlo, mhi, w[u].z, w[u].w);
+                    }
+                }
+                for (; j2 < nv / 2; ++j2) {
+                    const uint4 w = w4[j2];
+                    count_above64(rank, mlo, mhi, w.x, w.y);
+                    count_above64(rank, mlo, mhi, w.z, w.w);
+                }
+                if (rank == K - 1 && v > st.tau) st.tau = v;
             }
             __syncthreads();
         }
@@ -520,8 +615,49 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         }
         end_round(s, st, K, L.sort_cap);
 
-        // Shortlisted candidates.
-        if (M > 0) {
+        // Shortlisted candidates. Unconstrained wide beams: few reach tau, and
+        // when they fit the collector beside what it holds, they are offered
+        // in one pass without compaction rounds.
+        // A shortlist is sorted (log-prob desc), so the entries reaching tau
+        // are a prefix of it: one thread per beam measures its prefix, then
+        // offers it.
+        bool one_pass = false;
+        if (M > 0 && p.use_tau && K >= kWideBeam) {
+            // (K <= 64 with a shortlist: one wavefront, one lane per beam; the
+            // prefixes go to consecutive collector slots by a lane scan)
+            if (tid < 64) {
+                const float tau = st.tau;
+                const int k = tid;
+                int n = 0;
+                float praw = -kInf;
+                if (k < K) {
+                    praw = s.raw[k];
+                    const int cnt = s.rcount[k];
+                    while (n < cnt && !(praw + s.sl[sl_at(k, n, SL)].lp < tau)) ++n;
+                }
+                int incl = n;
+                for (int off = 1; off < 64; off <<= 1) {
+                    const int up = __shfl_up(incl, off);
+                    if (tid >= off) incl += up;
+                }
+                const int total = __shfl(incl, 63);
+                const int base = st.count;
+                if (base + total <= L.sort_cap && n > 0) {
+                    const int new_len = s.len[k] + 1;
+                    const float inv = inv_of(s, pen_len, new_len, p.alpha);
+                    for (int i = 0; i < n; ++i) {
+                        const ShortEntry e = s.sl[sl_at(k, i, SL)];
+                        const float raw = praw + e.lp;
+                        s.buf[base + incl - n + i] = Cand{raw * inv, raw, k, e.token, new_len, 1};
+                    }
+                }
+                if (tid == 0) st.rcount = base + total <= L.sort_cap ? base + total : -1;
+            }
+            __syncthreads();
+            one_pass = st.rcount >= 0;
+            if (one_pass && tid == 0) st.count = st.rcount;
+        }
+        if (M > 0 && !one_pass) {
             const float tau = st.tau;
             for (int base = 0; base < K * M; base += kSelectThreads) {
                 const int item = base + tid;
@@ -529,7 +665,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                     const int k = item / M;
                     const int i = item - k * M;
                     if (i < s.rcount[k]) {
-                        const ShortEntry e = s.sl[item];
+                        const ShortEntry e = s.sl[sl_at(k, i, SL)];
                         const float praw = s.raw[k];
                         if (!(praw + e.lp < tau)) {
                             const int new_len = s.len[k] + 1;
@@ -680,7 +816,7 @@ SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool st
     L.off_i32 = off;
     off = align(off + sizeof(int32_t) * 10 * static_cast<size_t>(K));
     L.off_sl = off;
-    off = align(off + sizeof(ShortEntry) * static_cast<size_t>(K) * static_cast<size_t>(M));
+    off = align(off + sizeof(ShortEntry) * static_cast<size_t>(K) * static_cast<size_t>(K >= kWideBeam ? M + 1 : M));
     const size_t prefix_bytes = sizeof(int32_t) * 2 * static_cast<size_t>(K) * static_cast<size_t>(prefix_cap);
     const size_t blk_bytes = sizeof(int32_t) * static_cast<size_t>(K) * static_cast<size_t>(prefix_cap);
     const size_t budget = 150 * 1024;
