@@ -19,6 +19,7 @@
 
 #include "dbs_cuda.h"
 #include "engine.hpp"
+#include "row_helpers.hpp"
 
 namespace dbs_hip {
 
@@ -101,10 +102,18 @@ __device__ __forceinline__ void store_out(void* out, int64_t i, float v, bool ac
     }
 }
 
-// Stores zeros over [0, V) of a row (fresh mode), 4 elements per thread per pass.
+// Stores zeros over [0, V) of a row (fresh mode): 16-byte stores when the row
+// is 16-byte aligned and whole 16-byte blocks long.
 template <int OT>
 __device__ __forceinline__ void zero_row(void* out, int64_t row_off, int V) {
     const int tid = static_cast<int>(threadIdx.x);
+    constexpr int per16 = OT == 0 ? 4 : 8;
+    char* row = static_cast<char*>(out) + row_off * (OT == 0 ? 4 : 2);
+    if (V % per16 == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {
+        uint4* r4 = reinterpret_cast<uint4*>(row);
+        for (int c = tid; c < V / per16; c += kDenseThreads) r4[c] = make_uint4(0u, 0u, 0u, 0u);
+        return;
+    }
     for (int v = tid; v < V; v += kDenseThreads) {
         if constexpr (OT == 0) {
             static_cast<float*>(out)[row_off + v] = 0.0f;
@@ -197,6 +206,67 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardP
     const float lse = p.row_lse[r];
     const size_t esz = DT == 0 ? 4 : 2;
     const void* x = static_cast<const char*>(p.logits) + static_cast<size_t>(r) * static_cast<size_t>(V) * esz;
+    if constexpr (DT == 2 && OT != 0) {
+        // bfloat16 logits into a 16-bit gradient: exp(fl(x - lse)) is a
+        // function of x's pattern for the row, so a per-row table of the exact
+        // terms (as in the row pass; table_fits) replaces the Cephes
+        // evaluation, and 16-byte loads and stores carry 8 entries. The
+        // entries' tokens are written after the rest of the row.
+        int ulo = 0;
+        const bool vec = (V & 7) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(p.out) & 15) == 0;
+        if (vec && !accumulate && table_fits(lse, ulo)) {
+            __shared__ float lut[2 * kLutHalf];
+            const uint32_t mp = f32_bits(lse) >> 16;  // largest bfloat16 <= lse (no x exceeds it)
+            for (int i = tid; i < 2 * kLutHalf; i += kDenseThreads) {
+                const bool neg = i >= kLutHalf;
+                const int k = i & (kLutHalf - 1);
+                float term = 0.0f;
+                if (k == 0) {
+                    term = exp_nonpositive(-lse);
+                } else {
+                    const int u = ulo - 1 + k;
+                    if (u < 0x7f80 && (neg || u <= static_cast<int>(mp)))
+                        term = exp_nonpositive(bf16_to_f32(static_cast<uint16_t>((neg ? 0x8000 : 0) | u)) - lse);
+                }
+                lut[i] = term;
+            }
+            __syncthreads();
+            const uint32_t base2 = static_cast<uint32_t>(ulo - 1) * 0x10001u;
+            auto terms = [&](uint32_t R, float& lo, float& hi) {
+                uint32_t idx = pk_sub_sat_u16(R & 0x7fff7fffu, base2);
+                idx = pk_min_u16(idx, 0x0fff0fffu);
+                idx |= (R >> 3) & 0x10001000u;
+                lo = lut[idx & 0xffffu];
+                hi = lut[idx >> 16];
+            };
+            const uint4* x4 = static_cast<const uint4*>(x);
+            uint4* o4 = reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + row_off);
+            auto out16 = [&](float g) -> uint32_t {
+                return OT == 1 ? f32_to_f16_rne(0.0f + g) : f32_to_bf16_rne(0.0f + g);
+            };
+            for (int c = tid; c < V / 8; c += kDenseThreads) {
+                const uint4 q = x4[c];
+                const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+                uint32_t o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float lo, hi;
+                    terms(w[e], lo, hi);
+                    o[e] = out16(0.0f - lo * S) | (out16(0.0f - hi * S) << 16);
+                }
+                o4[c] = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+            __syncthreads();  // the entries' tokens land after the rest of the row
+            for (int i = tid; i < ne; i += kDenseThreads) {
+                const int v = e_tok[i];
+                float lo, hi;
+                terms(static_cast<const uint16_t*>(x)[v], lo, hi);
+                static_cast<uint16_t*>(p.out)[row_off + v] = static_cast<uint16_t>(out16(e_val[i] - lo * S));
+            }
+            return;
+        }
+    }
     for (int v = tid; v < V; v += kDenseThreads) {
         const float xv = load_logit<DT>(x, v);
         const float pv = softmax_probability(xv, lse);

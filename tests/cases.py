@@ -31,7 +31,7 @@ def log_softmax(x: np.ndarray) -> np.ndarray:
 
 
 def make_case(seed: int, *, big: bool = False, allow_invalid: bool = True, dtypes=None, vocabs=None,
-              scales=None) -> dict:
+              scales=None, logits=None) -> dict:
     rng = np.random.default_rng(seed)
     B = int(rng.integers(1, 5))
     T = int(rng.integers(1, 9))
@@ -41,6 +41,8 @@ def make_case(seed: int, *, big: bool = False, allow_invalid: bool = True, dtype
     V = int(rng.choice(vocab_pool))
     dtype = str(rng.choice(dtypes if dtypes is not None else ["f32", "f16", "bf16"]))
     from_logits = bool(rng.integers(0, 2))
+    if logits is not None:
+        from_logits = bool(logits)
     scale = float(rng.choice(scales if scales is not None else [0.5, 2.0, 3.0]))
     x = rng.normal(0.0, scale, size=(B, T, K, V)).astype(np.float32)
     if not from_logits:

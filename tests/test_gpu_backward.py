@@ -55,6 +55,24 @@ def test_backward_matches_oracle(hip, oracle, seed):
         assert np.array_equal(dense16, to_bits(want, out_type)), out_type
 
 
+# bfloat16 logits with whole 16-byte blocks per row take the table-driven,
+# vectorized dense gradient (rows whose logsumexp is below 1 fall back to the
+# Cephes evaluation); every output type against the oracle, bit for bit.
+@pytest.mark.parametrize("seed", range(0, 12))
+def test_dense_gradient_bf16_logits(hip, oracle, seed):
+    case = make_case(2600 + seed, allow_invalid=False, dtypes=["bf16"], vocabs=[8, 1000, 4104, 8200],
+                     scales=[0.05, 0.5, 3.0, 8.0], logits=True)
+    rng = np.random.default_rng(seed + 100)
+    tr, grads, kw = _trace_and_grads(oracle, case, rng)
+    want = oracle.backward(tr, case["V"], alpha=kw["alpha"], steps=kw["steps"], logits=case["xin"],
+                           logits_dtype="bf16", row_lse=tr["row_lse"], **grads)
+    for out_type in ("bf16", "f16", "f32"):
+        got = hip.backward(tr, case["V"], alpha=kw["alpha"], steps=kw["steps"], logits=case["xin"], dtype="bf16",
+                           row_lse=tr["row_lse"], mode="dense", out_type=out_type, **grads)
+        expect = _bits(want) if out_type == "f32" else to_bits(want, out_type)
+        assert np.array_equal(_bits(got), expect), f"seed {seed} {out_type} V{case['V']}"
+
+
 def test_backward_accumulates(hip, oracle):
     case = make_case(77, allow_invalid=False)
     rng = np.random.default_rng(7)
