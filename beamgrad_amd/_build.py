@@ -35,7 +35,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-LIB_SOURCES = ["csrc/api.hip", "csrc/decode.hip", "csrc/row_pass.hip", "csrc/row_resident.hip", "csrc/row_pipe.hip", "csrc/select.hip", "csrc/backward.hip"]
+LIB_SOURCES = ["csrc/api.hip", "csrc/decode.hip", "csrc/row_pass.hip", "csrc/row_resident.hip", "csrc/row_pipe.hip", "csrc/row_logprob.hip", "csrc/select.hip", "csrc/backward.hip"]
 
 
 def lib_path() -> str:

@@ -139,6 +139,8 @@ hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream);
 bool row_resident_eligible(const DecodeParams& p);
 hipError_t launch_row_resident(const DecodeParams& p, int64_t rows, hipStream_t stream);
 bool row_pipe_eligible(const DecodeParams& p);
+bool row_logprob_eligible(const DecodeParams& p);
+hipError_t launch_row_logprob(const DecodeParams& p, int64_t rows, hipStream_t stream);
 extern std::atomic<int> g_row_pass_kind;  // dbs_hip_set_row_pass
 hipError_t launch_row_pipe(const DecodeParams& p, int64_t rows, hipStream_t stream);
 hipError_t launch_select(const DecodeParams& p, const SelectLayout& L, hipStream_t stream);

@@ -151,6 +151,7 @@ hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream) {
     const bool vec = (p.V % 4 == 0) && (reinterpret_cast<uintptr_t>(p.x) % (4 * esz) == 0);
     KernelTimer timer(kKindRowPass, stream);
     const int kind = g_row_pass_kind.load(std::memory_order_relaxed);
+    if ((kind == -1 || kind == 3) && row_logprob_eligible(p)) return launch_row_logprob(p, rows, stream);
     if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return launch_row_resident(p, rows, stream);
     if ((kind == -1 || kind == 2) && row_pipe_eligible(p)) return launch_row_pipe(p, rows, stream);
     const dim3 grid(static_cast<unsigned>(rows));

@@ -81,9 +81,11 @@ DBS_CUDA_EXPORT int dbs_hip_profile_read(int kernel, double* total_ms, int64_t* 
 
 /* Row-pass kernel choice for tests and measurements (no counterpart in the
  * reference; every choice gives the same results): -1 automatic (the
- * default: the resident 16-bit kernel where it applies, else the pipelined
+ * default: for log-prob rows the one-read log-prob kernel where it applies;
+ * else the resident 16-bit kernel where it applies, else the pipelined
  * 16-bit kernel, else the two-pass kernel), 0 two-pass, 1 resident 16-bit
- * (V % 8 == 0, 16-byte aligned rows), 2 pipelined 16-bit (any V).
+ * (V % 8 == 0, 16-byte aligned rows), 2 pipelined 16-bit (any V), 3 one-read
+ * log-prob rows (any dtype, rows up to 163824 bytes).
  * A kernel that does not apply to a decode falls back to the two-pass one.
  * Returns the previous choice, or -2 for an invalid argument. */
 DBS_CUDA_EXPORT int dbs_hip_set_row_pass(int kind);

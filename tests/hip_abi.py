@@ -32,9 +32,15 @@ class HipEngine:
     # ------------------------------------------------------------------
     def decode(self, xin: np.ndarray, dtype: str, *, from_logits=False, eos_token=-1, extra_eos=(), min_length=0,
                alpha=0.0, no_repeat_ngram_size=0, repetition_penalty=1.0, steps=None, banned=None,
-               banned_per_example=None, use_ex3: bool | None = None, workspace: bool = True) -> dict:
+               banned_per_example=None, use_ex3: bool | None = None, workspace: bool = True,
+               x_offset: int = 0) -> dict:
         B, T, K, V = xin.shape
         x = _dev(xin.view(np.int16) if xin.dtype == np.uint16 else xin)
+        if x_offset:
+            # the rows at an element offset from the allocation (any alignment)
+            flat = torch.empty(x.numel() + x_offset, dtype=x.dtype, device=x.device)
+            flat[x_offset:] = x.reshape(-1)
+            x = flat[x_offset:].view(B, T, K, V)
         dev = x.device
         f32 = dict(dtype=torch.float32, device=dev)
         i32 = dict(dtype=torch.int32, device=dev)

@@ -108,6 +108,22 @@ def test_decode_16bit_row_passes(hip, oracle, row_pass, seed, kind):
     _check(hip, oracle, case)
 
 
+# Log-prob rows of every dtype take the one-read kernel where the row fits on
+# chip (the default) and the two-pass kernel otherwise; both run on the same
+# inputs, with the rows at every alignment (an element offset of 0-4 from the
+# allocation), vocabularies at the block and on-chip limits (fp32 rows up to
+# 40956 elements, 16-bit up to 81912), and one past them.
+_LOGPROB_VOCABS = [2, 7, 8, 255, 256, 257, 1000, 1021, 4097, 8192, 32000, 40956, 40957, 50257, 81912, 81913]
+
+
+@pytest.mark.parametrize("kind", [3, 0])
+@pytest.mark.parametrize("seed", range(0, 24))
+def test_decode_logprob_row_passes(hip, oracle, row_pass, seed, kind):
+    row_pass(kind)
+    case = make_case(9700 + seed, vocabs=_LOGPROB_VOCABS, logits=False)
+    _check(hip, oracle, case, x_offset=seed % 5)
+
+
 @pytest.mark.parametrize("seed", range(0, 6))
 def test_decode_16bit_wide_beams(hip, oracle, seed):
     """K > 64: no shortlist (every read row is rescanned); the row pass still
