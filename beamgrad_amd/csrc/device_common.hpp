@@ -193,7 +193,9 @@ __device__ __forceinline__ uint64_t survivor_key(float x, int v) {
            static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(v));
 }
 
-// One wavefront: sorts the n row survivors (finite x >= theta) kept in LDS
+constexpr int kRankSurvivors = 128;  // up to this many survivors are placed by rank, else sorted
+
+// One wavefront: orders the n row survivors (finite x >= theta) kept in LDS
 // and writes the row's shortlist (the best M allowed tokens by value desc,
 // token asc, as log-probs) and RowInfo: the bound on every allowed token left
 // out is the (M+1)-th allowed survivor, else theta. FILTER: the survivors may
@@ -228,37 +230,72 @@ __device__ void finish_row_wave(const DecodeParams& p, int64_t r, float lse, flo
                     dropped += __popcll(__ballot(drop));
                 }
             }
-            for (int i = n + lane; i < np; i += 64) s_key[i] = 0;
-            wave_sync();
-            for (int kk = 2; kk <= np; kk <<= 1) {
-                for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-                    for (int i = lane; i < np; i += 64) {
-                        const int partner = i ^ jj;
-                        if (partner > i) {
-                            const bool desc = (i & kk) == 0;
-                            const uint64_t ki = s_key[i], kp = s_key[partner];
-                            if (desc ? (kp > ki) : (ki > kp)) {
-                                s_key[i] = kp;
-                                s_key[partner] = ki;
-                                const float xi = s_x[i];
-                                s_x[i] = s_x[partner];
-                                s_x[partner] = xi;
-                            }
-                        }
-                    }
-                    wave_sync();
-                }
-            }
             n -= dropped;
             const int cnt = n < M ? n : M;
             ShortEntry* out = p.shortlist + r * M;
-            for (int i = lane; i < cnt; i += 64) {
-                const float x = s_x[i];
-                const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(s_key[i] & 0xffffffffu));
-                store_shared(reinterpret_cast<uint32_t*>(&out[i].lp), f32_bits(LOGITS ? x - lse : x), coherent);
-                store_shared(reinterpret_cast<uint32_t*>(&out[i].token), static_cast<uint32_t>(tok), coherent);
+            float bx = theta;
+            if (n + dropped <= kRankSurvivors) {
+                // Few survivors: each lane ranks its own by counting the keys
+                // above it (keys are distinct; dropped ones are 0) and writes
+                // it in place; rank M is the bound.
+                const int nall = n + dropped;
+                wave_sync();
+                int bound_lane = -1;
+                float bound_x = -kInf;
+                for (int i0 = 0; i0 < nall; i0 += 64) {
+                    const int i = i0 + lane;
+                    const uint64_t ki = i < nall ? s_key[i] : 0;
+                    int rank = 0;
+                    int jj = 0;
+                    for (; jj + 2 <= nall; jj += 2) {
+                        const uint64_t k0 = s_key[jj], k1 = s_key[jj + 1];
+                        rank += static_cast<int>(k0 > ki) + static_cast<int>(k1 > ki);
+                    }
+                    if (jj < nall) rank += static_cast<int>(s_key[jj] > ki);
+                    const bool live = i < nall && ki != 0;
+                    const float x = live ? s_x[i] : 0.0f;
+                    if (live && rank < M) {
+                        const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(ki & 0xffffffffu));
+                        store_shared(reinterpret_cast<uint32_t*>(&out[rank].lp), f32_bits(LOGITS ? x - lse : x), coherent);
+                        store_shared(reinterpret_cast<uint32_t*>(&out[rank].token), static_cast<uint32_t>(tok), coherent);
+                    }
+                    const uint64_t at_m = __ballot(live && rank == M);
+                    if (at_m != 0) {
+                        bound_lane = __ffsll(static_cast<long long>(at_m)) - 1;
+                        bound_x = __shfl(x, bound_lane);
+                    }
+                }
+                if (n > M) bx = bound_x;
+            } else {
+                for (int i = n + dropped + lane; i < np; i += 64) s_key[i] = 0;
+                wave_sync();
+                for (int kk = 2; kk <= np; kk <<= 1) {
+                    for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+                        for (int i = lane; i < np; i += 64) {
+                            const int partner = i ^ jj;
+                            if (partner > i) {
+                                const bool desc = (i & kk) == 0;
+                                const uint64_t ki = s_key[i], kp = s_key[partner];
+                                if (desc ? (kp > ki) : (ki > kp)) {
+                                    s_key[i] = kp;
+                                    s_key[partner] = ki;
+                                    const float xi = s_x[i];
+                                    s_x[i] = s_x[partner];
+                                    s_x[partner] = xi;
+                                }
+                            }
+                        }
+                        wave_sync();
+                    }
+                }
+                for (int i = lane; i < cnt; i += 64) {
+                    const float x = s_x[i];
+                    const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(s_key[i] & 0xffffffffu));
+                    store_shared(reinterpret_cast<uint32_t*>(&out[i].lp), f32_bits(LOGITS ? x - lse : x), coherent);
+                    store_shared(reinterpret_cast<uint32_t*>(&out[i].token), static_cast<uint32_t>(tok), coherent);
+                }
+                if (n > M) bx = s_x[M];
             }
-            const float bx = n > M ? s_x[M] : theta;
             info.count = cnt;
             info.bound = (bx > -kInf) ? (LOGITS ? bx - lse : bx) : -kInf;
         }
