@@ -57,29 +57,24 @@ static_assert(kResLds <= 160 * 1024, "LDS of the resident row pass");
 // with two transposing reads: within each 16-lane group, lane i receives
 // element i % 4 of the 8 bytes addressed by lanes 4 k + i / 4 (k = 0..3), so
 // lane L = 16 G + a addresses (stripe 4 h + a / 4, lanes 16 G + 4 (a % 4) ..).
-// The write, the reads and their wait are one asm block (the LDS serves a
-// wavefront's operations in order).
+// The write and the reads go through the compiler's LDS operations, so the
+// next chunk's transpose can start before this one's results are used.
 __device__ __forceinline__ void transpose_chunk(unsigned char* slot, int L, uint32_t x0, uint32_t x1, uint32_t x2,
                                                 uint32_t x3, uint32_t (&R)[4]) {
+    typedef short v4i16 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) unsigned char lds_u8;
     const int G = L >> 4, a = L & 15;
-    const uint32_t base = static_cast<uint32_t>(
-        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char*)slot));
-    const uint32_t waddr = base + 16 * L;
-    const uint32_t raddr = base + 128 * (a >> 2) + 32 * G + 8 * (a & 3);
-    const v4u32 w = {x0, x1, x2, x3};
-    v2u32 t0, t1;
-    asm volatile(
-        "ds_write_b128 %2, %3\n\t"
-        "ds_read_b64_tr_b16 %0, %4\n\t"
-        "ds_read_b64_tr_b16 %1, %4 offset:512\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(t0), "=&v"(t1)
-        : "v"(waddr), "v"(w), "v"(raddr)
-        : "memory");
-    R[0] = t0.x;
-    R[1] = t0.y;
-    R[2] = t1.x;
-    R[3] = t1.y;
+    lds_u8* base = (lds_u8*)slot;
+    *reinterpret_cast<__attribute__((address_space(3))) v4u32*>(base + 16 * L) = v4u32{x0, x1, x2, x3};
+    lds_u8* rd = base + 128 * (a >> 2) + 32 * G + 8 * (a & 3);
+    const v4i16 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4i16*>(rd));
+    const v4i16 t1 =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4i16*>(rd + 512));
+    const v2u32 u0 = __builtin_bit_cast(v2u32, t0), u1 = __builtin_bit_cast(v2u32, t1);
+    R[0] = u0.x;
+    R[1] = u0.y;
+    R[2] = u1.x;
+    R[3] = u1.y;
 }
 
 template <int DT, bool LOGITS>
@@ -199,8 +194,8 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
         // Opaque copies per row: everything the unrolled load derives from
         // them is recomputed per row instead of being hoisted out of the row
         // loop into (spilled) registers.
-        int nch_r = nch, V_r = V, jr = j, lr = l;
-        asm volatile("" : "+s"(nch_r), "+s"(V_r));
+        int V_r = V, jr = j, lr = l;
+        asm volatile("" : "+s"(V_r));
         asm volatile("" : "+v"(jr), "+v"(lr));
 
         // ---- load the row's segment into registers, transposed to lanes ----
@@ -234,33 +229,35 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             reg[4 * c + 3] = q.w;
         }
         if (wave == 0 && pend) finish_pending();
+        // Software-pipelined: chunk c + 1's transpose is issued before chunk
+        // c's results are used. Chunks past the segment (zeros from the view)
+        // and elements past the row become padding.
+        const int seg_end = min(V_r, 256 * (s_begin + per));  // elements of the segment end here
+        uint32_t Tn[4];
+        transpose_chunk(stage, lr, reg[0], reg[1], reg[2], reg[3], Tn);
 #pragma unroll
         for (int c = 0; c < kResChunks; ++c) {
-            if (c < nch_r) {
-                uint32_t R4[4];
-                transpose_chunk(stage, lr, reg[4 * c], reg[4 * c + 1], reg[4 * c + 2], reg[4 * c + 3], R4);
-                const int sb = s_begin + 8 * c;
-                if (256 * (sb + 8) > V_r) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const bool lo_out = 256 * (sb + 2 * q) + jr >= V_r;
-                        const bool hi_out = 256 * (sb + 2 * q + 1) + jr >= V_r;
-                        R4[q] = (lo_out ? kPad : (R4[q] & 0xffffu)) | (hi_out ? (kPad << 16) : (R4[q] & 0xffff0000u));
-                    }
-                }
+            uint32_t R4[4] = {Tn[0], Tn[1], Tn[2], Tn[3]};
+            if (c + 1 < kResChunks)
+                transpose_chunk(stage, lr, reg[4 * c + 4], reg[4 * c + 5], reg[4 * c + 6], reg[4 * c + 7], Tn);
+            const int sb = s_begin + 8 * c;
+            if (256 * (sb + 8) > seg_end) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const int k = 4 * c + q;
-                    const uint32_t R = R4[q];
-                    reg[k] = R;
-                    const int g = k / kResGroupRegs;
-                    gmax[g] = pk_max_i16(gmax[g], R);
-                    gmin[g] = pk_min_i16(gmin[g], R);
-                    umax = pk_max_u16(umax, R);
+                    const bool lo_out = 256 * (sb + 2 * q) + jr >= seg_end;
+                    const bool hi_out = 256 * (sb + 2 * q + 1) + jr >= seg_end;
+                    R4[q] = (lo_out ? kPad : (R4[q] & 0xffffu)) | (hi_out ? (kPad << 16) : (R4[q] & 0xffff0000u));
                 }
-            } else {
+            }
 #pragma unroll
-                for (int q = 0; q < 4; ++q) reg[4 * c + q] = kPad | (kPad << 16);
+            for (int q = 0; q < 4; ++q) {
+                const int k = 4 * c + q;
+                const uint32_t R = R4[q];
+                reg[k] = R;
+                const int g = k / kResGroupRegs;
+                gmax[g] = pk_max_i16(gmax[g], R);
+                gmin[g] = pk_min_i16(gmin[g], R);
+                umax = pk_max_u16(umax, R);
             }
         }
 
