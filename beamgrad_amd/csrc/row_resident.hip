@@ -181,44 +181,22 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
     } else {
         r = next_read_row(blockIdx.x, b, new_len);
     }
-    while (r < rows) {
-        int bn = 0, lenn = 0;
-        int64_t rn = rows;
-        if (tickets) {
-            if (tid == 0) publish_next_row(p, rows, q_next, s_rows[par ^ 1]);
-        } else {
-            rn = next_read_row(r + gridDim.x, bn, lenn);
-        }
-        const bool mask_eos = new_len < p.min_length;
-        const uint16_t* row = static_cast<const uint16_t*>(p.x) + r * V;
-        // Opaque copies per row: everything the unrolled load derives from
-        // them is recomputed per row instead of being hoisted out of the row
-        // loop into (spilled) registers.
-        int V_r = V, jr = j, lr = l;
+    // Chunk c (8 stripes x this wavefront's 64 lanes): lane l loads the 16
+    // bytes of stripe 8c + l/8, lanes 64 wv + 8 (l % 8) .. into the four
+    // registers the chunk will occupy. Every chunk is in flight at once; the
+    // buffer view covers exactly the segment's stripes inside the row, so
+    // groups past it read zeros without touching memory, and are replaced by
+    // padding; a row index past the last gives an empty view. Each segment
+    // loads its part of the next row as soon as its chain has passed its
+    // registers: segment 0 while segment 1 folds, segment 1 at the row's end.
+    uint32_t reg[kResRegs];
+    auto issue_loads = [&](int64_t rr) {
+        int V_r = V;
         asm volatile("" : "+s"(V_r));
-        asm volatile("" : "+v"(jr), "+v"(lr));
-
-        // ---- load the row's segment into registers, transposed to lanes ----
-        // registers past the segment's chunks hold -inf pairs (term 0, never
-        // a survivor), so the chain below runs over all of them unguarded
-        uint32_t reg[kResRegs];
-        uint32_t gmax[kResGroups], gmin[kResGroups];
-        uint32_t umax = 0;
-#pragma unroll
-        for (int g = 0; g < kResGroups; ++g) {
-            gmax[g] = 0x80008000u;
-            gmin[g] = kPad | (kPad << 16);
-        }
-        // Chunk c (8 stripes x this wavefront's 64 lanes): lane l loads the 16
-        // bytes of stripe 8c + l/8, lanes 64 wv + 8 (l % 8) .. into the four
-        // registers the chunk will occupy. Every chunk is in flight at once;
-        // the buffer view covers exactly the segment's stripes inside the
-        // row, so groups past it read zeros without touching memory, and are
-        // replaced by padding. Consuming a chunk writes its 1 KB to the
-        // wavefront's staging slot and reads it back transposed, each lane its
-        // own lane's 8 stripes.
-        const int seg_bytes = max(0, 2 * min(V_r, 256 * (s_begin + per)) - 512 * s_begin);
-        const __amdgpu_buffer_rsrc_t rs = row_buffer(row + 256 * s_begin, seg_bytes);
+        const bool any = rr < rows;
+        const uint16_t* rrow = static_cast<const uint16_t*>(p.x) + (any ? rr : 0) * V_r;
+        const int seg_bytes = any ? max(0, 2 * min(V_r, 256 * (s_begin + per)) - 512 * s_begin) : 0;
+        const __amdgpu_buffer_rsrc_t rs = row_buffer(rrow + 256 * s_begin, seg_bytes);
         const int voff = lane_offset();
 #pragma unroll
         for (int c = 0; c < kResChunks; ++c) {
@@ -228,7 +206,42 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             reg[4 * c + 2] = q.z;
             reg[4 * c + 3] = q.w;
         }
-        if (wave == 0 && pend) finish_pending();
+    };
+    if (r < rows) issue_loads(r);
+    while (r < rows) {
+        int bn = 0, lenn = 0;
+        int64_t rn = rows;
+        if (tickets) {
+            if (tid == 0) publish_next_row(p, rows, q_next, s_rows[par ^ 1]);
+        } else {
+            rn = next_read_row(r + gridDim.x, bn, lenn);
+        }
+        // the next row (with tickets: published before this row's first barrier)
+        auto next_row = [&]() -> int64_t {
+            if (!tickets) return rn;
+            int bt = 0, lt = 0;
+            return read_row_slot(s_rows[par ^ 1], bt, lt);
+        };
+        const bool mask_eos = new_len < p.min_length;
+        const uint16_t* row = static_cast<const uint16_t*>(p.x) + r * V;
+        // Opaque copies per row: everything the unrolled load derives from
+        // them is recomputed per row instead of being hoisted out of the row
+        // loop into (spilled) registers.
+        int V_r = V, jr = j, lr = l;
+        asm volatile("" : "+s"(V_r));
+        asm volatile("" : "+v"(jr), "+v"(lr));
+
+        // ---- the row's segment in registers (loaded during the previous
+        // row, see issue_loads), transposed to lanes ----
+        // registers past the segment's chunks hold -inf pairs (term 0, never
+        // a survivor), so the chain below runs over all of them unguarded
+        uint32_t gmax[kResGroups], gmin[kResGroups];
+        uint32_t umax = 0;
+#pragma unroll
+        for (int g = 0; g < kResGroups; ++g) {
+            gmax[g] = 0x80008000u;
+            gmin[g] = kPad | (kPad << 16);
+        }
         // Software-pipelined: chunk c + 1's transpose is issued before chunk
         // c's results are used. Chunks past the segment (zeros from the view)
         // and elements past the row become padding.
@@ -260,6 +273,9 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
                 umax = pk_max_u16(umax, R);
             }
         }
+        // (wavefront 0 finishes the previous row now; segment 1's part of this
+        // row may still be arriving)
+        if (wave == 0 && pend) finish_pending();
 
         // ---- row maximum, flag, group keys; the key histogram for theta ----
         // (keys: key16 of the largest pattern of a group, per half the largest
@@ -475,6 +491,7 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             s_hist2[tid] = 0;  // every wavefront has read its b2
             push_hits();
         }
+        issue_loads(next_row());
         lds_barrier();
 
         if (wave == 0) {
