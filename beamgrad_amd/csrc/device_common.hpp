@@ -247,11 +247,14 @@ __device__ void finish_row_wave(const DecodeParams& p, int64_t r, float lse, flo
                     const uint64_t ki = i < nall ? s_key[i] : 0;
                     int rank = 0;
                     int jj = 0;
-                    for (; jj + 2 <= nall; jj += 2) {
-                        const uint64_t k0 = s_key[jj], k1 = s_key[jj + 1];
-                        rank += static_cast<int>(k0 > ki) + static_cast<int>(k1 > ki);
+                    for (; jj + 8 <= nall; jj += 8) {  // eight keys in flight
+                        uint64_t kk[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) kk[u] = s_key[jj + u];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) rank += static_cast<int>(kk[u] > ki);
                     }
-                    if (jj < nall) rank += static_cast<int>(s_key[jj] > ki);
+                    for (; jj < nall; ++jj) rank += static_cast<int>(s_key[jj] > ki);
                     const bool live = i < nall && ki != 0;
                     const float x = live ? s_x[i] : 0.0f;
                     if (live && rank < M) {

@@ -190,22 +190,26 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
     // loads its part of the next row as soon as its chain has passed its
     // registers: segment 0 while segment 1 folds, segment 1 at the row's end.
     uint32_t reg[kResRegs];
-    auto issue_loads = [&](int64_t rr) {
+    auto row_view = [&](int64_t rr) {
         int V_r = V;
         asm volatile("" : "+s"(V_r));
         const bool any = rr < rows;
         const uint16_t* rrow = static_cast<const uint16_t*>(p.x) + (any ? rr : 0) * V_r;
         const int seg_bytes = any ? max(0, 2 * min(V_r, 256 * (s_begin + per)) - 512 * s_begin) : 0;
-        const __amdgpu_buffer_rsrc_t rs = row_buffer(rrow + 256 * s_begin, seg_bytes);
+        return row_buffer(rrow + 256 * s_begin, seg_bytes);
+    };
+    auto issue_chunk = [&](const __amdgpu_buffer_rsrc_t& rs, int voff, int c) {
+        const v4u32 q = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 4096 * c, 0);
+        reg[4 * c] = q.x;
+        reg[4 * c + 1] = q.y;
+        reg[4 * c + 2] = q.z;
+        reg[4 * c + 3] = q.w;
+    };
+    auto issue_loads = [&](int64_t rr) {
+        const __amdgpu_buffer_rsrc_t rs = row_view(rr);
         const int voff = lane_offset();
 #pragma unroll
-        for (int c = 0; c < kResChunks; ++c) {
-            const v4u32 q = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 4096 * c, 0);
-            reg[4 * c] = q.x;
-            reg[4 * c + 1] = q.y;
-            reg[4 * c + 2] = q.z;
-            reg[4 * c + 3] = q.w;
-        }
+        for (int c = 0; c < kResChunks; ++c) issue_chunk(rs, voff, c);
     };
     if (r < rows) issue_loads(r);
     while (r < rows) {
@@ -435,6 +439,7 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             push_hits();
             lds_barrier();
         }
+        bool loaded = false;  // the next row's loads are issued
         if (do_lse) {
             float acc = seg == 0 ? 0.0f : s_acc[j];
             if (use_table) {
@@ -453,16 +458,23 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
                 };
                 // blocks of kBlk registers; the lookups of block b + 1 are in
                 // flight while block b is added in order
+                // (a block is one loaded chunk: once its lookups are issued,
+                // its registers take the same chunk of the next row)
                 constexpr int kBlk = 4;
+                static_assert(kBlk == 4, "a lookup block is one chunk");
+                const __amdgpu_buffer_rsrc_t rs_next = row_view(next_row());
+                const int voff_next = lane_offset();
                 float cur[2 * kBlk], nxt[2 * kBlk];
 #pragma unroll
                 for (int q = 0; q < kBlk; ++q) lookup(q, cur[2 * q], cur[2 * q + 1]);
+                issue_chunk(rs_next, voff_next, 0);
 #pragma unroll
                 for (int k0 = 0; k0 < kResRegs; k0 += kBlk) {
                     __builtin_amdgcn_sched_barrier(0);
                     if (k0 + kBlk < kResRegs) {
 #pragma unroll
                         for (int q = 0; q < kBlk; ++q) lookup(k0 + kBlk + q, nxt[2 * q], nxt[2 * q + 1]);
+                        issue_chunk(rs_next, voff_next, k0 / kBlk + 1);
                     }
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -470,6 +482,7 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
 #pragma unroll
                     for (int q = 0; q < 2 * kBlk; ++q) cur[q] = nxt[q];
                 }
+                loaded = true;
             } else {
                 // Cephes terms, re-reading the segment (its lines are still cached)
                 for (int s = s_begin; s < s_begin + 8 * nch; s += 8) {
@@ -491,7 +504,7 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             s_hist2[tid] = 0;  // every wavefront has read its b2
             push_hits();
         }
-        issue_loads(next_row());
+        if (!loaded) issue_loads(next_row());
         lds_barrier();
 
         if (wave == 0) {
