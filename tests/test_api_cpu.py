@@ -68,3 +68,43 @@ def test_fake_implementations_give_shapes():
     assert g.shape == (2, 3, 4, 7) and g.dtype == torch.bfloat16
     seq = torch.ops.beamgrad.backtrack(p, p, None)
     assert seq.shape == (2, 4, 3) and seq.dtype == torch.int64
+
+
+def test_beam_search_argument_errors():
+    """beam_search's checks that run before any step reaches the engine
+    (reference python/tests/test_search.py:223-238)."""
+    opts = bg.BeamOptions(beam_size=2)
+    good = lambda beams: torch.zeros(1, 2, 4).log_softmax(-1)  # noqa: E731
+    with pytest.raises(TypeError):
+        bg.beam_search(good, object(), max_steps=2)
+    with pytest.raises(ValueError, match="max_steps"):
+        bg.beam_search(good, opts, max_steps=0)
+    with pytest.raises(ValueError, match="max_steps"):
+        bg.beam_search(good, opts, max_steps=True)
+    with pytest.raises(ValueError, match="batch_size"):
+        bg.beam_search(good, opts, max_steps=2, batch_size=2**32 + 1)
+    with pytest.raises(ValueError, match=r"\[B, K, V\]"):
+        bg.beam_search(lambda beams: torch.zeros(1, 3, 4), opts, max_steps=2)
+    with pytest.raises(TypeError):
+        bg.beam_search(lambda beams: torch.zeros(1, 2, 4, dtype=torch.long), opts, max_steps=2)
+    with pytest.raises(ValueError, match="outside the vocabulary"):
+        bg.beam_search(good, bg.BeamOptions(beam_size=2, eos_token=4), max_steps=2)
+    # the product has no CPU engine: host rows are refused before any decode
+    with pytest.raises(ValueError, match="GPU"):
+        bg.beam_search(good, opts, max_steps=2)
+    with pytest.raises(ValueError, match="rescore_fn|GPU"):
+        bg.beam_search(good, opts, max_steps=2, rescore_fn=lambda s, n: torch.zeros(1, 2))
+
+
+def test_beam_search_state_on_a_fixed_device_checks_the_rows_device():
+    opts = bg.BeamOptions(beam_size=2)
+    with pytest.raises(ValueError, match="beam state is on meta"):
+        bg.beam_search(lambda beams: torch.zeros(1, 2, 4).log_softmax(-1), opts, max_steps=2, device="meta")
+
+
+def test_sequence_scores_rejects_lengths_outside_the_sequences():
+    lp = torch.zeros(2, 3)
+    with pytest.raises(ValueError, match=r"lengths must be in \[0, 3\]"):
+        bg.sequence_scores(lp, torch.tensor([1, 4]), bg.BeamOptions(beam_size=1))
+    with pytest.raises(ValueError, match="shape"):
+        bg.sequence_scores(lp, torch.tensor([1]), bg.BeamOptions(beam_size=1))
