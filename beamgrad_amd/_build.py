@@ -53,11 +53,24 @@ def _run(cmd: list[str]) -> None:
 
 
 def build_lib() -> str:
-    os.makedirs(os.path.join(HERE, "_lib"), exist_ok=True)
+    """Compiles each source to an object in parallel (one hipcc per source),
+    then links the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = os.path.join(HERE, "_lib", "obj")
+    os.makedirs(objdir, exist_ok=True)
     out = lib_path()
-    cmd = [HIPCC, *HIP_FLAGS, "-shared", "-fvisibility=hidden", f"-I{ROOT}/include", f"-I{HERE}/csrc",
-           *LIB_SOURCES, "-o", out + ".tmp"]
-    _run(cmd)
+    objs = [os.path.join(objdir, os.path.splitext(os.path.basename(src))[0] + ".o") for src in LIB_SOURCES]
+
+    def compile_one(src_obj):
+        src, obj = src_obj
+        _run([HIPCC, *HIP_FLAGS, "-fvisibility=hidden", f"-I{ROOT}/include", f"-I{HERE}/csrc", "-c", src,
+              "-o", obj])
+
+    jobs = max(1, min(len(LIB_SOURCES), int(os.environ.get("MAX_JOBS", "0") or 0) or (os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        list(pool.map(compile_one, zip(LIB_SOURCES, objs)))
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
     return out
 

@@ -126,9 +126,12 @@ size_t sync_bytes(int B, int T) {
 // pass can run alongside on a second stream, following the row pass step by
 // step: the row pass is queued first and never waits on the select pass, and
 // its rows are handed out by ticket, so it always progresses on the CUs left.
-// By default only constrained decodes (n-gram blocking, repetition penalty)
-// do: their select pass is as long as the row pass, while elsewhere the CUs
-// the row pass loses cost more than the overlap saves (measured on MI355X).
+// By default constrained decodes (n-gram blocking, repetition penalty) do,
+// whose select pass is as long as the row pass, and decodes whose row pass is
+// one of the persistent kernels (16-bit rows kept on chip), which lose only
+// the B CUs they leave free (MI355X: C2 2.00 -> 1.89 ms, C5 forward 2.35 ->
+// 1.75 ms). The one-read log-prob kernel runs several workgroups per CU and
+// loses more than the overlap saves (C4 3.03 -> 3.58 ms), so it does not.
 hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStream_t stream, char* ws) {
     DecodeParams p = p0;
     int device = 0;
@@ -137,7 +140,8 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     std::lock_guard<std::mutex> lock(g_aux_mutex);
     Aux* aux = nullptr;
     const int mode = g_overlap.load(std::memory_order_relaxed);
-    const bool want = !p.step_mode && p.T > 1 && (mode == 1 || (mode == -1 && p.constrained));
+    const bool want =
+        !p.step_mode && p.T > 1 && (mode == 1 || (mode == -1 && (p.constrained || row_pass_persistent(p))));
     if (want) {
         e = aux_for(device, aux);
         if (e != hipSuccess) return e;

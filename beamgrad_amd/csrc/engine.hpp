@@ -134,6 +134,9 @@ hipError_t launch_decode(const DecodeParams& p, const DecodeLayout& L, hipStream
 size_t sync_bytes(int B, int T);           // overlapped-decode counters in the workspace
 extern std::atomic<int> g_overlap;         // dbs_hip_set_decode_overlap
 hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream);
+// Whether launch_row_pass would run one of the persistent (one workgroup per
+// CU) row passes for p.
+bool row_pass_persistent(const DecodeParams& p);
 // Row pass that keeps each row on chip (16-bit rows, V % 8 == 0, 16-byte
 // aligned, V <= 155648); launch_row_pass uses it when eligible.
 bool row_resident_eligible(const DecodeParams& p);

@@ -144,6 +144,13 @@ __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
 
 std::atomic<int> g_row_pass_kind{-1};
 
+bool row_pass_persistent(const DecodeParams& p) {
+    const int kind = g_row_pass_kind.load(std::memory_order_relaxed);
+    if ((kind == -1 || kind == 3) && row_logprob_eligible(p)) return false;
+    if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return true;
+    return (kind == -1 || kind == 2) && row_pipe_eligible(p);
+}
+
 hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream) {
     const int64_t rows = p.step_mode ? static_cast<int64_t>(p.B) * p.K : static_cast<int64_t>(p.B) * p.T * p.K;
     if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
