@@ -108,3 +108,29 @@ def test_sequence_scores_rejects_lengths_outside_the_sequences():
         bg.sequence_scores(lp, torch.tensor([1, 4]), bg.BeamOptions(beam_size=1))
     with pytest.raises(ValueError, match="shape"):
         bg.sequence_scores(lp, torch.tensor([1]), bg.BeamOptions(beam_size=1))
+
+
+def test_fake_and_meta_tensors_trace_without_the_engine():
+    """Shape-only tensors go through the operators' fake implementations
+    (reference python/tests/test_api.py:446-454), so torch.compile and export
+    can trace the API without a GPU."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        out = bg.decode(torch.empty(3, 5, 4, 17), bg.BeamOptions(beam_size=4))
+        assert out.final_scores.shape == (3, 4)
+        assert out.tokens.shape == (3, 5, 4) and out.tokens.dtype == torch.int64
+        assert out.from_logprob.dtype == torch.bool
+        scores = bg.final_scores(torch.empty(2, 3, 4, 9, dtype=torch.bfloat16), bg.BeamOptions(beam_size=4),
+                                 from_logits=True)
+        assert scores.shape == (2, 4) and scores.dtype == torch.float32
+    meta = bg.decode(torch.empty(2, 6, 3, 11, device="meta"), bg.BeamOptions(beam_size=3))
+    assert meta.parents.shape == (2, 6, 3) and meta.parents.device.type == "meta"
+
+
+def test_batching_rules_are_registered():
+    import torch._C as C
+
+    for op in ("decode", "decode_ex", "decode_backward", "decode_backward_as", "final_scores_backward",
+               "final_scores_path_gradient", "length_penalty", "backtrack"):
+        assert C._dispatch_has_kernel_for_dispatch_key(f"beamgrad::{op}", "FuncTorchBatched"), op
