@@ -129,10 +129,8 @@ bool valid_args(const DBSCudaDecodeArgs* a) {
     return elements < 9.0e18;
 }
 
-// Per-example beams, EOS tokens and minimum lengths are not implemented by
-// this engine yet: such calls are rejected rather than decoded differently.
-bool unsupported_per_example(const DBSCudaDecodeArgs* a) {
-    return a->beam_sizes_per_example || a->eos_tokens_per_example || a->min_lengths_per_example;
+bool has_per_example(const DBSCudaDecodeArgs& a) {
+    return a.steps_per_example || a.beam_sizes_per_example || a.eos_tokens_per_example || a.min_lengths_per_example;
 }
 
 bool constrained(const DBSCudaDecodeArgs& a) { return a.no_repeat_ngram_size > 0 || a.repetition_penalty > 1.0f; }
@@ -143,19 +141,24 @@ bool valid_options(const DBSCudaSearchOptions* o, const DBSCudaDecodeArgs& a) {
     for (int i = 0; i < 4; ++i)
         if (o->reserved[i]) return false;
     if (o->extra_eos_count < 0 || o->extra_eos_count > DBS_CUDA_MAX_EXTRA_EOS) return false;
-    if (o->extra_eos_count > 0 && a.eos_token < 0) return false;
+    if (o->extra_eos_count > 0 && a.eos_token < 0 && !a.eos_tokens_per_example) return false;
     for (int i = 0; i < o->extra_eos_count; ++i)
         if (o->extra_eos_tokens[i] < 0 || o->extra_eos_tokens[i] >= a.vocab_size) return false;
     return true;
 }
 
+// The EOS tokens: the scalar one with the extra ones, or with per-example EOS
+// tokens the extra ones only (each example adds its own).
 void fill_eos(DecodeParams& p, const DBSCudaDecodeArgs& a, const DBSCudaSearchOptions* o) {
     p.eos = a.eos_token;
     p.n_eos = 0;
-    if (a.eos_token < 0) return;
+    p.eos_pe = a.eos_tokens_per_example;
+    p.minlen_pe = a.min_lengths_per_example;
+    p.beam_pe = a.beam_sizes_per_example;
+    if (a.eos_token < 0 && !a.eos_tokens_per_example) return;
     int32_t set[kMaxEos];
     int n = 0;
-    set[n++] = a.eos_token;
+    if (!a.eos_tokens_per_example) set[n++] = a.eos_token;
     if (o)
         for (int i = 0; i < o->extra_eos_count; ++i) set[n++] = o->extra_eos_tokens[i];
     // sort, unique (reference src/decoder.cpp:57-63)
@@ -196,12 +199,26 @@ struct Scratch {
     }
 };
 
+// Device-side range check of the per-example arrays, read back once
+// (synchronizes the stream); status is 4 bytes of device scratch.
+int check_per_example(const DBSCudaDecodeArgs& a, int32_t* status, hipStream_t stream) {
+    if (!has_per_example(a)) return DBS_CUDA_STATUS_OK;
+    hipError_t e = launch_check_examples(a.steps_per_example, a.beam_sizes_per_example, a.eos_tokens_per_example,
+                                         a.min_lengths_per_example, a.batch_size, a.steps, a.beam_size, a.vocab_size,
+                                         status, stream);
+    int32_t host = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&host, status, sizeof(host), hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return finish(stream, e);
+    return host != 0 ? DBS_CUDA_STATUS_INVALID_ARGUMENT : DBS_CUDA_STATUS_OK;
+}
+
 int decode_common(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                   const DBSCudaSearchOptions* options, const uint8_t* banned_pe, const DBSCudaDecodeOutputs* outputs,
                   float* row_lse, void* workspace, int64_t workspace_bytes, void* stream_ptr) {
     if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !outputs || !outputs->final_scores)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
-    if (unsupported_per_example(args) || !valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     const DBSCudaDecodeArgs& a = *args;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     const bool cons = constrained(a);
@@ -213,16 +230,8 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
     if (e != hipSuccess) return finish(stream, e);
     char* ws = static_cast<char*>(scratch.ptr);
 
-    if (a.steps_per_example) {
-        // device-side range check, read back once (synchronizes the stream)
-        int32_t* status = reinterpret_cast<int32_t*>(ws + L.off_rowinfo);
-        e = launch_check_steps(a.steps_per_example, a.batch_size, a.steps, status, stream);
-        int32_t host = 0;
-        if (e == hipSuccess) e = hipMemcpyAsync(&host, status, sizeof(host), hipMemcpyDeviceToHost, stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(stream);
-        if (e != hipSuccess) return finish(stream, e);
-        if (host != 0) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
-    }
+    const int checked = check_per_example(a, reinterpret_cast<int32_t*>(ws + L.off_rowinfo), stream);
+    if (checked != DBS_CUDA_STATUS_OK) return checked;
 
     DecodeParams p{};
     p.x = inputs;
@@ -274,7 +283,7 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
                 void* stream_ptr) {
     if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !state || !outputs)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
-    if (unsupported_per_example(args) || !valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     const DBSCudaDecodeArgs& a = *args;
     if (a.steps != 1 || a.steps_per_example) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!state->raw_scores || !state->lengths || !state->finished || state->prefix_stride < 0 || state->reserved0 != 0)
@@ -289,6 +298,8 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
     if (too_small) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (e != hipSuccess) return finish(stream, e);
     char* ws = static_cast<char*>(scratch.ptr);
+    const int checked = check_per_example(a, reinterpret_cast<int32_t*>(ws + L.off_rowinfo), stream);
+    if (checked != DBS_CUDA_STATUS_OK) return checked;
 
     DecodeParams p{};
     p.x = inputs;
@@ -340,7 +351,6 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
 int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, void* out, int out_type,
                     bool accumulate, void* workspace, int64_t workspace_bytes, void* stream_ptr) {
     if (!valid_args(args) || !in || !out) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
-    if (unsupported_per_example(args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!in->parents || !in->tokens || !in->lengths || !in->from_logprob) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (in->reserved0 != 0) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     for (int i = 0; i < 4; ++i)
@@ -356,15 +366,9 @@ int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* 
     if (e != hipSuccess) return finish(stream, e);
     char* ws = static_cast<char*>(scratch.ptr);
 
-    if (a.steps_per_example) {
-        int32_t* status = reinterpret_cast<int32_t*>(ws + backward_workspace_bytes(a.batch_size, a.steps, a.beam_size));
-        e = launch_check_steps(a.steps_per_example, a.batch_size, a.steps, status, stream);
-        int32_t host = 0;
-        if (e == hipSuccess) e = hipMemcpyAsync(&host, status, sizeof(host), hipMemcpyDeviceToHost, stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(stream);
-        if (e != hipSuccess) return finish(stream, e);
-        if (host != 0) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
-    }
+    const int checked = check_per_example(
+        a, reinterpret_cast<int32_t*>(ws + backward_workspace_bytes(a.batch_size, a.steps, a.beam_size)), stream);
+    if (checked != DBS_CUDA_STATUS_OK) return checked;
     BackwardParams p{};
     p.B = a.batch_size;
     p.T = a.steps;
@@ -372,6 +376,7 @@ int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* 
     p.V = a.vocab_size;
     p.alpha = a.length_penalty_alpha;
     p.steps = a.steps_per_example;
+    p.beams = a.beam_sizes_per_example;
     p.parents = in->parents;
     p.tokens = in->tokens;
     p.lengths = in->lengths;
@@ -425,19 +430,19 @@ DBS_CUDA_EXPORT int dbs_cuda_set_synchronization(int synchronize) {
 DBS_CUDA_EXPORT int dbs_cuda_get_synchronization(void) { return sync_flag(); }
 
 DBS_CUDA_EXPORT int64_t dbs_cuda_decode_workspace_size(const DBSCudaDecodeArgs* args) {
-    if (!valid_args(args) || unsupported_per_example(args)) return -1;
+    if (!valid_args(args)) return -1;
     return static_cast<int64_t>(
         decode_layout(args->batch_size, args->steps, args->beam_size, args->vocab_size, constrained(*args), false, 0)
             .total);
 }
 
 DBS_CUDA_EXPORT int64_t dbs_cuda_backward_workspace_size(const DBSCudaDecodeArgs* args) {
-    if (!valid_args(args) || unsupported_per_example(args)) return -1;
+    if (!valid_args(args)) return -1;
     return static_cast<int64_t>(backward_workspace_bytes(args->batch_size, args->steps, args->beam_size) + 256);
 }
 
 DBS_CUDA_EXPORT int64_t dbs_cuda_decode_step_workspace_size(const DBSCudaDecodeArgs* args, int prefix_stride) {
-    if (!valid_args(args) || unsupported_per_example(args) || args->steps != 1 || args->steps_per_example ||
+    if (!valid_args(args) || args->steps != 1 || args->steps_per_example ||
         prefix_stride < 0)
         return -1;
     return static_cast<int64_t>(decode_layout(args->batch_size, 1, args->beam_size, args->vocab_size,
@@ -537,23 +542,17 @@ DBS_CUDA_EXPORT int dbs_cuda_path_gradient(const DBSCudaDecodeArgs* args, const 
                                            const int32_t* tokens, const int32_t* lengths,
                                            const uint8_t* from_logprob, const float* grad_final_scores, float* draws,
                                            void* stream_ptr) {
-    if (!valid_args(args) || unsupported_per_example(args) || !parents || !tokens || !lengths || !from_logprob ||
-        !grad_final_scores || !draws)
+    if (!valid_args(args) || !parents || !tokens || !lengths || !from_logprob || !grad_final_scores || !draws)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     const DBSCudaDecodeArgs& a = *args;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    if (a.steps_per_example) {
+    if (has_per_example(a)) {
         Scratch scratch;
         bool too_small = false;
         hipError_t e = scratch.acquire(nullptr, 0, 256, stream, &too_small);
         if (e != hipSuccess) return finish(stream, e);
-        int32_t* status = static_cast<int32_t*>(scratch.ptr);
-        e = launch_check_steps(a.steps_per_example, a.batch_size, a.steps, status, stream);
-        int32_t host = 0;
-        if (e == hipSuccess) e = hipMemcpyAsync(&host, status, sizeof(host), hipMemcpyDeviceToHost, stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(stream);
-        if (e != hipSuccess) return finish(stream, e);
-        if (host != 0) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+        const int checked = check_per_example(a, static_cast<int32_t*>(scratch.ptr), stream);
+        if (checked != DBS_CUDA_STATUS_OK) return checked;
     }
     BackwardParams p{};
     p.B = a.batch_size;
@@ -562,6 +561,7 @@ DBS_CUDA_EXPORT int dbs_cuda_path_gradient(const DBSCudaDecodeArgs* args, const 
     p.V = a.vocab_size;
     p.alpha = a.length_penalty_alpha;
     p.steps = a.steps_per_example;
+    p.beams = a.beam_sizes_per_example;
     p.parents = parents;
     p.tokens = tokens;
     p.lengths = lengths;

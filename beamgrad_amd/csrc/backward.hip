@@ -37,6 +37,7 @@ __global__ __launch_bounds__(kWalkThreads) void path_walk_kernel(BackwardParams 
     const int tid = static_cast<int>(threadIdx.x);
     const int K = p.K, T = p.T, V = p.V;
     const int steps_b = p.steps ? p.steps[b] : T;
+    const int Kb = p.beams ? p.beams[b] : K;  // slots past the example's beams carry nothing
     for (int k = tid; k < K; k += kWalkThreads) next[k] = 0.0f;
     // steps the example did not decode carry no gradient
     for (int64_t i = static_cast<int64_t>(steps_b) * K + tid; i < static_cast<int64_t>(T) * K; i += kWalkThreads)
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(kWalkThreads) void path_walk_kernel(BackwardParams 
         for (int k = tid; k < K; k += kWalkThreads) {
             const int64_t slot = base + k;
             const int parent = p.parents[slot];
-            const bool valid = parent >= 0 && parent < K;  // malformed slots carry nothing
+            const bool valid = k < Kb && parent >= 0 && parent < Kb;  // malformed slots carry nothing
             float d = 0.0f;
             if (valid) {
                 float drank = 0.0f;

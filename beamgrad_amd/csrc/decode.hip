@@ -37,12 +37,18 @@ __global__ void length_penalty_kernel(const int32_t* lengths, int64_t n, float a
     for (int64_t j = i; j < n; j += stride) out[j] = length_penalty(lengths[j], alpha);
 }
 
-__global__ void check_steps_kernel(const int32_t* steps, int B, int T, int32_t* status) {
+// Range check of the per-example arrays (reference cuda/dbs_cuda.cu:376-385);
+// one workgroup, status[0] = 0 when every entry passes.
+__global__ void check_examples_kernel(const int32_t* steps, const int32_t* beams, const int32_t* eos,
+                                      const int32_t* min_lengths, int B, int T, int K, int V, int32_t* status) {
     __shared__ int bad;
     if (threadIdx.x == 0) bad = 0;
     __syncthreads();
-    for (int i = static_cast<int>(threadIdx.x); i < B; i += static_cast<int>(blockDim.x))
-        if (steps[i] < 1 || steps[i] > T) atomicOr(&bad, 1);
+    for (int i = static_cast<int>(threadIdx.x); i < B; i += static_cast<int>(blockDim.x)) {
+        const bool ok = (!steps || (steps[i] >= 1 && steps[i] <= T)) && (!beams || (beams[i] >= 1 && beams[i] <= K)) &&
+                        (!eos || (eos[i] >= -1 && eos[i] < V)) && (!min_lengths || min_lengths[i] >= 0);
+        if (!ok) atomicOr(&bad, 1);
+    }
     __syncthreads();
     if (threadIdx.x == 0) status[0] = bad;
 }
@@ -182,7 +188,14 @@ hipError_t launch_length_penalty(const int32_t* lengths, int64_t n, float alpha,
 }
 
 hipError_t launch_check_steps(const int32_t* steps, int B, int T, int32_t* status, hipStream_t stream) {
-    hipLaunchKernelGGL(check_steps_kernel, dim3(1), dim3(256), 0, stream, steps, B, T, status);
+    return launch_check_examples(steps, nullptr, nullptr, nullptr, B, T, 1, 1, status, stream);
+}
+
+hipError_t launch_check_examples(const int32_t* steps, const int32_t* beams, const int32_t* eos,
+                                 const int32_t* min_lengths, int B, int T, int K, int V, int32_t* status,
+                                 hipStream_t stream) {
+    hipLaunchKernelGGL(check_examples_kernel, dim3(1), dim3(256), 0, stream, steps, beams, eos, min_lengths, B, T, K,
+                       V, status);
     return hipGetLastError();
 }
 

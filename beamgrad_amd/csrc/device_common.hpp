@@ -27,10 +27,26 @@ __device__ __forceinline__ float load_one(const void* base, int64_t i) {
     }
 }
 
-__device__ __forceinline__ bool is_eos_tok(const DecodeParams& p, int32_t v) {
+__device__ __forceinline__ bool in_eos_set(const DecodeParams& p, int32_t v) {
     for (int i = 0; i < p.n_eos; ++i)
         if (p.eos_set[i] == v) return true;
     return false;
+}
+
+// Options of example b: its EOS token (-1: none), minimum length and beams
+// (reference cuda/dbs_cuda.cu:148-155 reads the same per-example arrays).
+__device__ __forceinline__ int eos_of(const DecodeParams& p, int b) { return p.eos_pe ? p.eos_pe[b] : p.eos; }
+__device__ __forceinline__ int min_length_of(const DecodeParams& p, int b) {
+    return p.minlen_pe ? p.minlen_pe[b] : p.min_length;
+}
+__device__ __forceinline__ int beams_of(const DecodeParams& p, int b) { return p.beam_pe ? p.beam_pe[b] : p.K; }
+
+// Whether token v ends a hypothesis of example b: its EOS token or an extra
+// one, where the example has EOS handling at all.
+__device__ __forceinline__ bool is_eos_of(const DecodeParams& p, int b, int32_t v) {
+    if (!p.eos_pe) return in_eos_set(p, v);  // the set holds the EOS token and the extra ones
+    const int e = p.eos_pe[b];
+    return e >= 0 && (v == e || in_eos_set(p, v));
 }
 
 // Statically excluded tokens of a row: banned (shared or per example) and the
@@ -38,7 +54,7 @@ __device__ __forceinline__ bool is_eos_tok(const DecodeParams& p, int32_t v) {
 __device__ __forceinline__ bool static_masked(const DecodeParams& p, int b, int v, bool mask_eos) {
     if (p.banned && p.banned[v]) return true;
     if (p.banned_pe && p.banned_pe[static_cast<int64_t>(b) * p.V + v]) return true;
-    if (mask_eos && is_eos_tok(p, v)) return true;
+    if (mask_eos && is_eos_of(p, b, v)) return true;
     return false;
 }
 
@@ -69,16 +85,17 @@ __device__ __forceinline__ bool row_is_read(const DecodeParams& p, int64_t r, in
     const int K = p.K;
     if (p.step_mode) {
         b = static_cast<int>(r / K);
+        if (static_cast<int>(r % K) >= beams_of(p, b)) return false;  // past the example's beams
         const float praw = p.st_raw[r];
         if (!(praw < kInf && praw > -kInf)) return false;  // dead beam
-        if (p.eos >= 0 && p.st_fin[r]) return false;        // finished
+        if (eos_of(p, b) >= 0 && p.st_fin[r]) return false;  // finished
         new_len = p.st_len[r] + 1;
         return true;
     }
     b = static_cast<int>(r / (static_cast<int64_t>(p.T) * K));
     const int t = static_cast<int>((r / K) % p.T);
     const int k = static_cast<int>(r % K);
-    if (t >= example_steps(p, b) || (t == 0 && k != 0)) return false;
+    if (t >= example_steps(p, b) || (t == 0 && k != 0) || k >= beams_of(p, b)) return false;
     new_len = t + 1;  // every unfinished live beam has length t at step t
     return true;
 }

@@ -60,10 +60,14 @@ struct DecodeParams {
     int dtype;
     int from_logits;
     int B, T, K, V;
-    int eos;                  // -1: no EOS handling
+    int eos;                  // -1: no EOS handling (eos_pe null)
     int n_eos;                // size of eos_set (0 when eos < 0)
-    int32_t eos_set[kMaxEos]; // every EOS token, sorted, distinct
+    int32_t eos_set[kMaxEos]; // every EOS token, sorted, distinct (with eos_pe: the extra EOS tokens only)
     int min_length;
+    // per example (reference include/dbs_cuda.h:80-85; null: the scalars above)
+    const int32_t* beam_pe;   // device [B] beams in [1, K]: slots past them stay empty
+    const int32_t* eos_pe;    // device [B] EOS token in [-1, V); the extra EOS tokens count only where >= 0
+    const int32_t* minlen_pe; // device [B] minimum length >= 0
     float alpha;
     int ngram;
     int penalise;
@@ -158,12 +162,18 @@ hipError_t wait_timeout_counter(int reset, unsigned long long* value);
 hipError_t launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream);
 hipError_t launch_length_penalty(const int32_t* lengths, int64_t n, float alpha, float* out, hipStream_t stream);
 hipError_t launch_check_steps(const int32_t* steps, int B, int T, int32_t* status, hipStream_t stream);
+// Range check of every per-example array (steps in [1, T], beams in [1, K],
+// EOS in [-1, V), minimum lengths >= 0): status 0 when all pass.
+hipError_t launch_check_examples(const int32_t* steps, const int32_t* beams, const int32_t* eos,
+                                 const int32_t* min_lengths, int B, int T, int K, int V, int32_t* status,
+                                 hipStream_t stream);
 
 // Backward.
 struct BackwardParams {
     int B, T, K, V;
     float alpha;
     const int32_t* steps;
+    const int32_t* beams;  // device [B] beams per example, or null (K)
     const int32_t* parents;
     const int32_t* tokens;
     const int32_t* lengths;

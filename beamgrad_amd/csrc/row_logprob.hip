@@ -79,7 +79,7 @@ __global__ __launch_bounds__(kLpThreads) void row_logprob_kernel(DecodeParams p)
     const int64_t r = row_of_ticket(p, blockIdx.x);
     int b, new_len;
     if (!row_is_read(p, r, b, new_len)) return;
-    const bool mask_eos = new_len < p.min_length;
+    const bool mask_eos = new_len < min_length_of(p, b);
     const int V = p.V;
     const int M = p.M;
     constexpr int esz = DT == 0 ? 4 : 2;

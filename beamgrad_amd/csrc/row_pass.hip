@@ -66,7 +66,7 @@ __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
     const int V = p.V;
     int b, new_len;
     if (!row_is_read(p, r, b, new_len)) return;
-    const bool mask_eos = new_len < p.min_length;
+    const bool mask_eos = new_len < min_length_of(p, b);
     const size_t esz = DT == 0 ? 4 : 2;
     const char* row = static_cast<const char*>(p.x) + static_cast<size_t>(r) * static_cast<size_t>(V) * esz;
     const int nq = (V + kLanes - 1) / kLanes;

@@ -186,7 +186,7 @@ __global__ __launch_bounds__(kPipeThreads) void row_pipe_kernel(DecodeParams p, 
     while (r < rows) {
         const int slot2 = rslot == 0 ? 2 : rslot - 1;  // (rslot + 2) % 3
         if (tid == 0) publish_next_row(p, rows, q_next, s_rows[slot2]);
-        const bool mask_eos = new_len < p.min_length;
+        const bool mask_eos = new_len < min_length_of(p, b);
         const uint16_t* row = static_cast<const uint16_t*>(p.x) + r * V;
         const int sh = static_cast<int>((r * static_cast<int64_t>(V)) & 1);
         // Opaque copies per row: what the unrolled code derives from them is

@@ -226,7 +226,7 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             int bt = 0, lt = 0;
             return read_row_slot(s_rows[par ^ 1], bt, lt);
         };
-        const bool mask_eos = new_len < p.min_length;
+        const bool mask_eos = new_len < min_length_of(p, b);
         const uint16_t* row = static_cast<const uint16_t*>(p.x) + r * V;
         // Opaque copies per row: everything the unrolled load derives from
         // them is recomputed per row instead of being hoisted out of the row

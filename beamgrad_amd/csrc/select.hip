@@ -314,7 +314,7 @@ __device__ __forceinline__ void end_round(Lds& s, State& st, int K, int sort_cap
 template <int DT, bool LOGITS>
 __device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State& st, int b, int k, int64_t row, float lse,
                            float praw, float inv_pen, int new_len, const PrefixView& pre, int sort_cap) {
-    const bool mask_eos = new_len < p.min_length;
+    const bool mask_eos = new_len < min_length_of(p, b);
     const int V = p.V;
     const int tid = static_cast<int>(threadIdx.x);
     const size_t esz = DT == 0 ? 4 : 2;
@@ -410,6 +410,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                          : p.blocked + static_cast<int64_t>(b) * K * p.prefix_cap;
 
     const int steps_b = p.step_mode ? 1 : example_steps(p, b);
+    // this example's beams (slots past them stay empty) and EOS token
+    const int Kb = beams_of(p, b), eos_b = eos_of(p, b);
     const int T_loop = p.step_mode ? 1 : T;
     const int pen_len = L.pen_len;
     for (int l = tid; l < pen_len; l += kSelectThreads) {
@@ -421,7 +423,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     for (int k = tid; k < K; k += kSelectThreads) {
         if (p.step_mode) {
             const int64_t i = static_cast<int64_t>(b) * K + k;
-            s.raw[k] = p.st_raw[i];
+            s.raw[k] = k < Kb ? p.st_raw[i] : -kInf;
             s.len[k] = p.st_len[i];
             s.ended[k] = p.st_fin[i] != 0;
             const int l = p.st_len[i];
@@ -473,7 +475,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         for (int k = tid; k < K; k += kSelectThreads) {
             const float praw = s.raw[k];
             const bool live = praw < kInf && praw > -kInf;
-            const bool carried = live && p.eos >= 0 && s.ended[k];
+            const bool carried = live && eos_b >= 0 && s.ended[k];
             int cnt = -2;
             float bound = -kInf;
             if (live && !carried) {
@@ -605,10 +607,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         for (int k = tid; k < K; k += kSelectThreads) {
             const float praw = s.raw[k];
             const bool live = praw < kInf && praw > -kInf;
-            if (live && p.eos >= 0 && s.ended[k]) {
+            if (live && eos_b >= 0 && s.ended[k]) {
                 const int l = s.len[k] > 1 ? s.len[k] : 1;
                 const int32_t last = s.last[k];
-                const Cand c{praw / pen_of(s, pen_len, l, p.alpha), praw, k, is_eos_tok(p, last) ? last : p.eos, l,
+                const Cand c{praw / pen_of(s, pen_len, l, p.alpha), praw, k, is_eos_of(p, b, last) ? last : eos_b, l,
                              0};
                 offer(s, st, c);
             }
@@ -693,7 +695,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 const float X = s.raw[k] + s.rbound[k];
                 if (X > -kInf) {
                     const float SX = X * inv_of(s, pen_len, s.len[k] + 1, p.alpha);
-                    const Cand kth = st.count >= K ? s.buf[K - 1] : dead_cand();
+                    const Cand kth = st.count >= Kb ? s.buf[Kb - 1] : dead_cand();
                     fail = !((kth.score > SX) || (kth.score == SX && kth.raw > X));
                 }
             }
@@ -721,8 +723,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             compact(s, st, K);
         }
 
-        // Selection (reference src/decoder.cpp:314-350).
-        const int nsel = st.count;
+        // Selection (reference src/decoder.cpp:314-350): the example's best Kb.
+        const int nsel = st.count < Kb ? st.count : Kb;
         for (int k = tid; k < K; k += kSelectThreads) {
             const Cand c = k < nsel ? s.buf[k] : dead_cand();
             const int64_t o = trace0 + k;
@@ -735,7 +737,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             s.nraw[k] = c.raw;
             s.nlen[k] = c.length;
             s.nlast[k] = c.token;
-            s.nended[k] = c.parent >= 0 ? (s.ended[c.parent] || is_eos_tok(p, c.token)) : 0;
+            s.nended[k] = c.parent >= 0 ? (s.ended[c.parent] || is_eos_of(p, b, c.token)) : 0;
             if (p.constrained && !p.step_mode) {
                 const int nxt = cur ^ 1;
                 s.plen[nxt * K + k] =

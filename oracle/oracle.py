@@ -180,6 +180,40 @@ class Oracle:
             raise ValueError("oracle decode: invalid arguments")
         return out
 
+    def decode_per_example(self, x: np.ndarray, *, beams=None, eos_tokens=None, min_lengths=None, steps=None,
+                           eos_token: int = -1, extra_eos=(), min_length: int = 0, banned_per_example=None,
+                           **kw) -> dict:
+        """Per-example beams, EOS tokens and minimum lengths: example b decoded
+        alone with its own options on the first beams[b] rows of each step,
+        its slots past them empty (reference src/c_api.cpp:638-698, the CUDA
+        engine's layout cuda/dbs_cuda.cu:944-955 and :969-980). The extra EOS
+        tokens count only for an example with an EOS token."""
+        B, T, K, V = x.shape
+        empty = {"final_scores": -np.inf, "final_raw_scores": -np.inf, "final_lengths": 0, "tokens": -1,
+                 "parents": -1, "lengths": 0, "scores": -np.inf, "raw_scores": -np.inf, "from_logprob": 0,
+                 "row_lse": 0.0, "row_read": 0}
+        parts = []
+        for b in range(B):
+            kb = K if beams is None else int(beams[b])
+            eb = eos_token if eos_tokens is None else int(eos_tokens[b])
+            mb = min_length if min_lengths is None else int(min_lengths[b])
+            st = None if steps is None else [int(np.asarray(steps)[b])]
+            bpe = None if banned_per_example is None else np.asarray(banned_per_example)[b:b + 1]
+            one = self.decode(np.ascontiguousarray(x[b:b + 1, :, :kb]), eos_token=eb,
+                              extra_eos=tuple(extra_eos) if eb >= 0 else (), min_length=mb, steps=st,
+                              banned_per_example=bpe, **kw)
+            full = {}
+            for name, a in one.items():
+                if name == "invalid":
+                    full[name] = a
+                    continue
+                shape = (1, K) if a.ndim == 2 else (1, T, K)
+                f = np.full(shape, empty[name], dtype=a.dtype)
+                f[..., :kb] = a
+                full[name] = f
+            parts.append(full)
+        return {k: np.concatenate([q[k] for q in parts], 0) for k in parts[0]}
+
     # -- backward ----------------------------------------------------------
     def _bwd_args(self, trace: dict, vocab_size: int, alpha: float, steps, grad_final, grad_final_raw, grad_scores,
                   grad_raw, logits, logits_dtype, row_lse, num_threads):
@@ -379,6 +413,67 @@ class Reference:
                 raise ReferenceError(self.lib.dbs_last_global_error().decode())
             return out
         finally:
+            self.lib.dbs_destroy(h)
+
+    def decode_variable(self, x: np.ndarray, *, beam_size: int, beams=None, eos_tokens=None, min_lengths=None,
+                        steps=None, eos_token: int = -1, extra_eos=(), min_length: int = 0, alpha: float = 0.0,
+                        num_threads: int = 0) -> dict:
+        """dbs_decode_batch_variable (float32 rows [B, T, K, V]): per-example
+        steps, beams, EOS tokens and minimum lengths; each example's trace
+        comes back [steps_b, beams_b] and is laid out here as [T, K] with
+        empty slots past it."""
+        x = np.ascontiguousarray(np.asarray(x, np.float32))
+        B, T, K, V = x.shape
+        L = self.lib
+        L.dbs_decode_batch_variable.argtypes = [
+            C.c_void_p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _i32p, _i32p, _u8p, _i32p, C.c_int,
+            C.POINTER(C.c_void_p)]
+        L.dbs_decode_batch_variable.restype = C.c_int
+        L.dbs_batch_result_at.argtypes = [C.c_void_p, C.c_int]
+        L.dbs_batch_result_at.restype = C.c_void_p
+        L.dbs_free_batch_result.argtypes = [C.c_void_p]
+        for name, rt in (("steps", C.c_int), ("beam_size", C.c_int)):
+            getattr(L, "dbs_result_" + name).argtypes = [C.c_void_p]
+            getattr(L, "dbs_result_" + name).restype = rt
+        fields = (("tokens", _i32p), ("parents", _i32p), ("lengths", _i32p), ("scores", _f32p),
+                  ("raw_scores", _f32p), ("final_scores", _f32p), ("final_raw_scores", _f32p))
+        for name, rt in fields:
+            getattr(L, "dbs_result_" + name).argtypes = [C.c_void_p]
+            getattr(L, "dbs_result_" + name).restype = rt
+        h = self._handle(beam_size, eos_token, extra_eos, min_length, alpha, False)
+        keep = {}
+
+        def arr(name, a):
+            if a is None:
+                return None
+            keep[name] = np.ascontiguousarray(np.asarray(a, np.int32))
+            return _ptr(keep[name], C.c_int32)
+
+        res = C.c_void_p()
+        try:
+            status = L.dbs_decode_batch_variable(
+                h, _ptr(x, C.c_float), B, T, K, V, arr("steps", steps), arr("beams", beams), arr("eos", eos_tokens),
+                arr("min", min_lengths), None, None, int(num_threads), C.byref(res))
+            if status != 0:
+                raise ReferenceError(self.lib.dbs_last_global_error().decode())
+            out = {"final_scores": np.full((B, K), -np.inf, np.float32),
+                   "final_raw_scores": np.full((B, K), -np.inf, np.float32),
+                   "tokens": np.full((B, T, K), -1, np.int32), "parents": np.full((B, T, K), -1, np.int32),
+                   "lengths": np.zeros((B, T, K), np.int32), "scores": np.full((B, T, K), -np.inf, np.float32),
+                   "raw_scores": np.full((B, T, K), -np.inf, np.float32)}
+            for b in range(B):
+                r = L.dbs_batch_result_at(res, b)
+                st, kb = L.dbs_result_steps(r), L.dbs_result_beam_size(r)
+                for name, _ in fields:
+                    ptr = getattr(L, "dbs_result_" + name)(r)
+                    if name.startswith("final"):
+                        out[name][b, :kb] = np.ctypeslib.as_array(ptr, shape=(kb,))
+                    else:
+                        out[name][b, :st, :kb] = np.ctypeslib.as_array(ptr, shape=(st, kb))
+            return out
+        finally:
+            if res:
+                L.dbs_free_batch_result(res)
             self.lib.dbs_destroy(h)
 
     def decode_per_example_banned(self, x: np.ndarray, banned_per_example: np.ndarray, *, steps=None, **kw) -> dict:

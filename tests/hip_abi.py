@@ -33,7 +33,7 @@ class HipEngine:
     def decode(self, xin: np.ndarray, dtype: str, *, from_logits=False, eos_token=-1, extra_eos=(), min_length=0,
                alpha=0.0, no_repeat_ngram_size=0, repetition_penalty=1.0, steps=None, banned=None,
                banned_per_example=None, use_ex3: bool | None = None, workspace: bool = True,
-               x_offset: int = 0) -> dict:
+               x_offset: int = 0, beams=None, eos_tokens=None, min_lengths=None, expect_status=None) -> dict:
         B, T, K, V = xin.shape
         x = _dev(xin.view(np.int16) if xin.dtype == np.uint16 else xin)
         if x_offset:
@@ -62,6 +62,11 @@ class HipEngine:
         args.no_repeat_ngram_size, args.repetition_penalty = no_repeat_ngram_size, repetition_penalty
         args.steps_per_example = _abi.ptr(steps_d)
         args.banned_tokens = _abi.ptr(banned_d)
+        per_example = {name: _dev(None if a is None else np.asarray(a, np.int32))
+                       for name, a in (("beams", beams), ("eos", eos_tokens), ("min", min_lengths))}
+        args.beam_sizes_per_example = _abi.ptr(per_example["beams"])
+        args.eos_tokens_per_example = _abi.ptr(per_example["eos"])
+        args.min_lengths_per_example = _abi.ptr(per_example["min"])
         o = _abi.DecodeOutputs(*(_abi.ptr(out[k]) for k in (
             "final_scores", "final_raw_scores", "final_lengths", "tokens", "parents", "lengths", "scores",
             "raw_scores", "from_logprob", "invalid")))
@@ -83,6 +88,9 @@ class HipEngine:
             status = self.lib.dbs_cuda_decode_ex2(
                 _abi.ptr(x), _abi.DTYPE[dtype], int(from_logits), C.byref(args), C.byref(opts), C.byref(o),
                 _abi.ptr(out["row_lse"]), _abi.ptr(ws), ws_bytes if ws is not None else 0, self.stream())
+        if expect_status is not None:
+            torch.cuda.synchronize()
+            return status
         assert status == _abi.STATUS_OK, self.lib.dbs_cuda_status_string(status)
         torch.cuda.synchronize()
         return {k: v.cpu().numpy() for k, v in out.items()}
@@ -108,7 +116,7 @@ class HipEngine:
             inp.row_lse = _abi.ptr(keep["row_lse"])
         return inp
 
-    def _args(self, B, T, K, V, alpha, steps, keep):
+    def _args(self, B, T, K, V, alpha, steps, keep, beams=None):
         args = _abi.DecodeArgs()
         args.batch_size, args.steps, args.beam_size, args.vocab_size = B, T, K, V
         args.eos_token = -1
@@ -116,15 +124,18 @@ class HipEngine:
         args.repetition_penalty = 1.0
         keep["steps"] = _dev(None if steps is None else np.asarray(steps, np.int32))
         args.steps_per_example = _abi.ptr(keep["steps"])
+        keep["beams"] = _dev(None if beams is None else np.asarray(beams, np.int32))
+        args.beam_sizes_per_example = _abi.ptr(keep["beams"])
         return args
 
     def backward(self, trace: dict, V: int, *, alpha=0.0, steps=None, logits=None, dtype="f32", row_lse=None,
-                 mode="accumulate", out_type="f32", initial: np.ndarray | None = None, **grads) -> np.ndarray:
+                 mode="accumulate", out_type="f32", initial: np.ndarray | None = None, beams=None,
+                 **grads) -> np.ndarray:
         """mode 'accumulate': dbs_cuda_backward_ex into `initial` (zeros by
         default); 'dense': dbs_hip_backward_dense in out_type; 'final': dbs_cuda_backward."""
         B, T, K = np.asarray(trace["parents"]).shape
         keep = {}
-        args = self._args(B, T, K, V, alpha, steps, keep)
+        args = self._args(B, T, K, V, alpha, steps, keep, beams)
         inp = self._bwd_inputs(trace, grads, logits, dtype, row_lse, keep)
         ws_bytes = self.lib.dbs_cuda_backward_workspace_size(C.byref(args))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
@@ -148,10 +159,11 @@ class HipEngine:
             return grad.cpu().numpy()
         return grad.view(torch.int16).cpu().numpy().view(np.uint16)
 
-    def path_gradient(self, trace: dict, V: int, grad_final: np.ndarray, *, alpha=0.0, steps=None) -> np.ndarray:
+    def path_gradient(self, trace: dict, V: int, grad_final: np.ndarray, *, alpha=0.0, steps=None,
+                      beams=None) -> np.ndarray:
         B, T, K = np.asarray(trace["parents"]).shape
         keep = {}
-        args = self._args(B, T, K, V, alpha, steps, keep)
+        args = self._args(B, T, K, V, alpha, steps, keep, beams)
         inp = self._bwd_inputs(trace, {"grad_final": grad_final}, None, "f32", None, keep)
         draws = torch.full((B, T, K), 5.0, dtype=torch.float32, device="cuda")
         status = self.lib.dbs_cuda_path_gradient(C.byref(args), inp.parents, inp.tokens, inp.lengths,
@@ -180,3 +192,60 @@ class HipEngine:
         assert status == _abi.STATUS_OK
         torch.cuda.synchronize()
         return out.cpu().numpy()
+
+    # ------------------------------------------------------------------
+    def steps(self, xin: np.ndarray, dtype: str, *, from_logits=False, eos_token=-1, extra_eos=(), min_length=0,
+              alpha=0.0, beams=None, eos_tokens=None, min_lengths=None) -> dict:
+        """The decode of [B, T, K, V] rows run as T calls of
+        dbs_cuda_decode_step_ex2 from the initial beam state (unconstrained),
+        with the trace collected step by step."""
+        B, T, K, V = xin.shape
+        x = _dev(xin.view(np.int16) if xin.dtype == np.uint16 else xin)
+        dev = x.device
+        raw = torch.full((B, K), float("-inf"), dtype=torch.float32, device=dev)
+        raw[:, 0] = 0.0
+        lengths = torch.zeros(B, K, dtype=torch.int32, device=dev)
+        finished = torch.zeros(B, K, dtype=torch.uint8, device=dev)
+        per_example = {name: _dev(None if a is None else np.asarray(a, np.int32))
+                       for name, a in (("beams", beams), ("eos", eos_tokens), ("min", min_lengths))}
+        args = _abi.DecodeArgs()
+        args.batch_size, args.steps, args.beam_size, args.vocab_size = B, 1, K, V
+        args.eos_token, args.min_length, args.length_penalty_alpha = eos_token, min_length, alpha
+        args.repetition_penalty = 1.0
+        args.beam_sizes_per_example = _abi.ptr(per_example["beams"])
+        args.eos_tokens_per_example = _abi.ptr(per_example["eos"])
+        args.min_lengths_per_example = _abi.ptr(per_example["min"])
+        opts = _abi.SearchOptions()
+        opts.extra_eos_count = len(extra_eos)
+        for i, v in enumerate(extra_eos):
+            opts.extra_eos_tokens[i] = int(v)
+        state = _abi.BeamState(_abi.ptr(raw), _abi.ptr(lengths), _abi.ptr(finished), None, 0, 0)
+        ws_bytes = self.lib.dbs_cuda_decode_step_workspace_size(C.byref(args), 0)
+        assert ws_bytes > 0
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        names = ("tokens", "parents", "lengths", "scores", "raw_scores", "from_logprob")
+        trace = {n: [] for n in names}
+        final = torch.empty(B, K, dtype=torch.float32, device=dev)
+        for t in range(T):
+            out = {"tokens": torch.empty(B, K, dtype=torch.int32, device=dev),
+                   "parents": torch.empty(B, K, dtype=torch.int32, device=dev),
+                   "lengths": torch.empty(B, K, dtype=torch.int32, device=dev),
+                   "scores": torch.empty(B, K, dtype=torch.float32, device=dev),
+                   "raw_scores": torch.empty(B, K, dtype=torch.float32, device=dev),
+                   "from_logprob": torch.empty(B, K, dtype=torch.uint8, device=dev)}
+            o = _abi.DecodeOutputs(_abi.ptr(final), None, None, _abi.ptr(out["tokens"]), _abi.ptr(out["parents"]),
+                                   _abi.ptr(out["lengths"]), _abi.ptr(out["scores"]), _abi.ptr(out["raw_scores"]),
+                                   _abi.ptr(out["from_logprob"]), None)
+            rows = x[:, t].contiguous()
+            status = self.lib.dbs_cuda_decode_step_ex2(
+                _abi.ptr(rows), _abi.DTYPE[dtype], int(from_logits), C.byref(args), C.byref(opts), C.byref(state),
+                C.byref(o), None, _abi.ptr(ws), ws_bytes, self.stream())
+            assert status == _abi.STATUS_OK, self.lib.dbs_cuda_status_string(status)
+            torch.cuda.synchronize()
+            for n in names:
+                trace[n].append(out[n].cpu().numpy())
+        res = {n: np.stack(v, 1) for n, v in trace.items()}
+        res["final_scores"] = final.cpu().numpy()
+        res["final_raw_scores"] = raw.cpu().numpy()
+        res["final_lengths"] = lengths.cpu().numpy()
+        return res

@@ -51,6 +51,34 @@ def test_decode_matches_reference_library(oracle, seed):
 
 
 @needs_ref
+@pytest.mark.parametrize("seed", range(0, 24))
+def test_per_example_options_match_reference_variable_batch(oracle, seed):
+    """Oracle.decode_per_example (each example alone on its first beams[b]
+    rows, slots past them empty) against the reference library's
+    dbs_decode_batch_variable (float32 rows, per-example steps, beams, EOS
+    tokens, minimum lengths)."""
+    rng = np.random.default_rng(seed)
+    B, T = int(rng.integers(1, 6)), int(rng.integers(1, 8))
+    K, V = int(rng.choice([1, 2, 4, 7])), int(rng.choice([3, 13, 40, 300]))
+    x = log_softmax(rng.normal(0, 2.0, (B, T, K, V)).astype(np.float32))
+    if rng.random() < 0.5:
+        x[rng.random(x.shape) < 0.05] = x.reshape(-1)[0]  # ties
+    beams = [int(v) for v in rng.integers(1, K + 1, B)]
+    eos = [int(v) for v in rng.integers(0, V, B)] if rng.random() < 0.7 else [int(v) for v in rng.integers(-1, V, B)]
+    mins = [int(v) for v in rng.integers(0, 5, B)]
+    steps = [int(v) for v in rng.integers(1, T + 1, B)] if rng.random() < 0.5 else None
+    # the reference library's extra EOS tokens need an EOS token for every example
+    extra = tuple(int(v) for v in rng.integers(0, V, 2)) if min(eos) >= 0 and rng.random() < 0.5 else ()
+    alpha = float(rng.choice([0.0, 0.6, 1.0]))
+    want = Reference().decode_variable(x, beam_size=K, beams=beams, eos_tokens=eos, min_lengths=mins, steps=steps,
+                                       eos_token=0, extra_eos=extra, alpha=alpha)
+    got = oracle.decode_per_example(x, dtype="f32", beams=beams, eos_tokens=eos, min_lengths=mins, steps=steps,
+                                    extra_eos=extra, alpha=alpha)
+    keys = ("final_scores", "final_raw_scores", "tokens", "parents", "lengths", "scores", "raw_scores")
+    assert first_difference(got, want, keys) is None
+
+
+@needs_ref
 @pytest.mark.parametrize("seed", range(0, 30))
 def test_invalid_flags_match_reference_validation(oracle, seed):
     """The reference rejects (validate_inputs) exactly the examples the oracle flags."""
