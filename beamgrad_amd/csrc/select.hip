@@ -118,10 +118,23 @@ __device__ __forceinline__ PrefixView prefix_of(const DecodeParams& p, const Lds
     return PrefixView{s.prefix + (static_cast<int64_t>(cur) * p.K + k) * p.prefix_cap, s.plen[cur * p.K + k]};
 }
 
+// Membership of v in a[0, n): eight independent loads in flight per round
+// (the list is in LDS or global memory; its latency, not its length, bounds
+// the scan).
 __device__ __forceinline__ bool in_list(const int32_t* a, int n, int v) {
-    for (int i = 0; i < n; ++i)
-        if (a[i] == v) return true;
-    return false;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+        int32_t t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = a[i + u];
+        bool hit = false;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) hit = hit | (t[u] == v);
+        if (hit) return true;
+    }
+    bool hit = false;
+    for (; i < n; ++i) hit = hit | (a[i] == v);
+    return hit;
 }
 
 // The candidate of token v (finite log-prob lp, statically allowed) in the
@@ -494,24 +507,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 cnt = M > 0 ? info.count : -1;
                 bound = info.bound;
                 s.nraw[k] = info.lse;  // the row's logsumexp, kept for a rescan
-                if (p.constrained && p.ngram > 1) {
-                    const PrefixView pre = prefix_of(p, s, b, k, cur);
-                    const int n = p.ngram;
-                    int nb = 0;
-                    int32_t* out = s.blk + static_cast<int64_t>(k) * p.prefix_cap;
-                    if (pre.len >= n - 1) {
-                        const int tail = pre.len - (n - 1);
-                        for (int i = 0; i + n <= pre.len; ++i) {
-                            bool same = true;
-                            for (int j = 0; j < n - 1 && same; ++j) same = pre.tok[i + j] == pre.tok[tail + j];
-                            if (same) out[nb++] = pre.tok[i + n - 1];
-                        }
-                    }
-                    s.nblk[k] = nb;
-                }
             }
             s.rcount[k] = cnt;
             s.rbound[k] = bound;
+            if (p.constrained && p.ngram > 1) s.nblk[k] = 0;
         }
         if (M > 0) {
             const ShortEntry* src = p.shortlist + trace0 * M;
@@ -552,6 +551,27 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             }
         }
         __syncthreads();
+        if (p.constrained && p.ngram > 1) {
+            // n-gram blocking (reference src/decoder.cpp:196-230): for each
+            // read beam, the tokens that followed an earlier occurrence of its
+            // last n - 1 tokens; one thread per (beam, prefix position), the
+            // list in any order (it is only searched)
+            const int n = p.ngram, P = p.prefix_cap;
+            for (int item = tid; item < K * P; item += kSelectThreads) {
+                const int k = item / P, i = item - k * P;
+                if (s.rcount[k] == -2) continue;
+                const PrefixView pre = prefix_of(p, s, b, k, cur);
+                if (i + n > pre.len) continue;
+                const int tail = pre.len - (n - 1);
+                bool same = true;
+                for (int j = 0; j < n - 1; ++j) same = same & (pre.tok[i + j] == pre.tok[tail + j]);
+                if (same) {
+                    const int slot = atomicAdd(&s.nblk[k], 1);
+                    s.blk[static_cast<int64_t>(k) * P + slot] = pre.tok[i + n - 1];
+                }
+            }
+            __syncthreads();
+        }
         if (p.use_tau) {
             // Lower bounds of the K-th best expanded raw (unconstrained: raw =
             // fl(p + lp), monotone in lp; every beam expanded has the same
