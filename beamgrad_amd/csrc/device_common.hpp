@@ -220,7 +220,8 @@ constexpr int kRankSurvivors = 128;  // up to this many survivors are placed by 
 // b), which are dropped here (key 0 sorts last).
 template <bool LOGITS, bool FILTER>
 __device__ void finish_row_wave(const DecodeParams& p, int64_t r, float lse, float theta, bool any_bad,
-                                uint64_t* s_key, float* s_x, int n, int lane, int b, bool mask_eos) {
+                                uint64_t* s_key, float* s_x, int n, int lane, int b, bool mask_eos,
+                                bool signal = true) {
     const int M = p.M;
     const bool coherent = p.step_done != nullptr;
     RowInfo info;
@@ -328,7 +329,7 @@ __device__ void finish_row_wave(const DecodeParams& p, int64_t r, float lse, flo
 #pragma unroll
         for (int i = 0; i < 4; ++i) store_shared(dst + i, w[i], coherent);
     }
-    signal_row_done(p, r, lane);
+    if (signal) signal_row_done(p, r, lane);  // else the caller signals later
 }
 
 }  // namespace dbs_hip

@@ -57,6 +57,25 @@ DBS_HD float exp_nonpositive(float x) {
     return p * bits_f32(static_cast<uint32_t>(static_cast<int>(k) + 127) << 23);
 }
 
+// exp_nonpositive without branches: the same operations on max(x, -87),
+// then 0 below -87 (and for NaN).
+DBS_HD float exp_nonpositive_nb(float x) {
+    const bool in = x >= -87.0f;
+    const float xc = in ? x : -87.0f;
+    const float k = __builtin_floorf(xc * 1.44269504088896341f + 0.5f);
+    const float r = (xc - k * 0.693359375f) - k * -2.12194440e-4f;
+    const float r2 = r * r;
+    float p = 1.9875691500e-4f;
+    p = p * r + 1.3981999507e-3f;
+    p = p * r + 8.3334519073e-3f;
+    p = p * r + 4.1665795894e-2f;
+    p = p * r + 1.6666665459e-1f;
+    p = p * r + 5.0000001201e-1f;
+    p = (p * r2 + r) + 1.0f;
+    const float e = p * bits_f32(static_cast<uint32_t>(static_cast<int>(k) + 127) << 23);
+    return in ? e : 0.0f;
+}
+
 // ln(x), x >= 1, in double.
 DBS_HD double log_ge1(double x) {
     int e = 0;

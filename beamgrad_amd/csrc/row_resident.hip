@@ -117,9 +117,12 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
     }
     __syncthreads();
 
-    // Wavefront 0 finishes row r (lane tree, shortlist, RowInfo) after it has
-    // queued the first loads of the next row, so the loads cover it.
-    bool pend = false;
+    // Wavefront kFinisher (the first of segment 1) finishes row r (lane tree,
+    // shortlist, RowInfo) at the start of the next row, while its part of
+    // that row is still arriving; it signals the row done (overlapped
+    // decode: a wait for its stores) once that part has landed.
+    constexpr int kFinisher = 4;
+    bool pend = false, pend_signal = false;
     int64_t pend_r = 0;
     float pend_m = 0.0f, pend_theta = 0.0f;
     bool pend_bad = false, pend_lse = false, pend_mask = false, pend_full = false;
@@ -137,10 +140,12 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             }
         }
         const int n = pend_full ? kSurvivorCap + 1 : *s_count;
-        finish_row_wave<LOGITS, true>(p, pend_r, lse, pend_theta, pend_bad, s_key, s_x, n, l, pend_b, pend_mask);
+        finish_row_wave<LOGITS, true>(p, pend_r, lse, pend_theta, pend_bad, s_key, s_x, n, l, pend_b, pend_mask,
+                                      false);
         wave_sync();
         if (l == 0) *s_count = 0;
         pend = false;
+        pend_signal = true;
     };
 
     // byte offset in the segment of this lane's 16 bytes of chunk 0 (stripe
@@ -234,6 +239,7 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
         int V_r = V, jr = j, lr = l;
         asm volatile("" : "+s"(V_r));
         asm volatile("" : "+v"(jr), "+v"(lr));
+        if (wave == kFinisher && pend) finish_pending();
 
         // ---- the row's segment in registers (loaded during the previous
         // row, see issue_loads), transposed to lanes ----
@@ -277,9 +283,10 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
                 umax = pk_max_u16(umax, R);
             }
         }
-        // (wavefront 0 finishes the previous row now; segment 1's part of this
-        // row may still be arriving)
-        if (wave == 0 && pend) finish_pending();
+        if (wave == kFinisher && pend_signal) {
+            signal_row_done(p, pend_r, l);
+            pend_signal = false;
+        }
 
         // ---- row maximum, flag, group keys; the key histogram for theta ----
         // (keys: key16 of the largest pattern of a group, per half the largest
@@ -359,19 +366,20 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
         const bool do_lse = LOGITS && m > -kInf;
         const bool use_table = DT == 2 && do_lse && table_fits(m, ulo);
         if (use_table) {
+            // the 8192 slots, 16 per thread (slots tid + 512 i: the negative
+            // half from i = 8), evaluated without branches; slots past the
+            // row's range hold 0
             const uint32_t mp = f32_bits(m) >> 16;
-            for (int s = tid; s < 2 * kLutHalf; s += kResThreads) {
-                const bool neg = s >= kLutHalf;
-                const int k = s & (kLutHalf - 1);
-                float term = 0.0f;
-                if (k == 0) {
-                    term = exp_nonpositive(-m);
-                } else {
-                    const int u = ulo - 1 + k;
-                    if (u < 0x7f80 && (neg || u <= static_cast<int>(mp)))
-                        term = exp_nonpositive(bf16_to_f32(static_cast<uint16_t>((neg ? 0x8000 : 0) | u)) - m);
-                }
-                lut[s] = term;
+            const float em = exp_nonpositive(-m);
+#pragma unroll
+            for (int i = 0; i < 2 * kLutHalf / kResThreads; ++i) {
+                const bool neg = i >= kLutHalf / kResThreads;
+                const int k = tid + kResThreads * (i % (kLutHalf / kResThreads));
+                const int u = ulo - 1 + k;
+                const bool valid = u < 0x7f80 && (neg || u <= static_cast<int>(mp));
+                const float x = bf16_to_f32(static_cast<uint16_t>((neg ? 0x8000 : 0) | (valid ? u : 0)));
+                const float t = exp_nonpositive_nb(x - m);
+                lut[(neg ? kLutHalf : 0) + k] = k == 0 ? em : (valid ? t : 0.0f);
             }
         }
         lds_barrier();
@@ -407,23 +415,43 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
                 }
             }
         }
+        // Their elements, re-read from the row (in cache): the loads of up to
+        // four marked registers are in flight at once, then each element
+        // reaching theta goes to the LDS list (banned and masked tokens are
+        // dropped when the row is finished).
         auto push_hits = [&]() {
 #pragma unroll
             for (int w = 0; w < (kResRegs + 31) / 32; ++w) {
                 uint32_t bits = hm[w];
                 while (bits != 0u) {
-                    const int k = 32 * w + __builtin_ctz(bits);
-                    bits &= bits - 1u;
+                    int ks[4];
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const int v = 256 * (s_begin + 2 * k + h) + j;
-                        const float x = v < V ? load_one<DT>(row, v) : -kInf;
-                        if (x >= theta && x < kInf && x > -kInf) {
-                            // banned / EOS-below-min_length tokens are dropped when the row is finished
-                            const int slot = atomicAdd(s_count, 1);
-                            if (slot < kSurvivorCap) {
-                                s_key[slot] = survivor_key(x, v);
-                                s_x[slot] = x;
+                    for (int u = 0; u < 4; ++u) {
+                        ks[u] = bits != 0u ? 32 * w + __builtin_ctz(bits) : -1;
+                        bits &= bits - 1u;
+                    }
+                    float xs[8];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const int v = 256 * (s_begin + 2 * ks[u] + h) + j;
+                            const bool ok = ks[u] >= 0 && v < V;
+                            const float xv = load_one<DT>(row, ok ? v : 0);  // in bounds either way
+                            xs[2 * u + h] = ok ? xv : -kInf;
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const float x = xs[2 * u + h];
+                            if (x >= theta && x < kInf && x > -kInf) {
+                                const int slot = atomicAdd(s_count, 1);
+                                if (slot < kSurvivorCap) {
+                                    s_key[slot] = survivor_key(x, 256 * (s_begin + 2 * ks[u] + h) + j);
+                                    s_x[slot] = x;
+                                }
                             }
                         }
                     }
@@ -507,7 +535,7 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
         if (!loaded) issue_loads(next_row());
         lds_barrier();
 
-        if (wave == 0) {
+        if (wave == kFinisher) {
             pend = true;
             pend_r = r;
             pend_m = m;
@@ -527,7 +555,8 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             new_len = lenn;
         }
     }
-    if (wave == 0 && pend) finish_pending();
+    if (wave == kFinisher && pend) finish_pending();
+    if (wave == kFinisher && pend_signal) signal_row_done(p, pend_r, l);
 }
 
 int g_cu_count[64];
