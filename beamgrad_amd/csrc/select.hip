@@ -52,6 +52,7 @@ constexpr int kRescanBuf = 512;   // candidates of one rescanned row kept before
 constexpr int kRescanPerThread = 16;
 constexpr int kTauHead = 2;       // entries per row behind the second tau bound
 constexpr int kWideBeam = 16;     // beams from which the wide-beam paths pay off
+constexpr int kPfRegs = 12;       // 16-byte prefetch registers per thread (K * M <= 6144)
 
 struct Lds {
     Cand* buf;        // [sort_cap] the collector
@@ -386,7 +387,10 @@ __device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State&
     }
 }
 
-template <int DT, bool LOGITS>
+// PF: the next step's RowInfo and shortlists are prefetched into registers
+// (chosen on the host: prefetch_fits); a separate instantiation, so the other
+// paths keep their register budget.
+template <int DT, bool LOGITS, bool PF>
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, SelectLayout L) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ State st;
@@ -456,6 +460,25 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     }
     __syncthreads();
 
+    // Prefetch (the row pass has finished before this kernel: not the
+    // overlapped decode): the next step's RowInfo and shortlists sit at fixed
+    // addresses (rows (b, t + 1, k) of every slot), so their loads are issued
+    // into registers as soon as a step's own are staged, and land while the
+    // step runs.
+    constexpr int kPf = PF ? kPfRegs : 1;
+    uint4 pf_sl[kPf];
+    uint4 pf_info = make_uint4(0u, 0u, 0u, 0u);
+    bool have_pf = false;
+    auto prefetch = [&](int t_next) {
+        const int64_t base = (static_cast<int64_t>(b) * T + t_next) * K;
+        if (tid < K) pf_info = reinterpret_cast<const uint4*>(p.rowinfo)[base + tid];
+        const uint4* src4 = reinterpret_cast<const uint4*>(p.shortlist + base * M);
+        const int n4 = K * M / 2;
+#pragma unroll
+        for (int u = 0; u < kPf; ++u)
+            if (tid + u * kSelectThreads < n4) pf_sl[u] = src4[tid + u * kSelectThreads];
+    };
+
     int cur = 0;
     for (int t = 0; t < T_loop; ++t) {
         const int64_t trace0 = (static_cast<int64_t>(b) * T + t) * K;  // step mode: T == 1
@@ -493,7 +516,9 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             float bound = -kInf;
             if (live && !carried) {
                 RowInfo info;
-                if (!coherent) {
+                if (have_pf) {
+                    __builtin_memcpy(&info, &pf_info, sizeof(info));  // k == tid
+                } else if (!coherent) {
                     info = p.rowinfo[trace0 + k];
                 } else {
                     uint32_t w[4];
@@ -512,7 +537,19 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             s.rbound[k] = bound;
             if (p.constrained && p.ngram > 1) s.nblk[k] = 0;
         }
-        if (M > 0) {
+        if (have_pf) {
+            const int n4 = K * M / 2;
+#pragma unroll
+            for (int u = 0; u < kPf; ++u) {
+                const int q = tid + u * kSelectThreads;
+                if (q < n4) {
+                    const int k = (2 * q) / M, i = 2 * q - k * M;
+                    uint2* dst = reinterpret_cast<uint2*>(s.sl + sl_at(k, i, SL));
+                    dst[0] = make_uint2(pf_sl[u].x, pf_sl[u].y);
+                    dst[1] = make_uint2(pf_sl[u].z, pf_sl[u].w);
+                }
+            }
+        } else if (M > 0) {
             const ShortEntry* src = p.shortlist + trace0 * M;
             if (!coherent && (M & 1) == 0 && K * M >= kWideBeam * 16) {
                 // 16-byte loads (two entries of one row: with M even the rows'
@@ -549,6 +586,11 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                     s.sl[SL == M ? i : sl_at(i / M, i % M, SL)] = e;
                 }
             }
+        }
+        // this step's rows are staged: the next step's loads go out now
+        if constexpr (PF) {
+            have_pf = t + 1 < steps_b;
+            if (have_pf) prefetch(t + 1);
         }
         __syncthreads();
         if (p.constrained && p.ngram > 1) {
@@ -804,16 +846,30 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     if (tid == 0 && p.invalid) p.invalid[b] = static_cast<uint8_t>(st.invalid != 0);
 }
 
-template <int DT, bool LOGITS>
-hipError_t launch_select_typed(const DecodeParams& p, const SelectLayout& L, hipStream_t stream) {
+// The prefetch needs the row pass finished before the select pass starts (not
+// the overlapped decode, whose rows land while it runs) and a step's
+// shortlists within the prefetch registers, as 16-byte pairs of entries.
+bool prefetch_fits(const DecodeParams& p) {
+    return p.step_done == nullptr && !p.step_mode && p.M > 0 && (p.M & 1) == 0 && p.K <= kSelectThreads &&
+           p.K * p.M <= 2 * kPfRegs * kSelectThreads;
+}
+
+template <int DT, bool LOGITS, bool PF>
+hipError_t launch_select_variant(const DecodeParams& p, const SelectLayout& L, hipStream_t stream) {
     if (L.smem > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<DT, LOGITS>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<DT, LOGITS, PF>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L.smem));
         if (e != hipSuccess) return e;
     }
     KernelTimer timer(kKindSelect, stream);
-    hipLaunchKernelGGL((select_kernel<DT, LOGITS>), dim3(p.B), dim3(kSelectThreads), L.smem, stream, p, L);
+    hipLaunchKernelGGL((select_kernel<DT, LOGITS, PF>), dim3(p.B), dim3(kSelectThreads), L.smem, stream, p, L);
     return hipGetLastError();
+}
+
+template <int DT, bool LOGITS>
+hipError_t launch_select_typed(const DecodeParams& p, const SelectLayout& L, hipStream_t stream) {
+    return prefetch_fits(p) ? launch_select_variant<DT, LOGITS, true>(p, L, stream)
+                            : launch_select_variant<DT, LOGITS, false>(p, L, stream);
 }
 
 }  // namespace
