@@ -186,22 +186,46 @@ __device__ __forceinline__ float shortlist_threshold(float (&a)[4], int lane, in
     return __shfl(mine, idx >> 2);
 }
 
+// lane + d's value of v for the lanes < d (d = 1, 2, 4, 8: DPP row shifts;
+// 16, 32: the gfx950 permlane swaps), without a trip through the LDS;
+// other lanes get unspecified values.
+template <int D>
+__device__ __forceinline__ float from_lane_above(float v) {
+    const int u = static_cast<int>(f32_bits(v));
+    int r;
+    if constexpr (D == 32) {
+        r = static_cast<int>(__builtin_amdgcn_permlane32_swap(u, u, false, false)[1]);
+    } else if constexpr (D == 16) {
+        r = static_cast<int>(__builtin_amdgcn_permlane16_swap(u, u, false, false)[1]);
+    } else {
+        static_assert(D == 1 || D == 2 || D == 4 || D == 8, "row shift");
+        r = __builtin_amdgcn_update_dpp(0, u, 0x100 + D, 0xf, 0xf, false);  // row_shl:D
+    }
+    return bits_f32(static_cast<uint32_t>(r));
+}
+
 // Combination of the 256 logsumexp lane sums held 4 per lane (lane j = 4 *
 // lane + e), pairwise with strides 128, 64, ..., 1: lane j += lane j + s
-// (reference src/kernels.hpp:196-202).
-__device__ __forceinline__ float lane_tree_sum(float (&acc)[4], int lane) {
-    for (int s = 128; s >= 4; s >>= 1) {
-        const int d = s >> 2;
+// (reference src/kernels.hpp:196-202). The whole wavefront calls it.
+template <int D>
+__device__ __forceinline__ void lane_tree_step(float (&acc)[4], int lane) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float other = __shfl_down(acc[e], d);
-            if (4 * lane + e < s) acc[e] = acc[e] + other;
-        }
+    for (int e = 0; e < 4; ++e) {
+        const float other = from_lane_above<D>(acc[e]);
+        if (lane < D) acc[e] = acc[e] + other;  // 4 lane + e < 4 D
     }
+}
+__device__ __forceinline__ float lane_tree_sum(float (&acc)[4], int lane) {
+    lane_tree_step<32>(acc, lane);
+    lane_tree_step<16>(acc, lane);
+    lane_tree_step<8>(acc, lane);
+    lane_tree_step<4>(acc, lane);
+    lane_tree_step<2>(acc, lane);
+    lane_tree_step<1>(acc, lane);
     acc[0] = acc[0] + acc[2];
     acc[1] = acc[1] + acc[3];
     acc[0] = acc[0] + acc[1];
-    return __shfl(acc[0], 0);
+    return bits_f32(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(f32_bits(acc[0])), 0)));
 }
 
 // Survivor key: value descending, then token ascending.
