@@ -108,6 +108,8 @@ SIGNATURES = {
                                          C.c_void_p, C.c_int64, C.c_void_p]),
     "dbs_hip_backtrack": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                     C.c_void_p]),
+    "dbs_hip_backtrack_i64": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                        C.c_void_p]),
     "dbs_hip_profile_enable": (C.c_int, [C.c_int]),
     "dbs_hip_profile_read": (C.c_int, [C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
     "dbs_hip_set_row_pass": (C.c_int, [C.c_int]),

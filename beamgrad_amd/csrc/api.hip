@@ -627,4 +627,15 @@ DBS_CUDA_EXPORT int dbs_hip_backtrack(const int32_t* tokens, const int32_t* pare
                   launch_backtrack(tokens, parents, steps_per_example, batch_size, steps, beam_size, sequences, stream));
 }
 
+DBS_CUDA_EXPORT int dbs_hip_backtrack_i64(const int64_t* tokens, const int64_t* parents,
+                                          const int64_t* steps_per_example, int batch_size, int steps, int beam_size,
+                                          int64_t* sequences, void* stream_ptr) {
+    if (!tokens || !parents || !sequences || batch_size <= 0 || steps <= 0 || beam_size <= 0 ||
+        beam_size > DBS_CUDA_MAX_BEAM)
+        return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    return finish(stream,
+                  launch_backtrack(tokens, parents, steps_per_example, batch_size, steps, beam_size, sequences, stream));
+}
+
 }  // extern "C"

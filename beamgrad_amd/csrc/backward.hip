@@ -301,10 +301,12 @@ hipError_t launch_dense_ot(const BackwardParams& p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-__global__ void backtrack_kernel(const int32_t* tokens, const int32_t* parents, const int32_t* steps, int T, int K,
-                                 int64_t* seq) {
+// I: the index type of tokens, parents and steps (int32, or int64 as torch
+// hands the trace to the caller).
+template <typename I>
+__global__ void backtrack_kernel(const I* tokens, const I* parents, const I* steps, int T, int K, int64_t* seq) {
     const int b = static_cast<int>(blockIdx.x);
-    const int steps_b = steps ? steps[b] : T;
+    const int64_t steps_b = steps ? static_cast<int64_t>(steps[b]) : T;
     for (int k = static_cast<int>(threadIdx.x); k < K; k += static_cast<int>(blockDim.x)) {
         int beam = k;
         int64_t* dst = seq + (static_cast<int64_t>(b) * K + k) * T;
@@ -314,9 +316,9 @@ __global__ void backtrack_kernel(const int32_t* tokens, const int32_t* parents, 
                 continue;
             }
             const int64_t slot = (static_cast<int64_t>(b) * T + t) * K + beam;
-            dst[t] = tokens[slot];
-            const int next = parents[slot];
-            beam = next < K ? next : -1;  // a malformed parent ends the path
+            dst[t] = static_cast<int64_t>(tokens[slot]);
+            const int64_t next = static_cast<int64_t>(parents[slot]);
+            beam = next >= 0 && next < K ? static_cast<int>(next) : -1;  // a malformed parent ends the path
         }
     }
 }
@@ -342,12 +344,23 @@ hipError_t launch_dense_gradient(const BackwardParams& p, hipStream_t stream) {
     }
 }
 
-hipError_t launch_backtrack(const int32_t* tokens, const int32_t* parents, const int32_t* steps, int B, int T, int K,
-                            int64_t* seq, hipStream_t stream) {
+template <typename I>
+hipError_t launch_backtrack_t(const I* tokens, const I* parents, const I* steps, int B, int T, int K, int64_t* seq,
+                              hipStream_t stream) {
     const int threads = K < 256 ? ((K + 63) / 64) * 64 : 256;
     KernelTimer timer(kKindBacktrack, stream);
-    hipLaunchKernelGGL(backtrack_kernel, dim3(B), dim3(threads), 0, stream, tokens, parents, steps, T, K, seq);
+    hipLaunchKernelGGL((backtrack_kernel<I>), dim3(B), dim3(threads), 0, stream, tokens, parents, steps, T, K, seq);
     return hipGetLastError();
+}
+
+hipError_t launch_backtrack(const int32_t* tokens, const int32_t* parents, const int32_t* steps, int B, int T, int K,
+                            int64_t* seq, hipStream_t stream) {
+    return launch_backtrack_t(tokens, parents, steps, B, T, K, seq, stream);
+}
+
+hipError_t launch_backtrack(const int64_t* tokens, const int64_t* parents, const int64_t* steps, int B, int T, int K,
+                            int64_t* seq, hipStream_t stream) {
+    return launch_backtrack_t(tokens, parents, steps, B, T, K, seq, stream);
 }
 
 }  // namespace dbs_hip

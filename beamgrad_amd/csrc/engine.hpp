@@ -196,5 +196,7 @@ hipError_t launch_path_walk(const BackwardParams& p, hipStream_t stream);
 hipError_t launch_dense_gradient(const BackwardParams& p, hipStream_t stream);
 hipError_t launch_backtrack(const int32_t* tokens, const int32_t* parents, const int32_t* steps, int B, int T, int K,
                             int64_t* seq, hipStream_t stream);
+hipError_t launch_backtrack(const int64_t* tokens, const int64_t* parents, const int64_t* steps, int B, int T, int K,
+                            int64_t* seq, hipStream_t stream);
 
 }  // namespace dbs_hip

@@ -66,6 +66,20 @@ DBS_CUDA_EXPORT int dbs_hip_backtrack(
     int64_t* sequences,
     void* stream);
 
+/* dbs_hip_backtrack with int64 tokens, parents and steps_per_example (the
+ * dtype torch hands the trace to the caller in), so the caller converts
+ * nothing before the launch. No counterpart in the reference (its backtrack
+ * is the torch loop named above). */
+DBS_CUDA_EXPORT int dbs_hip_backtrack_i64(
+    const int64_t* tokens,
+    const int64_t* parents,
+    const int64_t* steps_per_example,
+    int batch_size,
+    int steps,
+    int beam_size,
+    int64_t* sequences,
+    void* stream);
+
 /* Launch timing for measurement tools (no counterpart in the reference).
  * With profiling on, every kernel the library launches is bracketed by HIP
  * events on the caller's stream, and its duration is summed per kernel kind:

@@ -193,6 +193,18 @@ class HipEngine:
         torch.cuda.synchronize()
         return out.cpu().numpy()
 
+    def backtrack_i64(self, tokens, parents, steps=None) -> np.ndarray:
+        tok = _dev(np.asarray(tokens, np.int64))
+        par = _dev(np.asarray(parents, np.int64))
+        st = _dev(None if steps is None else np.asarray(steps, np.int64))
+        B, T, K = tok.shape
+        out = torch.full((B, K, T), 9, dtype=torch.int64, device="cuda")
+        status = self.lib.dbs_hip_backtrack_i64(_abi.ptr(tok), _abi.ptr(par), _abi.ptr(st), B, T, K, _abi.ptr(out),
+                                                self.stream())
+        assert status == _abi.STATUS_OK
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
     # ------------------------------------------------------------------
     def steps(self, xin: np.ndarray, dtype: str, *, from_logits=False, eos_token=-1, extra_eos=(), min_length=0,
               alpha=0.0, beams=None, eos_tokens=None, min_lengths=None) -> dict:

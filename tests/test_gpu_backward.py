@@ -135,6 +135,7 @@ def test_backtrack_matches_oracle(hip, oracle, seed):
     got = hip.backtrack(tr["tokens"], tr["parents"], kw["steps"])
     want = oracle.backtrack(tr["tokens"], tr["parents"], kw["steps"])
     assert np.array_equal(got, want)
+    assert np.array_equal(hip.backtrack_i64(tr["tokens"], tr["parents"], kw["steps"]), want)
     # the path of every live final beam reproduces its raw score (reference
     # python/tests/test_api.py:118-133), checked in float64 on expanded slots
     assert got.shape == (case["B"], case["K"], case["T"])
