@@ -172,7 +172,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build's hot path runs on a single MI355X "
-              "(examples shard over GPUs with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(examples are independent and would shard over GPUs with no exchange). Run with --gpus 1.",
+              file=sys.stderr)
         return 2
 
     import beamgrad_amd as bg
