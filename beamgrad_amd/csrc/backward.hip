@@ -302,11 +302,26 @@ hipError_t launch_dense_ot(const BackwardParams& p, hipStream_t stream) {
 }
 
 // I: the index type of tokens, parents and steps (int32, or int64 as torch
-// hands the trace to the caller).
-template <typename I>
+// hands the trace to the caller). STAGED: the example's tokens and parents
+// are first copied into LDS by the whole workgroup (coalesced), so each
+// beam's walk back through the steps reads the LDS instead of waiting on one
+// dependent global load per step.
+template <typename I, bool STAGED>
 __global__ void backtrack_kernel(const I* tokens, const I* parents, const I* steps, int T, int K, int64_t* seq) {
+    extern __shared__ __align__(16) unsigned char smem[];
     const int b = static_cast<int>(blockIdx.x);
     const int64_t steps_b = steps ? static_cast<int64_t>(steps[b]) : T;
+    const int64_t base = static_cast<int64_t>(b) * T * K;
+    int64_t* s_tok = reinterpret_cast<int64_t*>(smem);
+    int32_t* s_par = reinterpret_cast<int32_t*>(smem + sizeof(int64_t) * static_cast<size_t>(T) * K);
+    if constexpr (STAGED) {
+        for (int i = static_cast<int>(threadIdx.x); i < T * K; i += static_cast<int>(blockDim.x)) {
+            s_tok[i] = static_cast<int64_t>(tokens[base + i]);
+            const int64_t next = static_cast<int64_t>(parents[base + i]);
+            s_par[i] = next >= 0 && next < K ? static_cast<int32_t>(next) : -1;
+        }
+        __syncthreads();
+    }
     for (int k = static_cast<int>(threadIdx.x); k < K; k += static_cast<int>(blockDim.x)) {
         int beam = k;
         int64_t* dst = seq + (static_cast<int64_t>(b) * K + k) * T;
@@ -315,10 +330,15 @@ __global__ void backtrack_kernel(const I* tokens, const I* parents, const I* ste
                 dst[t] = -1;
                 continue;
             }
-            const int64_t slot = (static_cast<int64_t>(b) * T + t) * K + beam;
-            dst[t] = static_cast<int64_t>(tokens[slot]);
-            const int64_t next = static_cast<int64_t>(parents[slot]);
-            beam = next >= 0 && next < K ? static_cast<int>(next) : -1;  // a malformed parent ends the path
+            const int64_t slot = static_cast<int64_t>(t) * K + beam;
+            if constexpr (STAGED) {
+                dst[t] = s_tok[slot];
+                beam = s_par[slot];
+            } else {
+                dst[t] = static_cast<int64_t>(tokens[base + slot]);
+                const int64_t next = static_cast<int64_t>(parents[base + slot]);
+                beam = next >= 0 && next < K ? static_cast<int>(next) : -1;  // a malformed parent ends the path
+            }
         }
     }
 }
@@ -349,7 +369,14 @@ hipError_t launch_backtrack_t(const I* tokens, const I* parents, const I* steps,
                               hipStream_t stream) {
     const int threads = K < 256 ? ((K + 63) / 64) * 64 : 256;
     KernelTimer timer(kKindBacktrack, stream);
-    hipLaunchKernelGGL((backtrack_kernel<I>), dim3(B), dim3(threads), 0, stream, tokens, parents, steps, T, K, seq);
+    const size_t staged = (sizeof(int64_t) + sizeof(int32_t)) * static_cast<size_t>(T) * static_cast<size_t>(K);
+    if (staged <= 48 * 1024) {
+        hipLaunchKernelGGL((backtrack_kernel<I, true>), dim3(B), dim3(threads), staged, stream, tokens, parents, steps,
+                           T, K, seq);
+    } else {
+        hipLaunchKernelGGL((backtrack_kernel<I, false>), dim3(B), dim3(threads), 0, stream, tokens, parents, steps, T,
+                           K, seq);
+    }
     return hipGetLastError();
 }
 

@@ -139,3 +139,18 @@ def test_backtrack_matches_oracle(hip, oracle, seed):
     # the path of every live final beam reproduces its raw score (reference
     # python/tests/test_api.py:118-133), checked in float64 on expanded slots
     assert got.shape == (case["B"], case["K"], case["T"])
+
+
+@pytest.mark.parametrize("T", [5, 700])  # the trace staged in LDS, and too long for it
+def test_backtrack_random_traces(hip, oracle, T):
+    """Arbitrary parent pointers (dead ones -1) and per-example steps: the
+    int32 and int64 entry points follow them as the oracle does."""
+    rng = np.random.default_rng(77 + T)
+    B, K = 3, 8
+    tokens = rng.integers(0, 50000, size=(B, T, K))
+    parents = rng.integers(-1, K, size=(B, T, K))
+    steps = np.array([T, max(1, T // 2), 1])
+    for st in (None, steps):
+        want = oracle.backtrack(tokens, parents, st)
+        assert np.array_equal(hip.backtrack(tokens, parents, st), want)
+        assert np.array_equal(hip.backtrack_i64(tokens, parents, st), want)
