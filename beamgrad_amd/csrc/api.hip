@@ -84,18 +84,17 @@ KernelTimer::~KernelTimer() {
 
 namespace {
 
-std::atomic<int> g_sync{-1};
+// dbs_cuda_set_synchronization's flag; the environment can also ask for a
+// synchronisation after every call (DBS_CUDA_SYNC_CHECK=1, or the legacy
+// DBS_CUDA_DEBUG_SYNC=1), read on every call as the reference does
+// (reference cuda/dbs_cuda.cu:1226-1231).
+std::atomic<int> g_sync{0};
 
-int sync_flag() {
-    int s = g_sync.load(std::memory_order_relaxed);
-    if (s < 0) {
-        const char* env = std::getenv("DBS_CUDA_SYNC_CHECK");
-        s = (env && env[0] == '1') ? 1 : 0;
-        int expected = -1;
-        g_sync.compare_exchange_strong(expected, s);
-        s = g_sync.load(std::memory_order_relaxed);
-    }
-    return s;
+bool sync_requested() {
+    if (g_sync.load(std::memory_order_relaxed) != 0) return true;
+    const char* v = std::getenv("DBS_CUDA_SYNC_CHECK");
+    const char* legacy = std::getenv("DBS_CUDA_DEBUG_SYNC");
+    return (v && v[0] == '1') || (legacy && legacy[0] == '1');
 }
 
 int status_of(hipError_t e) {
@@ -106,9 +105,24 @@ int status_of(hipError_t e) {
 }
 
 int finish(hipStream_t stream, hipError_t e) {
-    if (e == hipSuccess && sync_flag() == 1) e = hipStreamSynchronize(stream);
+    if (e == hipSuccess && sync_requested()) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) (void)hipGetLastError();
     return status_of(e);
+}
+
+// finish() for a decode: when the call synchronises, an overlapped decode
+// whose select pass gave up a wait (fault word set) reports a failed launch;
+// asynchronous callers see it as invalid_input[b] == 2.
+int finish_decode(hipStream_t stream, hipError_t e, const int32_t* fault) {
+    if (e != hipSuccess || !sync_requested()) return finish(stream, e);
+    e = hipStreamSynchronize(stream);
+    int32_t host = 0;
+    if (e == hipSuccess && fault) e = hipMemcpy(&host, fault, sizeof(host), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return status_of(e);
+    }
+    return host != 0 ? DBS_CUDA_STATUS_LAUNCH_FAILED : DBS_CUDA_STATUS_OK;
 }
 
 bool valid_dtype(int d) { return d == DBS_CUDA_DTYPE_F32 || d == DBS_CUDA_DTYPE_F16 || d == DBS_CUDA_DTYPE_BF16; }
@@ -184,7 +198,8 @@ struct Scratch {
         stream = s;
         *too_small = false;
         if (ws) {
-            if (ws_bytes < static_cast<int64_t>(need)) {
+            // the workspace holds 16-byte words: it must be 16-byte aligned
+            if (ws_bytes < static_cast<int64_t>(need) || reinterpret_cast<uintptr_t>(ws) % 16 != 0) {
                 *too_small = true;
                 return hipSuccess;
             }
@@ -273,8 +288,9 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
         e = launch_fill_f32(row_lse, 0.0f, static_cast<int64_t>(a.batch_size) * a.steps * a.beam_size, stream);
         if (e != hipSuccess) return finish(stream, e);
     }
-    e = launch_decode(p, L, stream, ws);
-    return finish(stream, e);
+    int32_t* fault = nullptr;
+    e = launch_decode(p, L, stream, ws, &fault);
+    return finish_decode(stream, e, fault);
 }
 
 int step_common(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
@@ -344,8 +360,9 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
         e = launch_fill_f32(row_lse, 0.0f, static_cast<int64_t>(a.batch_size) * a.beam_size, stream);
         if (e != hipSuccess) return finish(stream, e);
     }
-    e = launch_decode(p, L, stream, ws);
-    return finish(stream, e);
+    int32_t* fault = nullptr;
+    e = launch_decode(p, L, stream, ws, &fault);
+    return finish_decode(stream, e, fault);
 }
 
 int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, void* out, int out_type,
@@ -427,7 +444,7 @@ DBS_CUDA_EXPORT int dbs_cuda_set_synchronization(int synchronize) {
     return DBS_CUDA_STATUS_OK;
 }
 
-DBS_CUDA_EXPORT int dbs_cuda_get_synchronization(void) { return sync_flag(); }
+DBS_CUDA_EXPORT int dbs_cuda_get_synchronization(void) { return g_sync.load(std::memory_order_relaxed); }
 
 DBS_CUDA_EXPORT int64_t dbs_cuda_decode_workspace_size(const DBSCudaDecodeArgs* args) {
     if (!valid_args(args)) return -1;

@@ -31,6 +31,13 @@ __global__ void fill_f32_kernel(float* dst, float value, int64_t n) {
     for (int64_t j = i; j < n; j += stride) dst[j] = value;
 }
 
+// Zeroes n16 16-byte words.
+__global__ void clear_kernel(uint4* dst, int64_t n16) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t j = i; j < n16; j += stride) dst[j] = make_uint4(0u, 0u, 0u, 0u);
+}
+
 __global__ void length_penalty_kernel(const int32_t* lengths, int64_t n, float alpha, float* out) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -93,37 +100,73 @@ std::atomic<int> g_overlap{-1};
 
 namespace {
 
-// The second stream of the overlapped decode and its two events, per device
-// (default priority; created on first use, kept until the process ends).
+// The second stream of the overlapped decode and its two events, one set per
+// (device, caller stream): callers on different streams never share one, so
+// their decodes do not serialise. Default priority; created on first use and
+// kept until the process ends. At most kMaxAux per process; past that the
+// decode runs its passes one after the other on the caller's stream.
 struct Aux {
+    int device = -1;
+    hipStream_t caller = nullptr;
     hipStream_t stream = nullptr;
     hipEvent_t start = nullptr, done = nullptr;
     int cus = 0;
+    std::mutex mutex;  // one decode's enqueue sequence at a time on this pair
 };
-Aux g_aux[64];
-std::mutex g_aux_mutex;
+constexpr int kMaxAux = 64;
+Aux g_aux[kMaxAux];
+int g_aux_used = 0;
+std::mutex g_aux_mutex;  // guards the table, not the launches
 
-hipError_t aux_for(int device, Aux*& out) {
-    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
-    Aux& a = g_aux[device];
-    if (!a.stream) {
-        hipError_t e = hipDeviceGetAttribute(&a.cus, hipDeviceAttributeMultiprocessorCount, device);
-        if (e == hipSuccess) e = hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking);
-        if (e == hipSuccess) e = hipEventCreateWithFlags(&a.start, hipEventDisableTiming);
-        if (e == hipSuccess) e = hipEventCreateWithFlags(&a.done, hipEventDisableTiming);
-        if (e != hipSuccess) {
-            a.stream = nullptr;
-            return e;
+// The caller's Aux (created on first use), or null when the table is full.
+hipError_t aux_for(int device, hipStream_t caller, Aux*& out) {
+    out = nullptr;
+    std::lock_guard<std::mutex> lock(g_aux_mutex);
+    for (int i = 0; i < g_aux_used; ++i) {
+        if (g_aux[i].device == device && g_aux[i].caller == caller) {
+            out = &g_aux[i];
+            return hipSuccess;
         }
     }
+    if (g_aux_used == kMaxAux) return hipSuccess;
+    Aux& a = g_aux[g_aux_used];
+    hipError_t e = hipDeviceGetAttribute(&a.cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&a.start, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&a.done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        if (a.stream) (void)hipStreamDestroy(a.stream);
+        if (a.start) (void)hipEventDestroy(a.start);
+        a.stream = nullptr;
+        a.start = nullptr;
+        return e;
+    }
+    a.device = device;
+    a.caller = caller;
+    ++g_aux_used;
     out = &a;
     return hipSuccess;
+}
+
+// Bound of one select-pass wait: 2 s of the 100 MHz real-time counter. Test
+// knob DBS_HIP_TEST_WAIT_GIVE_UP=1: every wait needs one row more than the
+// row pass ever counts and gives up after 10 us, so the error path runs with
+// every kernel exiting normally.
+void wait_policy(DecodeParams& p) {
+    p.wait_ticks = 200000000ull;
+    p.wait_extra = 0;
+    const char* env = std::getenv("DBS_HIP_TEST_WAIT_GIVE_UP");
+    if (env && env[0] == '1') {
+        p.wait_ticks = 1000ull;
+        p.wait_extra = 1;
+    }
 }
 
 }  // namespace
 
 size_t sync_bytes(int B, int T) {
-    return ((sizeof(int32_t) * static_cast<size_t>(B) * static_cast<size_t>(T) + 7) & ~static_cast<size_t>(7)) +
+    // [B, T] step counts, the fault word (padded to 8 bytes), the row ticket
+    return ((sizeof(int32_t) * static_cast<size_t>(B) * static_cast<size_t>(T) + 7) & ~static_cast<size_t>(7)) + 8 +
            sizeof(unsigned long long);
 }
 
@@ -138,37 +181,58 @@ size_t sync_bytes(int B, int T) {
 // the B CUs they leave free (MI355X: C2 2.00 -> 1.89 ms, C5 forward 2.35 ->
 // 1.75 ms). The one-read log-prob kernel runs several workgroups per CU and
 // loses more than the overlap saves (C4 3.03 -> 3.58 ms), so it does not.
-hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStream_t stream, char* ws) {
+// *fault: the overlapped decode's fault word (non-zero once a select-pass
+// wait gave up), else null.
+hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStream_t stream, char* ws,
+                         int32_t** fault) {
     DecodeParams p = p0;
+    *fault = nullptr;
     int device = 0;
     hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess) return e;
-    std::lock_guard<std::mutex> lock(g_aux_mutex);
     Aux* aux = nullptr;
     const int mode = g_overlap.load(std::memory_order_relaxed);
     const bool want =
         !p.step_mode && p.T > 1 && (mode == 1 || (mode == -1 && (p.constrained || row_pass_persistent(p))));
     if (want) {
-        e = aux_for(device, aux);
+        e = aux_for(device, stream, aux);
         if (e != hipSuccess) return e;
     }
-    if (!want || 2 * p.B > aux->cus) {
+    if (!aux || 2 * p.B > aux->cus) {
         e = launch_row_pass(p, stream);
         if (e != hipSuccess) return e;
         return launch_select(p, L.sel, stream);
     }
     char* sync = ws + L.off_sync;
+    const size_t counts = (sizeof(int32_t) * static_cast<size_t>(p.B) * static_cast<size_t>(p.T) + 7) & ~static_cast<size_t>(7);
     p.step_done = reinterpret_cast<int32_t*>(sync);
-    p.row_ticket = reinterpret_cast<unsigned long long*>(sync + sync_bytes(p.B, p.T) - sizeof(unsigned long long));
+    p.fault = reinterpret_cast<int32_t*>(sync + counts);
+    p.row_ticket = reinterpret_cast<unsigned long long*>(sync + counts + 8);
     p.reserve_cus = p.B;  // a persistent row pass would otherwise hold every CU until it ends
-    e = launch_fill_f32(reinterpret_cast<float*>(sync), 0.0f, static_cast<int64_t>(sync_bytes(p.B, p.T) / 4), stream);
+    wait_policy(p);
+    std::lock_guard<std::mutex> lock(aux->mutex);
+    // the counters, and the RowInfo and shortlist words (tag 0: not written)
+    e = launch_clear(sync, sync_bytes(p.B, p.T), stream);
+    if (e == hipSuccess) e = launch_clear(ws + L.off_rowinfo, L.off_prefix - L.off_rowinfo, stream);
     if (e == hipSuccess) e = hipEventRecord(aux->start, stream);
     if (e == hipSuccess) e = launch_row_pass(p, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(aux->stream, aux->start, 0);
     if (e == hipSuccess) e = launch_select(p, L.sel, aux->stream);
     if (e == hipSuccess) e = hipEventRecord(aux->done, aux->stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(stream, aux->done, 0);
+    if (e == hipSuccess) *fault = p.fault;
     return e;
+}
+
+// Zeroes [dst, dst + bytes rounded up to 16); dst 16-byte aligned, the
+// rounded range inside the allocation.
+hipError_t launch_clear(void* dst, size_t bytes, hipStream_t stream) {
+    const int64_t n16 = static_cast<int64_t>((bytes + 15) / 16);
+    if (n16 <= 0) return hipSuccess;
+    const int64_t blocks = (n16 + 255) / 256;
+    hipLaunchKernelGGL(clear_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)), dim3(256), 0, stream,
+                       static_cast<uint4*>(dst), n16);
+    return hipGetLastError();
 }
 
 hipError_t launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream) {

@@ -119,23 +119,49 @@ __device__ __forceinline__ int64_t take_ticket(const DecodeParams& p, int64_t af
     return static_cast<int64_t>(__hip_atomic_fetch_add(p.row_ticket, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
-// Shared words of the overlapped decode (the row pass's RowInfo and
-// shortlists, read by the select pass while the row pass still runs) are
-// stored and loaded as device-scope atomics: coherent across the XCDs' L2
-// caches word by word, without whole-cache write-backs or invalidations.
-__device__ __forceinline__ void store_shared(uint32_t* dst, uint32_t v, bool coherent) {
-    if (coherent) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *dst = v;
-}
-__device__ __forceinline__ uint32_t load_shared(const uint32_t* src, bool coherent) {
-    return coherent ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *src;
+// Words of the overlapped decode (the row pass's RowInfo and shortlists, read
+// by the select pass while the row pass still runs) are 64-bit device-scope
+// atomics, each validated by its own tag (upper half non-zero once written,
+// over a cleared workspace): coherent across the XCDs' L2 caches word by
+// word, with no cache write-back or invalidation and no ordering between
+// words. Otherwise plain stores (the select pass starts after the row pass).
+__device__ __forceinline__ void publish_word(uint32_t* dst, uint32_t lo, uint32_t hi, bool coherent) {
+    if (coherent) {
+        const unsigned long long w = (static_cast<unsigned long long>(hi) << 32) | lo;
+        __hip_atomic_store(reinterpret_cast<unsigned long long*>(dst), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        dst[0] = lo;
+        dst[1] = hi;
+    }
 }
 
-// Row r's RowInfo and shortlist are stored (device-scope words): once they
-// have completed, count the row for its step. One wavefront.
+// Entry i of a shortlist: token + 1 is the overlapped decode's tag.
+__device__ __forceinline__ void publish_entry(ShortEntry* out, int i, float lp, int32_t tok, bool coherent) {
+    publish_word(reinterpret_cast<uint32_t*>(out + i), f32_bits(lp),
+                 static_cast<uint32_t>(coherent ? tok + 1 : tok), coherent);
+}
+
+// A row's RowInfo: count + 2 and invalid + 1 are the overlapped decode's tags.
+__device__ __forceinline__ void publish_rowinfo(RowInfo* dst, const RowInfo& info, bool coherent) {
+    uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+    publish_word(d, f32_bits(info.lse), static_cast<uint32_t>(coherent ? info.count + 2 : info.count), coherent);
+    publish_word(d + 2, f32_bits(info.bound), coherent ? info.invalid + 1u : info.invalid, coherent);
+}
+
+// Reads one tagged word; false while it is not written yet.
+__device__ __forceinline__ bool read_tagged(const uint32_t* src, uint32_t& lo, uint32_t& hi) {
+    const unsigned long long w =
+        __hip_atomic_load(reinterpret_cast<const unsigned long long*>(src), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lo = static_cast<uint32_t>(w);
+    hi = static_cast<uint32_t>(w >> 32);
+    return hi != 0u;
+}
+
+// Row r's RowInfo and shortlist words are stored: count the row for its
+// step. The count only tells the select pass when to start reading the step;
+// each word it reads proves itself by its tag. One wavefront.
 __device__ __forceinline__ void signal_row_done(const DecodeParams& p, int64_t r, int lane) {
     if (!p.step_done) return;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (lane == 0) {
         const int64_t bt = r / p.K;  // b * T + t
         __hip_atomic_fetch_add(p.step_done + bt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -301,8 +327,7 @@ __device__ void finish_row_wave(const DecodeParams& p, int64_t r, float lse, flo
                     const float x = live ? s_x[i] : 0.0f;
                     if (live && rank < M) {
                         const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(ki & 0xffffffffu));
-                        store_shared(reinterpret_cast<uint32_t*>(&out[rank].lp), f32_bits(LOGITS ? x - lse : x), coherent);
-                        store_shared(reinterpret_cast<uint32_t*>(&out[rank].token), static_cast<uint32_t>(tok), coherent);
+                        publish_entry(out, rank, LOGITS ? x - lse : x, tok, coherent);
                     }
                     const uint64_t at_m = __ballot(live && rank == M);
                     if (at_m != 0) {
@@ -336,8 +361,7 @@ __device__ void finish_row_wave(const DecodeParams& p, int64_t r, float lse, flo
                 for (int i = lane; i < cnt; i += 64) {
                     const float x = s_x[i];
                     const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(s_key[i] & 0xffffffffu));
-                    store_shared(reinterpret_cast<uint32_t*>(&out[i].lp), f32_bits(LOGITS ? x - lse : x), coherent);
-                    store_shared(reinterpret_cast<uint32_t*>(&out[i].token), static_cast<uint32_t>(tok), coherent);
+                    publish_entry(out, i, LOGITS ? x - lse : x, tok, coherent);
                 }
                 if (n > M) bx = s_x[M];
             }
@@ -345,14 +369,7 @@ __device__ void finish_row_wave(const DecodeParams& p, int64_t r, float lse, flo
             info.bound = (bx > -kInf) ? (LOGITS ? bx - lse : bx) : -kInf;
         }
     }
-    if (lane == 0) {
-        static_assert(sizeof(RowInfo) == 16, "RowInfo words");
-        uint32_t w[4];
-        __builtin_memcpy(w, &info, sizeof(w));
-        uint32_t* dst = reinterpret_cast<uint32_t*>(p.rowinfo + r);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) store_shared(dst + i, w[i], coherent);
-    }
+    if (lane == 0) publish_rowinfo(p.rowinfo + r, info, coherent);
     if (signal) signal_row_done(p, r, lane);  // else the caller signals later
 }
 

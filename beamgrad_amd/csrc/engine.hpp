@@ -41,11 +41,15 @@ constexpr int kSurvivorCap = 512;    // row-pass candidates kept per row before 
 constexpr int kSelectThreads = 256;  // one workgroup per example in the select pass
 constexpr int kRound = kSelectThreads;      // candidates offered per collector round (one per thread)
 
-// Per-row result of the row pass.
+// Per-row result of the row pass. In the overlapped decode every 8-byte
+// half of it, and every shortlist entry, is published as one 64-bit atomic
+// word whose upper half carries a non-zero tag (count + 2, invalid + 1,
+// token + 1) over a workspace cleared before the row pass: a reader that
+// sees the tag has the whole word, so no ordering between words is needed.
 struct RowInfo {
     float lse;     // logsumexp of the row (from logits), else 0
-    float bound;   // upper bound on the log-prob of every allowed token not in the shortlist (-inf: none)
     int32_t count; // shortlist entries; -1: no usable shortlist (the select pass rescans the row)
+    float bound;   // upper bound on the log-prob of every allowed token not in the shortlist (-inf: none)
     uint32_t invalid;  // the row holds NaN or +inf
 };
 
@@ -105,10 +109,18 @@ struct DecodeParams {
     // Overlapped decode (null: the select pass runs after the row pass): the
     // row pass hands out rows step-major through row_ticket and counts the
     // finished rows of each (example, step) in step_done [B, T]; the select
-    // pass waits for a step's count before it reads that step.
+    // pass waits for a step's count, then reads the step's tagged words
+    // (waiting on any not yet written).
     int32_t* step_done;
     unsigned long long* row_ticket;
     int reserve_cus;  // CUs the persistent row-pass kernels leave free (the select pass's workgroups)
+    // A select-pass wait that gives up (bounded by wait_ticks of the 100 MHz
+    // counter) sets *fault and marks its example invalid (2); the example's
+    // remaining steps are written as padding. wait_extra raises the count a
+    // wait needs (a test knob: the count is then never reached).
+    int32_t* fault;
+    unsigned long long wait_ticks;
+    int wait_extra;
 };
 
 // LDS plan of the select pass (byte offsets into its dynamic shared memory).
@@ -134,7 +146,10 @@ SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool st
 
 // Queues the decode (or one step) on `stream` with workspace ws; returns a
 // hipError_t.
-hipError_t launch_decode(const DecodeParams& p, const DecodeLayout& L, hipStream_t stream, char* ws);
+// *fault: the overlapped decode's fault word in the workspace (non-zero once
+// a select-pass wait gave up), or null when the passes ran one after the other.
+hipError_t launch_decode(const DecodeParams& p, const DecodeLayout& L, hipStream_t stream, char* ws,
+                         int32_t** fault);
 size_t sync_bytes(int B, int T);           // overlapped-decode counters in the workspace
 extern std::atomic<int> g_overlap;         // dbs_hip_set_decode_overlap
 hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream);
@@ -160,6 +175,7 @@ hipError_t wait_timeout_counter(int reset, unsigned long long* value);
 
 // Elementwise helpers.
 hipError_t launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream);
+hipError_t launch_clear(void* dst, size_t bytes, hipStream_t stream);
 hipError_t launch_length_penalty(const int32_t* lengths, int64_t n, float alpha, float* out, hipStream_t stream);
 hipError_t launch_check_steps(const int32_t* steps, int B, int T, int32_t* status, hipStream_t stream);
 // Range check of every per-example array (steps in [1, T], beams in [1, K],

@@ -233,13 +233,11 @@ __global__ __launch_bounds__(kLpThreads) void row_logprob_kernel(DecodeParams p)
             for (; j < n; ++j) rank += static_cast<int>(s_key[j] > ki);
             if (rank < M) {
                 const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(ki & 0xffffffffu));
-                store_shared(reinterpret_cast<uint32_t*>(&out[rank].lp), f32_bits(s_x[i]), coherent);
-                store_shared(reinterpret_cast<uint32_t*>(&out[rank].token), static_cast<uint32_t>(tok), coherent);
+                publish_entry(out, rank, s_x[i], tok, coherent);
             } else if (rank == M) {
                 s_bound = s_x[i];
             }
         }
-        if (coherent) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();
     if (tid < 64) {
@@ -256,13 +254,7 @@ __global__ __launch_bounds__(kLpThreads) void row_logprob_kernel(DecodeParams p)
                 info.count = -1;
             }
         }
-        if (tid == 0) {
-            uint32_t w[4];
-            __builtin_memcpy(w, &info, sizeof(w));
-            uint32_t* dst = reinterpret_cast<uint32_t*>(p.rowinfo + r);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) store_shared(dst + i, w[i], coherent);
-        }
+        if (tid == 0) publish_rowinfo(p.rowinfo + r, info, coherent);
         signal_row_done(p, r, tid);
     }
 }

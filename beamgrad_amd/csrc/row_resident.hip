@@ -118,11 +118,10 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
     __syncthreads();
 
     // Wavefront kFinisher (the first of segment 1) finishes row r (lane tree,
-    // shortlist, RowInfo) at the start of the next row, while its part of
-    // that row is still arriving; it signals the row done (overlapped
-    // decode: a wait for its stores) once that part has landed.
+    // shortlist, RowInfo; counted done for the overlapped decode) at the
+    // start of the next row, while its part of that row is still arriving.
     constexpr int kFinisher = 4;
-    bool pend = false, pend_signal = false;
+    bool pend = false;
     int64_t pend_r = 0;
     float pend_m = 0.0f, pend_theta = 0.0f;
     bool pend_bad = false, pend_lse = false, pend_mask = false, pend_full = false;
@@ -140,12 +139,10 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
             }
         }
         const int n = pend_full ? kSurvivorCap + 1 : *s_count;
-        finish_row_wave<LOGITS, true>(p, pend_r, lse, pend_theta, pend_bad, s_key, s_x, n, l, pend_b, pend_mask,
-                                      false);
+        finish_row_wave<LOGITS, true>(p, pend_r, lse, pend_theta, pend_bad, s_key, s_x, n, l, pend_b, pend_mask);
         wave_sync();
         if (l == 0) *s_count = 0;
         pend = false;
-        pend_signal = true;
     };
 
     // byte offset in the segment of this lane's 16 bytes of chunk 0 (stripe
@@ -282,10 +279,6 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
                 gmin[g] = pk_min_i16(gmin[g], R);
                 umax = pk_max_u16(umax, R);
             }
-        }
-        if (wave == kFinisher && pend_signal) {
-            signal_row_done(p, pend_r, l);
-            pend_signal = false;
         }
 
         // ---- row maximum, flag, group keys; the key histogram for theta ----
@@ -556,7 +549,6 @@ __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams 
         }
     }
     if (wave == kFinisher && pend) finish_pending();
-    if (wave == kFinisher && pend_signal) signal_row_done(p, pend_r, l);
 }
 
 int g_cu_count[64];

@@ -23,24 +23,38 @@ __device__ unsigned long long g_rescanned_rows;
 // Waits for a step of the overlapped decode that gave up (should stay 0).
 __device__ unsigned long long g_wait_timeouts;
 
-// Upper bound of one wait for a step's rows: 2 s of the 100 MHz real-time
-// counter (a whole row pass takes milliseconds). The row pass never waits on
-// the select pass, so the bound only keeps a fault elsewhere from hanging the
-// workgroup; after one wait gives up, the workgroup waits no more.
-constexpr unsigned long long kWaitTicks = 200000000ull;
-
-// Overlapped decode: waits until the row pass has finished every row of
-// example b's step t (one at step 0, else K). Their RowInfo and shortlist
-// words were stored, and are read, as device-scope atomics, and the count
-// follows their completion. One thread; false when the wait gave up.
+// Overlapped decode: waits until the row pass has counted every row of
+// example b's step t: one at step 0, else one per beam of the example (the
+// row pass reads, and counts, exactly those rows). The count is a relaxed
+// hint of when to start reading: each word read afterwards is checked by its
+// own tag (wait_tagged). Every wait is bounded (p.wait_ticks of the 100 MHz
+// real-time counter; a whole row pass takes milliseconds): the row pass
+// never waits on the select pass, so the bound only keeps a fault elsewhere
+// from hanging the workgroup. One thread; false when the wait gave up.
 __device__ __forceinline__ bool wait_step_rows(const DecodeParams& p, int b, int t) {
-    const int need = t == 0 ? 1 : p.K;
+    const int need = (t == 0 ? 1 : beams_of(p, b)) + p.wait_extra;
     const int32_t* cnt = p.step_done + static_cast<int64_t>(b) * p.T + t;
     if (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= need) return true;
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
         __builtin_amdgcn_s_sleep(4);
-        if (__builtin_amdgcn_s_memrealtime() - t0 > kWaitTicks) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 > p.wait_ticks) {
+            atomicAdd(&g_wait_timeouts, 1ull);
+            return false;
+        }
+    }
+    return true;
+}
+
+// Overlapped decode: one tagged word of the row pass (RowInfo half or
+// shortlist entry), waited for while its tag is 0; false when the wait gave
+// up (bounded like wait_step_rows).
+__device__ __forceinline__ bool wait_tagged(const DecodeParams& p, const uint32_t* src, uint32_t& lo, uint32_t& hi) {
+    if (read_tagged(src, lo, hi)) return true;
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (!read_tagged(src, lo, hi)) {
+        __builtin_amdgcn_s_sleep(2);
+        if (__builtin_amdgcn_s_memrealtime() - t0 > p.wait_ticks) {
             atomicAdd(&g_wait_timeouts, 1ull);
             return false;
         }
@@ -479,19 +493,23 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             if (tid + u * kSelectThreads < n4) pf_sl[u] = src4[tid + u * kSelectThreads];
     };
 
+    // A padding step (reference src/c_api.cpp:764-781): no token, no parent.
+    auto pad_step = [&](int64_t trace0) {
+        for (int k = tid; k < K; k += kSelectThreads) {
+            if (p.tokens) p.tokens[trace0 + k] = -1;
+            if (p.parents) p.parents[trace0 + k] = -1;
+            if (p.lengths) p.lengths[trace0 + k] = 0;
+            if (p.scores) p.scores[trace0 + k] = -kInf;
+            if (p.raw_scores) p.raw_scores[trace0 + k] = -kInf;
+            if (p.from_logprob) p.from_logprob[trace0 + k] = 0;
+        }
+    };
+
     int cur = 0;
     for (int t = 0; t < T_loop; ++t) {
         const int64_t trace0 = (static_cast<int64_t>(b) * T + t) * K;  // step mode: T == 1
         if (t >= steps_b) {
-            // padding step (reference src/c_api.cpp:764-781)
-            for (int k = tid; k < K; k += kSelectThreads) {
-                if (p.tokens) p.tokens[trace0 + k] = -1;
-                if (p.parents) p.parents[trace0 + k] = -1;
-                if (p.lengths) p.lengths[trace0 + k] = 0;
-                if (p.scores) p.scores[trace0 + k] = -kInf;
-                if (p.raw_scores) p.raw_scores[trace0 + k] = -kInf;
-                if (p.from_logprob) p.from_logprob[trace0 + k] = 0;
-            }
+            pad_step(trace0);
             continue;
         }
         if (tid == 0) {
@@ -500,10 +518,17 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             st.tau = -kInf;
             st.thr = dead_cand();
         }
-        if (p.step_done && !st.gave_up) {
-            // the row pass runs alongside: wait for this step's rows
-            if (tid == 0 && !wait_step_rows(p, b, t)) st.gave_up = 1;
+        if (p.step_done) {
+            // The row pass runs alongside: wait for this step's rows. After a
+            // wait gives up, nothing more of the workspace is read: the
+            // example's remaining steps are padding and it is reported
+            // invalid.
+            if (tid == 0 && !st.gave_up && !wait_step_rows(p, b, t)) st.gave_up = 1;
             __syncthreads();
+            if (st.gave_up) {
+                pad_step(trace0);
+                continue;
+            }
         }
         const bool coherent = p.step_done != nullptr;
         // Stage the step: row statistics of the rows read, the shortlists,
@@ -521,11 +546,19 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 } else if (!coherent) {
                     info = p.rowinfo[trace0 + k];
                 } else {
-                    uint32_t w[4];
+                    // the two tagged words (count + 2, invalid + 1)
                     const uint32_t* src = reinterpret_cast<const uint32_t*>(p.rowinfo + trace0 + k);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) w[i] = load_shared(src + i, true);
-                    __builtin_memcpy(&info, w, sizeof(info));
+                    uint32_t lo0 = 0, hi0 = 2, lo1 = 0, hi1 = 1;
+                    if (!wait_tagged(p, src, lo0, hi0) || !wait_tagged(p, src + 2, lo1, hi1)) {
+                        atomicOr(&st.gave_up, 1);
+                        lo0 = lo1 = 0;
+                        hi0 = 2;
+                        hi1 = 1;
+                    }
+                    info.lse = bits_f32(lo0);
+                    info.count = static_cast<int32_t>(hi0) - 2;
+                    info.bound = bits_f32(lo1);
+                    info.invalid = hi1 - 1u;
                 }
                 if (info.invalid) atomicOr(&st.invalid, 1u);
                 if (p.row_lse && LOGITS) p.row_lse[trace0 + k] = info.lse;
@@ -536,6 +569,14 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             s.rcount[k] = cnt;
             s.rbound[k] = bound;
             if (p.constrained && p.ngram > 1) s.nblk[k] = 0;
+        }
+        if (coherent) {
+            // a shortlist is read only as far as its row's count
+            __syncthreads();
+            if (st.gave_up) {
+                pad_step(trace0);
+                continue;
+            }
         }
         if (have_pf) {
             const int n4 = K * M / 2;
@@ -580,8 +621,15 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                     if (!coherent) {
                         e = src[i];
                     } else {
-                        e.lp = bits_f32(load_shared(src32 + 2 * i, true));
-                        e.token = static_cast<int32_t>(load_shared(src32 + 2 * i + 1, true));
+                        // the entries the row pass wrote (tag token + 1)
+                        if (i % M >= s.rcount[i / M]) continue;
+                        uint32_t lo = 0, hi = 1;
+                        if (!wait_tagged(p, src32 + 2 * i, lo, hi)) {
+                            atomicOr(&st.gave_up, 1);
+                            hi = 1;
+                        }
+                        e.lp = bits_f32(lo);
+                        e.token = static_cast<int32_t>(hi) - 1;
                     }
                     s.sl[SL == M ? i : sl_at(i / M, i % M, SL)] = e;
                 }
@@ -593,6 +641,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             if (have_pf) prefetch(t + 1);
         }
         __syncthreads();
+        if (coherent && st.gave_up) {
+            pad_step(trace0);
+            continue;
+        }
         if (p.constrained && p.ngram > 1) {
             // n-gram blocking (reference src/decoder.cpp:196-230): for each
             // read beam, the tokens that followed an earlier occurrence of its
@@ -831,6 +883,15 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         __syncthreads();
     }
 
+    if (st.gave_up) {
+        // no hypothesis survives an abandoned decode
+        for (int k = tid; k < K; k += kSelectThreads) {
+            s.raw[k] = -kInf;
+            s.len[k] = 0;
+        }
+        if (tid == 0 && p.fault) __hip_atomic_store(p.fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+    }
     // Final scores (reference src/decoder.cpp:179-187) and the state (step mode).
     for (int k = tid; k < K; k += kSelectThreads) {
         const int64_t i = static_cast<int64_t>(b) * K + k;
@@ -843,7 +904,9 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             p.st_fin[i] = static_cast<uint8_t>(s.ended[k] != 0);
         }
     }
-    if (tid == 0 && p.invalid) p.invalid[b] = static_cast<uint8_t>(st.invalid != 0);
+    // 1: a row the search read holds NaN or +inf; 2: the decode of the
+    // example did not complete (an overlapped wait gave up)
+    if (tid == 0 && p.invalid) p.invalid[b] = static_cast<uint8_t>(st.gave_up ? 2 : (st.invalid != 0 ? 1 : 0));
 }
 
 // The prefetch needs the row pass finished before the select pass starts (not

@@ -33,7 +33,8 @@ class HipEngine:
     def decode(self, xin: np.ndarray, dtype: str, *, from_logits=False, eos_token=-1, extra_eos=(), min_length=0,
                alpha=0.0, no_repeat_ngram_size=0, repetition_penalty=1.0, steps=None, banned=None,
                banned_per_example=None, use_ex3: bool | None = None, workspace: bool = True,
-               x_offset: int = 0, beams=None, eos_tokens=None, min_lengths=None, expect_status=None) -> dict:
+               x_offset: int = 0, beams=None, eos_tokens=None, min_lengths=None, expect_status=None,
+               with_status: bool = False) -> dict:
         B, T, K, V = xin.shape
         x = _dev(xin.view(np.int16) if xin.dtype == np.uint16 else xin)
         if x_offset:
@@ -89,11 +90,13 @@ class HipEngine:
                 _abi.ptr(x), _abi.DTYPE[dtype], int(from_logits), C.byref(args), C.byref(opts), C.byref(o),
                 _abi.ptr(out["row_lse"]), _abi.ptr(ws), ws_bytes if ws is not None else 0, self.stream())
         if expect_status is not None:
-            torch.cuda.synchronize()
+            torch.cuda.current_stream().synchronize()
             return status
-        assert status == _abi.STATUS_OK, self.lib.dbs_cuda_status_string(status)
-        torch.cuda.synchronize()
-        return {k: v.cpu().numpy() for k, v in out.items()}
+        if not with_status:
+            assert status == _abi.STATUS_OK, self.lib.dbs_cuda_status_string(status)
+        torch.cuda.current_stream().synchronize()
+        res = {k: v.cpu().numpy() for k, v in out.items()}
+        return (status, res) if with_status else res
 
     # ------------------------------------------------------------------
     def _bwd_inputs(self, trace, grads, logits, dtype, row_lse, keep):

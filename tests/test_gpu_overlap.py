@@ -1,0 +1,161 @@
+# SPDX-License-Identifier: MIT
+"""The overlapped decode's contract: the select pass follows the row pass
+step by step on a second stream (one per caller stream), waits for exactly the
+rows the row pass reads, and reports a wait that gave up as an error instead
+of reading rows that may not be written.
+
+* per-example beams below K (the row pass reads, and counts, only the
+  example's beams): bit-exact vs the oracle, and no wait gives up;
+* a forced give-up (DBS_HIP_TEST_WAIT_GIVE_UP=1 makes every wait need one
+  row more than the row pass ever counts, with a 10 us bound, so every kernel
+  still exits normally): invalid_input[b] == 2, the example's trace is
+  padding, and a synchronising call (dbs_cuda_set_synchronization(1), or the
+  legacy DBS_CUDA_DEBUG_SYNC=1 environment switch) returns LAUNCH_FAILED;
+* two host threads decoding on two streams at once, each bit-exact.
+"""
+
+import ctypes as C
+import os
+import threading
+
+import numpy as np
+import pytest
+import torch
+
+from beamgrad_amd import _abi
+from tests.cases import first_difference, make_case
+
+pytestmark = pytest.mark.gpu
+
+
+def _timeouts(lib) -> int:
+    ms, n = C.c_double(), C.c_int64()
+    assert lib.dbs_hip_profile_read(6, C.byref(ms), C.byref(n)) == 0
+    return n.value
+
+
+@pytest.fixture
+def overlap_on(hip):
+    lib = hip.lib
+    prev = lib.dbs_hip_set_decode_overlap(1)
+    lib.dbs_hip_profile_enable(1)  # clears the counters
+    try:
+        yield lib
+    finally:
+        lib.dbs_hip_profile_enable(0)
+        lib.dbs_hip_set_decode_overlap(prev)
+
+
+def _big_case(seed):
+    """A multi-step 16-bit from-logits case for the persistent row passes."""
+    return make_case(seed, vocabs=[4096, 20000], dtypes=["bf16", "f16"], logits=True, allow_invalid=False)
+
+
+@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("constrained", [False, True])
+def test_per_example_beams_below_k_do_not_wait(hip, oracle, overlap_on, seed, constrained):
+    case = _big_case(7300 + seed) if not constrained else make_case(7350 + seed, allow_invalid=False)
+    kw = dict(case["kw"])
+    if constrained:
+        kw["no_repeat_ngram_size"], kw["repetition_penalty"] = 2, 1.2
+    B, K = case["B"], case["K"]
+    rng = np.random.default_rng(seed)
+    beams = [int(v) for v in rng.integers(1, K + 1, size=B)]
+    beams[0] = max(1, K - 1) if K > 1 else 1  # at least one example below K where K allows
+    got = hip.decode(case["xin"], case["dtype"], beams=beams, **kw)
+    want = oracle.decode_per_example(case["xin"], dtype=case["dtype"], beams=beams, **kw)
+    assert first_difference(got, want) is None, (case["seed"], beams)
+    assert _timeouts(overlap_on) == 0, "a wait of the overlapped decode gave up"
+
+
+def _forced_give_up(monkeypatch):
+    monkeypatch.setenv("DBS_HIP_TEST_WAIT_GIVE_UP", "1")
+
+
+def _check_abandoned(res, B, T, K):
+    assert (res["invalid"] == 2).all(), res["invalid"]
+    assert (res["tokens"] == -1).all() and (res["parents"] == -1).all()
+    assert (res["lengths"] == 0).all() and (res["from_logprob"] == 0).all()
+    assert np.isneginf(res["final_scores"]).all() and np.isneginf(res["final_raw_scores"]).all()
+    assert (res["final_lengths"] == 0).all()
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_given_up_wait_is_reported_async(hip, overlap_on, monkeypatch, seed):
+    case = _big_case(7400 + seed)
+    kw = dict(case["kw"])
+    _forced_give_up(monkeypatch)
+    status, res = hip.decode(case["xin"], case["dtype"], with_status=True, **kw)
+    assert status == _abi.STATUS_OK  # asynchronous call: the flags carry the failure
+    if case["T"] > 1:
+        _check_abandoned(res, case["B"], case["T"], case["K"])
+        assert _timeouts(overlap_on) >= case["B"]
+
+
+@pytest.mark.parametrize("how", ["api", "env_legacy", "env"])
+def test_given_up_wait_fails_a_synchronising_call(hip, oracle, overlap_on, monkeypatch, how):
+    case = _big_case(7410)
+    while case["T"] < 2:
+        case = _big_case(case["seed"] + 1)
+    kw = dict(case["kw"])
+    lib = overlap_on
+    _forced_give_up(monkeypatch)
+    prev = lib.dbs_cuda_get_synchronization()
+    try:
+        if how == "api":
+            assert lib.dbs_cuda_set_synchronization(1) == 0
+        elif how == "env_legacy":
+            monkeypatch.setenv("DBS_CUDA_DEBUG_SYNC", "1")
+        else:
+            monkeypatch.setenv("DBS_CUDA_SYNC_CHECK", "1")
+        status, res = hip.decode(case["xin"], case["dtype"], with_status=True, **kw)
+        assert status == _abi.STATUS_LAUNCH_FAILED, lib.dbs_cuda_status_string(status)
+        _check_abandoned(res, case["B"], case["T"], case["K"])
+    finally:
+        lib.dbs_cuda_set_synchronization(prev)
+    # the switches off again: the same decode completes and matches the oracle
+    monkeypatch.delenv("DBS_HIP_TEST_WAIT_GIVE_UP")
+    monkeypatch.delenv("DBS_CUDA_DEBUG_SYNC", raising=False)
+    monkeypatch.delenv("DBS_CUDA_SYNC_CHECK", raising=False)
+    got = hip.decode(case["xin"], case["dtype"], **kw)
+    assert first_difference(got, oracle.decode(case["xin"], dtype=case["dtype"], **kw)) is None
+
+
+def test_legacy_debug_sync_is_read_per_call(hip, monkeypatch):
+    lib = hip.lib
+    assert lib.dbs_cuda_get_synchronization() == 0
+    monkeypatch.setenv("DBS_CUDA_DEBUG_SYNC", "1")
+    # the flag getter reports the API flag only (reference semantics); the
+    # environment switch acts on the calls
+    assert lib.dbs_cuda_get_synchronization() == 0
+    x = np.zeros((1, 2, 2, 9), np.float32)
+    assert hip.decode(x, "f32", expect_status=True) == _abi.STATUS_OK
+
+
+def test_two_threads_two_streams(hip, oracle, overlap_on):
+    cases = [_big_case(7500 + i) for i in range(2)]
+    wants = [oracle.decode(c["xin"], dtype=c["dtype"], **c["kw"]) for c in cases]
+    results = [[None] * 4 for _ in cases]
+    errors = []
+    barrier = threading.Barrier(2)
+
+    def run(i):
+        try:
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                barrier.wait()
+                for rep in range(4):
+                    results[i][rep] = hip.decode(cases[i]["xin"], cases[i]["dtype"], **cases[i]["kw"])
+        except BaseException as e:  # reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not errors, errors
+    for i, c in enumerate(cases):
+        for rep in range(4):
+            assert first_difference(results[i][rep], wants[i]) is None, (i, rep)
+    assert _timeouts(overlap_on) == 0
