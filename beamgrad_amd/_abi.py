@@ -24,6 +24,8 @@ STATUS_UNAVAILABLE = 1
 STATUS_INVALID_ARGUMENT = 2
 STATUS_LAUNCH_FAILED = 3
 STATUS_OUT_OF_MEMORY = 4
+STATUS_SCRATCH_LIMIT = 5  # dbs_hip_decode_noalloc: the decode needs more than its static scratch
+NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024
 MAX_BEAM = 1024
 MAX_EXTRA_EOS = 16
 DTYPE = {"f32": 0, "f16": 1, "bf16": 2}
@@ -104,6 +106,9 @@ SIGNATURES = {
     "dbs_hip_decode_ex3": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.POINTER(DecodeArgs), C.POINTER(SearchOptions),
                                      C.c_void_p, C.POINTER(DecodeOutputs), C.c_void_p, C.c_void_p, C.c_int64,
                                      C.c_void_p]),
+    "dbs_hip_decode_noalloc": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.POINTER(DecodeArgs),
+                                         C.POINTER(SearchOptions), C.c_void_p, C.POINTER(DecodeOutputs), C.c_void_p,
+                                         C.c_void_p]),
     "dbs_hip_backward_dense": (C.c_int, [C.POINTER(DecodeArgs), C.POINTER(BackwardInputs), C.c_void_p, C.c_int,
                                          C.c_void_p, C.c_int64, C.c_void_p]),
     "dbs_hip_backtrack": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,

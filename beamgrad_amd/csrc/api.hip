@@ -230,7 +230,8 @@ int check_per_example(const DBSCudaDecodeArgs& a, int32_t* status, hipStream_t s
 
 int decode_common(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                   const DBSCudaSearchOptions* options, const uint8_t* banned_pe, const DBSCudaDecodeOutputs* outputs,
-                  float* row_lse, void* workspace, int64_t workspace_bytes, void* stream_ptr) {
+                  float* row_lse, void* workspace, int64_t workspace_bytes, void* stream_ptr,
+                  bool allow_overlap = true) {
     if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !outputs || !outputs->final_scores)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
@@ -289,7 +290,7 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
         if (e != hipSuccess) return finish(stream, e);
     }
     int32_t* fault = nullptr;
-    e = launch_decode(p, L, stream, ws, &fault);
+    e = launch_decode(p, L, stream, ws, &fault, allow_overlap);
     return finish_decode(stream, e, fault);
 }
 
@@ -361,7 +362,7 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
         if (e != hipSuccess) return finish(stream, e);
     }
     int32_t* fault = nullptr;
-    e = launch_decode(p, L, stream, ws, &fault);
+    e = launch_decode(p, L, stream, ws, &fault, true);
     return finish_decode(stream, e, fault);
 }
 
@@ -414,6 +415,37 @@ int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* 
     return finish(stream, e);
 }
 
+// ---------------------------------------------------------------------------
+// The decode that allocates nothing (dbs_hip_decode_noalloc)
+// ---------------------------------------------------------------------------
+
+// Its workspace: a static device array, one copy per GPU the library runs on
+// (held until the process ends), shared by every call on that GPU. In host
+// code the name is only a stand-in: the kernels get each device's address
+// from hipGetSymbolAddress, taken once per device with that device current.
+__device__ __align__(256) unsigned char scratch[DBS_HIP_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mutex;
+
+// The current device's scratch address (set up on the device's first call).
+hipError_t scratch_address(void** out) {
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return hipSuccess;
+}
+
 }  // namespace
 
 extern "C" {
@@ -434,6 +466,9 @@ DBS_CUDA_EXPORT const char* dbs_cuda_status_string(int status) {
         case DBS_CUDA_STATUS_INVALID_ARGUMENT: return "invalid argument";
         case DBS_CUDA_STATUS_LAUNCH_FAILED: return "kernel launch failed";
         case DBS_CUDA_STATUS_OUT_OF_MEMORY: return "out of device memory";
+        case DBS_HIP_STATUS_SCRATCH_LIMIT:
+            return "the decode needs more than the static scratch of dbs_hip_decode_noalloc "
+                   "(DBS_HIP_NOALLOC_SCRATCH_BYTES); call dbs_hip_decode_ex3 with a workspace";
         default: return "unknown status";
     }
 }
@@ -495,6 +530,29 @@ DBS_CUDA_EXPORT int dbs_hip_decode_ex3(const void* inputs, int data_type, int fr
                                        float* row_lse, void* workspace, int64_t workspace_bytes, void* stream) {
     return decode_common(inputs, data_type, from_logits, args, options, banned_per_example, outputs, row_lse,
                          workspace, workspace_bytes, stream);
+}
+
+DBS_CUDA_EXPORT int dbs_hip_decode_noalloc(const void* inputs, int data_type, int from_logits,
+                                           const DBSCudaDecodeArgs* args, const DBSCudaSearchOptions* options,
+                                           const uint8_t* banned_per_example, const DBSCudaDecodeOutputs* outputs,
+                                           float* row_lse, void* stream) {
+    if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !outputs || !outputs->final_scores)
+        return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    const DBSCudaDecodeArgs& a = *args;
+    const DecodeLayout L =
+        decode_layout(a.batch_size, a.steps, a.beam_size, a.vocab_size, constrained(a), false, 0);
+    if (L.total > static_cast<size_t>(DBS_HIP_NOALLOC_SCRATCH_BYTES)) return DBS_HIP_STATUS_SCRATCH_LIMIT;
+    void* ws = nullptr;
+    const hipError_t e = scratch_address(&ws);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return status_of(e);
+    }
+    // the passes one after the other on the caller's stream: no second
+    // stream or event is created, and nothing in the scratch needs clearing
+    return decode_common(inputs, data_type, from_logits, args, options, banned_per_example, outputs, row_lse, ws,
+                         DBS_HIP_NOALLOC_SCRATCH_BYTES, stream, false);
 }
 
 DBS_CUDA_EXPORT int dbs_cuda_decode_step(const float* log_probs, const DBSCudaDecodeArgs* args,

@@ -184,7 +184,7 @@ size_t sync_bytes(int B, int T) {
 // *fault: the overlapped decode's fault word (non-zero once a select-pass
 // wait gave up), else null.
 hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStream_t stream, char* ws,
-                         int32_t** fault) {
+                         int32_t** fault, bool allow_overlap) {
     DecodeParams p = p0;
     *fault = nullptr;
     int device = 0;
@@ -192,8 +192,8 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     if (e != hipSuccess) return e;
     Aux* aux = nullptr;
     const int mode = g_overlap.load(std::memory_order_relaxed);
-    const bool want =
-        !p.step_mode && p.T > 1 && (mode == 1 || (mode == -1 && (p.constrained || row_pass_persistent(p))));
+    const bool want = allow_overlap && !p.step_mode && p.T > 1 &&
+                      (mode == 1 || (mode == -1 && (p.constrained || row_pass_persistent(p))));
     if (want) {
         e = aux_for(device, stream, aux);
         if (e != hipSuccess) return e;

@@ -147,9 +147,10 @@ SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool st
 // Queues the decode (or one step) on `stream` with workspace ws; returns a
 // hipError_t.
 // *fault: the overlapped decode's fault word in the workspace (non-zero once
-// a select-pass wait gave up), or null when the passes ran one after the other.
+// a select-pass wait gave up), or null when the passes ran one after the other
+// (always so when allow_overlap is false).
 hipError_t launch_decode(const DecodeParams& p, const DecodeLayout& L, hipStream_t stream, char* ws,
-                         int32_t** fault);
+                         int32_t** fault, bool allow_overlap);
 size_t sync_bytes(int B, int T);           // overlapped-decode counters in the workspace
 extern std::atomic<int> g_overlap;         // dbs_hip_set_decode_overlap
 hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream);

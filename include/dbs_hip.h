@@ -30,6 +30,32 @@ DBS_CUDA_EXPORT int dbs_hip_decode_ex3(
     int64_t workspace_bytes,
     void* stream);
 
+/* dbs_hip_decode_ex3 without a workspace argument and without any device
+ * allocation, for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The workspace is a static device array of
+ * DBS_HIP_NOALLOC_SCRATCH_BYTES per GPU, held from the library's first use on
+ * that GPU until the process ends and shared by every call on it: calls that
+ * overlap on one GPU (two streams, two threads) race on it and must be
+ * serialised by the caller. A decode whose workspace
+ * (dbs_cuda_decode_workspace_size) exceeds the maximum returns
+ * DBS_HIP_STATUS_SCRATCH_LIMIT without launching anything. The passes run one
+ * after the other on `stream` (no second stream or event is created). With
+ * per-example arrays the call synchronises the stream once, as
+ * dbs_cuda_decode_ex2 does. */
+#define DBS_HIP_NOALLOC_SCRATCH_BYTES (64 * 1024 * 1024)
+#define DBS_HIP_STATUS_SCRATCH_LIMIT 5
+DBS_CUDA_EXPORT int dbs_hip_decode_noalloc(
+    const void* inputs,
+    int data_type,
+    int from_logits,
+    const DBSCudaDecodeArgs* args,
+    const DBSCudaSearchOptions* options,
+    const uint8_t* banned_per_example,
+    const DBSCudaDecodeOutputs* outputs,
+    float* row_lse,
+    void* stream);
+
 /* Output element types of dbs_hip_backward_dense. */
 #define DBS_HIP_GRAD_F32 0
 #define DBS_HIP_GRAD_F16 1

@@ -34,7 +34,7 @@ class HipEngine:
                alpha=0.0, no_repeat_ngram_size=0, repetition_penalty=1.0, steps=None, banned=None,
                banned_per_example=None, use_ex3: bool | None = None, workspace: bool = True,
                x_offset: int = 0, beams=None, eos_tokens=None, min_lengths=None, expect_status=None,
-               with_status: bool = False) -> dict:
+               with_status: bool = False, noalloc: bool = False) -> dict:
         B, T, K, V = xin.shape
         x = _dev(xin.view(np.int16) if xin.dtype == np.uint16 else xin)
         if x_offset:
@@ -80,7 +80,11 @@ class HipEngine:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if workspace else None
         if use_ex3 is None:
             use_ex3 = bpe_d is not None
-        if use_ex3:
+        if noalloc:
+            status = self.lib.dbs_hip_decode_noalloc(
+                _abi.ptr(x), _abi.DTYPE[dtype], int(from_logits), C.byref(args), C.byref(opts), _abi.ptr(bpe_d),
+                C.byref(o), _abi.ptr(out["row_lse"]), self.stream())
+        elif use_ex3:
             status = self.lib.dbs_hip_decode_ex3(
                 _abi.ptr(x), _abi.DTYPE[dtype], int(from_logits), C.byref(args), C.byref(opts), _abi.ptr(bpe_d),
                 C.byref(o), _abi.ptr(out["row_lse"]), _abi.ptr(ws), ws_bytes if ws is not None else 0, self.stream())
