@@ -1,8 +1,9 @@
 # SPDX-License-Identifier: MIT
 """In-tree build of the native parts of beamgrad_amd for gfx950.
 
-* ``_lib/libdbs_hip.so``: the HIP engine and its C ABI (include/dbs_cuda.h,
-  include/dbs_hip.h), compiled by hipcc for gfx950 only;
+* ``_lib/libdbs_hip.so``: the HIP engine and its C ABIs (include/dbs_cuda.h,
+  include/dbs_hip.h, and the host ABI include/dbs.h), compiled by hipcc for
+  gfx950 only;
 * ``_C*.so``: the torch.ops.beamgrad operators, linked against libdbs_hip.
 
 Run ``python -m beamgrad_amd._build`` (or ``__graft_entry__.build()``).
@@ -35,7 +36,8 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-LIB_SOURCES = ["csrc/api.hip", "csrc/decode.hip", "csrc/row_pass.hip", "csrc/row_resident.hip", "csrc/row_pipe.hip", "csrc/row_logprob.hip", "csrc/select.hip", "csrc/backward.hip"]
+LIB_SOURCES = ["csrc/api.hip", "csrc/host_abi.cpp", "csrc/decode.hip", "csrc/row_pass.hip", "csrc/row_resident.hip",
+               "csrc/row_pipe.hip", "csrc/row_logprob.hip", "csrc/select.hip", "csrc/backward.hip"]
 
 
 def lib_path() -> str:
@@ -70,7 +72,9 @@ def build_lib() -> str:
     jobs = max(1, min(len(LIB_SOURCES), int(os.environ.get("MAX_JOBS", "0") or 0) or (os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         list(pool.map(compile_one, zip(LIB_SOURCES, objs)))
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", out + ".tmp"])
+    # -Bsymbolic: the library's own calls stay inside it even where another
+    # library exporting the same dbs_* names is loaded first
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-Bsymbolic", *objs, "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
     return out
 

@@ -17,6 +17,7 @@
 #include "dbs_cuda.h"
 #include "dbs_hip.h"
 #include "engine.hpp"
+#include "host_entry.hpp"
 
 using namespace dbs_hip;
 
@@ -231,7 +232,7 @@ int check_per_example(const DBSCudaDecodeArgs& a, int32_t* status, hipStream_t s
 int decode_common(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                   const DBSCudaSearchOptions* options, const uint8_t* banned_pe, const DBSCudaDecodeOutputs* outputs,
                   float* row_lse, void* workspace, int64_t workspace_bytes, void* stream_ptr,
-                  bool allow_overlap = true) {
+                  bool allow_overlap = true, int32_t* first_invalid = nullptr) {
     if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !outputs || !outputs->final_scores)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
@@ -285,6 +286,7 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
     p.from_logprob = outputs->from_logprob;
     p.invalid = outputs->invalid_input;
     p.row_lse = row_lse;
+    p.first_invalid = first_invalid;
     if (row_lse) {
         e = launch_fill_f32(row_lse, 0.0f, static_cast<int64_t>(a.batch_size) * a.steps * a.beam_size, stream);
         if (e != hipSuccess) return finish(stream, e);
@@ -414,6 +416,46 @@ int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* 
     if (e == hipSuccess) e = launch_dense_gradient(p, stream);
     return finish(stream, e);
 }
+
+}  // namespace
+
+// Entry points for the host ABI (host_abi.cpp), inside the library.
+namespace dbs_hip {
+
+int decode_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
+                    const DBSCudaSearchOptions* options, const DBSCudaDecodeOutputs* outputs, float* row_lse,
+                    int32_t* first_invalid, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+    return decode_common(inputs, data_type, from_logits, args, options, nullptr, outputs, row_lse, workspace,
+                         workspace_bytes, stream, true, first_invalid);
+}
+
+int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, float* draws,
+                        hipStream_t stream) {
+    if (!valid_args(args) || !in || !draws || !in->parents || !in->tokens || !in->lengths || !in->from_logprob)
+        return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    const DBSCudaDecodeArgs& a = *args;
+    BackwardParams p{};
+    p.B = a.batch_size;
+    p.T = a.steps;
+    p.K = a.beam_size;
+    p.V = a.vocab_size;
+    p.alpha = a.length_penalty_alpha;
+    p.steps = a.steps_per_example;
+    p.parents = in->parents;
+    p.tokens = in->tokens;
+    p.lengths = in->lengths;
+    p.from_logprob = in->from_logprob;
+    p.g_final = in->grad_final_scores;
+    p.g_final_raw = in->grad_final_raw_scores;
+    p.g_scores = in->grad_scores;
+    p.g_raw = in->grad_raw_scores;
+    p.draws = draws;
+    return finish(stream, launch_path_walk(p, stream));
+}
+
+}  // namespace dbs_hip
+
+namespace {
 
 // ---------------------------------------------------------------------------
 // The decode that allocates nothing (dbs_hip_decode_noalloc)

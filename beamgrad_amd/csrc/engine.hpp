@@ -121,6 +121,9 @@ struct DecodeParams {
     int32_t* fault;
     unsigned long long wait_ticks;
     int wait_extra;
+    // optional [B]: the first row holding NaN or +inf that example b's search
+    // read, as t * K + k in reading order, or -1 (the host ABI's error text)
+    int32_t* first_invalid;
 };
 
 // LDS plan of the select pass (byte offsets into its dynamic shared memory).

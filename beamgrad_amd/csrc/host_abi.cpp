@@ -1,0 +1,605 @@
+// SPDX-License-Identifier: MIT
+//
+// The libdbs host C ABI (include/dbs.h) served by the HIP engine: decoder
+// handles and the batch entry points of the reference's host library
+// (reference src/c_api.cpp:312-400, 700-983), with host arrays in and out.
+//
+// A call checks its arguments as the reference does, with the same status
+// and error text, stages the host arrays into device buffers owned by the
+// handle (kept between calls, grown on demand), runs the device decode or
+// path walk on the handle's stream, and copies the results back. The
+// backward accumulates into the caller's host buffer exactly where the
+// reference's does: the log-prob entries on the beams' paths (from the
+// per-slot path gradients), or, from logits, the whole rows on those paths
+// (from the device's log-softmax gradient rows).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <exception>
+#include <limits>
+#include <mutex>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "dbs.h"
+#include "dbs_cuda.h"
+#include "dbs_hip.h"
+#include "host_entry.hpp"
+
+namespace {
+
+thread_local std::string t_error;  // the calling thread's latest error
+
+// Device buffers of one handle, by purpose; grown on demand, freed with the
+// handle.
+enum Slot : int {
+    kInputs, kBanned, kSteps, kFinalScores, kFinalRaw, kFinalLengths, kTokens, kParents, kLengths, kScores,
+    kRawScores, kFromLogprob, kRowLse, kFirstInvalid, kWorkspace, kGradFinal, kGradFinalRaw, kGradScores,
+    kGradRaw, kDraws, kDense, kSlotCount
+};
+
+struct Arena {
+    void* ptr[kSlotCount] = {};
+    size_t size[kSlotCount] = {};
+
+    void* get(Slot s, size_t bytes) {
+        if (bytes == 0) bytes = 1;
+        if (size[s] < bytes) {
+            if (ptr[s]) (void)hipFree(ptr[s]);
+            ptr[s] = nullptr;
+            size[s] = 0;
+            if (hipMalloc(&ptr[s], bytes) != hipSuccess) {
+                (void)hipGetLastError();
+                ptr[s] = nullptr;
+                throw std::bad_alloc();
+            }
+            size[s] = bytes;
+        }
+        return ptr[s];
+    }
+    void release() {
+        for (int i = 0; i < kSlotCount; ++i) {
+            if (ptr[i]) (void)hipFree(ptr[i]);
+            ptr[i] = nullptr;
+            size[i] = 0;
+        }
+    }
+};
+
+}  // namespace
+
+struct DBSDecoderHandle {
+    // options after their defaults (reference src/c_api.cpp:160-189)
+    int beam_size = 8;
+    int eos_token = -1;
+    float alpha = 0.0f;
+    int min_length = 0;
+    int validate = 0;
+    int pool_multiplier = 0;
+    std::vector<int32_t> extra_eos;
+
+    std::mutex error_mutex;
+    std::string error;
+
+    std::mutex run_mutex;  // one GPU call at a time on a handle
+    Arena arena;
+    hipStream_t stream = nullptr;
+    int device = -1;
+
+    ~DBSDecoderHandle() {
+        arena.release();
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+void need(bool ok, const char* message) {
+    if (!ok) throw std::invalid_argument(message);
+}
+
+size_t mul(size_t a, size_t b, const char* what) {
+    if (a != 0 && b > std::numeric_limits<size_t>::max() / a) throw std::overflow_error(what);
+    return a * b;
+}
+
+// An input error of one example, prefixed as the reference's batch functions
+// do (reference src/c_api.cpp:264-267).
+[[noreturn]] void example_error(int b, const std::string& what) {
+    throw std::invalid_argument("example " + std::to_string(b) + ": " + what);
+}
+
+void record(DBSDecoderHandle* h, const std::string& message) {
+    t_error = message;
+    if (h) {
+        std::lock_guard<std::mutex> lock(h->error_mutex);
+        h->error = message;
+    }
+}
+
+// Runs body and turns its exceptions into the ABI's statuses; a success
+// clears the recorded errors.
+template <class Body>
+int run(DBSDecoderHandle* h, Body&& body) {
+    try {
+        body();
+        record(h, std::string());
+        return DBS_OK;
+    } catch (const std::invalid_argument& e) {
+        record(h, e.what());
+        return DBS_ERROR_INVALID_ARGUMENT;
+    } catch (const std::overflow_error& e) {
+        record(h, e.what());
+        return DBS_ERROR_INVALID_ARGUMENT;
+    } catch (const std::length_error& e) {
+        record(h, e.what());
+        return DBS_ERROR_INVALID_ARGUMENT;
+    } catch (const std::bad_alloc&) {
+        record(h, "out of memory");
+        return DBS_ERROR_RUNTIME;
+    } catch (const std::exception& e) {
+        record(h, e.what());
+        return DBS_ERROR_RUNTIME;
+    } catch (...) {
+        record(h, "unknown exception");
+        return DBS_ERROR_UNKNOWN;
+    }
+}
+
+void hip_check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return;
+    (void)hipGetLastError();
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) throw std::bad_alloc();
+    throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void engine_check(int status, const char* what) {
+    if (status == DBS_CUDA_STATUS_OK) return;
+    if (status == DBS_CUDA_STATUS_OUT_OF_MEMORY) throw std::bad_alloc();
+    throw std::runtime_error(std::string(what) + ": " + dbs_cuda_status_string(status));
+}
+
+// The handle's stream on the calling thread's device (set up on first use;
+// a change of device drops the buffers of the previous one).
+hipStream_t stream_of(DBSDecoderHandle* h) {
+    int device = 0;
+    hip_check(hipGetDevice(&device), "no usable GPU");
+    if (h->stream && h->device != device) {
+        h->arena.release();
+        (void)hipStreamDestroy(h->stream);
+        h->stream = nullptr;
+    }
+    if (!h->stream) {
+        hip_check(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking), "stream creation");
+        h->device = device;
+    }
+    return h->stream;
+}
+
+template <class T>
+T* upload(DBSDecoderHandle* h, Slot s, const T* host, size_t count, hipStream_t st) {
+    if (!host) return nullptr;
+    T* d = static_cast<T*>(h->arena.get(s, sizeof(T) * count));
+    hip_check(hipMemcpyAsync(d, host, sizeof(T) * count, hipMemcpyHostToDevice, st), "copy to the device");
+    return d;
+}
+
+template <class T>
+T* device_out(DBSDecoderHandle* h, Slot s, const T* host, size_t count) {
+    return host ? static_cast<T*>(h->arena.get(s, sizeof(T) * count)) : nullptr;
+}
+
+template <class T>
+void download(T* host, const T* dev, size_t count, hipStream_t st) {
+    if (host && dev) hip_check(hipMemcpyAsync(host, dev, sizeof(T) * count, hipMemcpyDeviceToHost, st), "copy back");
+}
+
+size_t dtype_bytes(int data_type) { return data_type == DBS_DTYPE_F32 ? 4 : 2; }
+
+void check_dtype(int data_type) {
+    need(data_type == DBS_DTYPE_F32 || data_type == DBS_DTYPE_F16 || data_type == DBS_DTYPE_BF16,
+         "unsupported DBS data type");
+}
+
+// Steps of each example (reference src/c_api.cpp:269-279).
+std::vector<int32_t> steps_of(const int32_t* steps_per_example, int B, int T) {
+    std::vector<int32_t> out(static_cast<size_t>(B), T);
+    if (!steps_per_example) return out;
+    for (int b = 0; b < B; ++b) {
+        if (steps_per_example[b] < 1 || steps_per_example[b] > T)
+            throw std::invalid_argument("steps_per_example[" + std::to_string(b) + "] must be in [1, steps]");
+        out[static_cast<size_t>(b)] = steps_per_example[b];
+    }
+    return out;
+}
+
+// The engine's own limits (device ABI): K <= DBS_CUDA_MAX_BEAM, candidate
+// indices K * V within int32, at most DBS_CUDA_MAX_EXTRA_EOS extra EOS tokens.
+void check_engine_limits(const DBSDecoderHandle* h, int V) {
+    if (h->beam_size > DBS_CUDA_MAX_BEAM ||
+        static_cast<int64_t>(h->beam_size) * V > std::numeric_limits<int32_t>::max())
+        throw std::invalid_argument("beam_size " + std::to_string(h->beam_size) + " with vocab_size " +
+                                    std::to_string(V) + " is beyond the HIP engine (beam_size <= " +
+                                    std::to_string(DBS_CUDA_MAX_BEAM) + ", beam_size * vocab_size < 2^31)");
+    if (h->extra_eos.size() > static_cast<size_t>(DBS_CUDA_MAX_EXTRA_EOS))
+        throw std::invalid_argument("more than " + std::to_string(DBS_CUDA_MAX_EXTRA_EOS) +
+                                    " extra EOS tokens are beyond the HIP engine");
+}
+
+// dbs_decode_batch_into(_ex) (reference src/c_api.cpp:703-800); ex may be null.
+void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool from_logits, int B, int T, int V,
+                  const int32_t* steps_per_example, const DBSAdvancedConstraintsC* cons,
+                  const DBSDecodeOutputsC* out, const DBSDecodeOutputsExC* ex) {
+    need(h != nullptr, "decoder handle cannot be null");
+    check_dtype(data_type);
+    need(inputs != nullptr, "log_probs cannot be null");
+    need(out != nullptr && out->final_scores != nullptr, "outputs and outputs->final_scores cannot be null");
+    need(B > 0 && T > 0 && V > 0, "batch_size, steps and vocab_size must be positive");
+    const bool pool = ex && (ex->pool_parents || ex->pool_tokens || ex->pool_lengths || ex->pool_scores ||
+                             ex->pool_raw_scores || ex->pool_from_logprob);
+    if (ex) {
+        need(!ex->reserved[0] && !ex->reserved[1] && !ex->reserved[2] && !ex->reserved[3],
+             "reserved fields must be NULL");
+        need(!pool || h->pool_multiplier > 0, "pool outputs need a relaxed pool: set relaxed_pool_multiplier >= 1");
+    }
+    const int K = h->beam_size;
+    const size_t trace = mul(static_cast<size_t>(T), static_cast<size_t>(K), "batch stride overflow");
+    const size_t per_example = mul(trace, static_cast<size_t>(V), "batch stride overflow");
+    const size_t elements = mul(per_example, static_cast<size_t>(B), "batch size overflow");
+    (void)mul(per_example, dtype_bytes(data_type), "batch stride overflow");
+    const std::vector<int32_t> steps_b = steps_of(steps_per_example, B, T);
+
+    // What the reference's decoder checks per example (reference
+    // src/decoder.cpp:385-406, 779-793); the options are shared, so example
+    // 0 is the first to fail.
+    const int min_length = cons && cons->min_length >= 0 ? cons->min_length : h->min_length;
+    const float rep = cons ? (cons->repetition_penalty > 0.0f ? cons->repetition_penalty : 1.0f) : 1.0f;
+    if (h->eos_token >= V) example_error(0, "eos_token is outside the vocabulary");
+    for (int32_t tok : h->extra_eos)
+        if (tok >= V) example_error(0, "an extra EOS token is outside the vocabulary");
+    if (cons && cons->forced_tokens) {
+        for (int t = 0; t < steps_b[0]; ++t)
+            if (cons->forced_tokens[t] >= V) example_error(0, "forced token is outside the vocabulary");
+    }
+    if (cons && (!(rep > 0.0f) || !std::isfinite(rep)))
+        example_error(0, "repetition_penalty must be finite and positive (1 disables it)");
+    // What the GPU engine does not serve.
+    need(!(cons && cons->forced_tokens), "forced_tokens are not served by libdbs_hip (the HIP engine)");
+    need(!(cons && cons->token_filter), "token_filter callbacks are not served by libdbs_hip (the HIP engine)");
+    need(!pool, "relaxed-pool outputs are not served by libdbs_hip (the HIP engine)");
+    check_engine_limits(h, V);
+
+    std::lock_guard<std::mutex> lock(h->run_mutex);
+    const hipStream_t st = stream_of(h);
+    const size_t BK = static_cast<size_t>(B) * K, BTK = static_cast<size_t>(B) * trace;
+    const void* x = upload(h, kInputs, static_cast<const unsigned char*>(inputs), elements * dtype_bytes(data_type), st);
+    const uint8_t* banned = cons ? upload(h, kBanned, cons->banned_tokens, static_cast<size_t>(V), st) : nullptr;
+    const int32_t* steps_d = upload(h, kSteps, steps_per_example, static_cast<size_t>(B), st);
+
+    DBSCudaDecodeOutputs o{};
+    o.final_scores = device_out(h, kFinalScores, out->final_scores, BK);
+    o.final_raw_scores = device_out(h, kFinalRaw, out->final_raw_scores, BK);
+    o.final_lengths = device_out(h, kFinalLengths, out->final_lengths, BK);
+    o.tokens = device_out(h, kTokens, out->tokens, BTK);
+    o.parents = device_out(h, kParents, out->parents, BTK);
+    o.lengths = device_out(h, kLengths, out->lengths, BTK);
+    o.scores = device_out(h, kScores, out->scores, BTK);
+    o.raw_scores = device_out(h, kRawScores, out->raw_scores, BTK);
+    o.from_logprob = device_out(h, kFromLogprob, out->from_logprob, BTK);
+    float* row_lse = ex ? device_out(h, kRowLse, ex->row_lse, BTK) : nullptr;
+    int32_t* first_invalid =
+        h->validate ? static_cast<int32_t*>(h->arena.get(kFirstInvalid, sizeof(int32_t) * static_cast<size_t>(B)))
+                    : nullptr;
+
+    DBSCudaDecodeArgs a{};
+    a.batch_size = B;
+    a.steps = T;
+    a.beam_size = K;
+    a.vocab_size = V;
+    a.eos_token = h->eos_token;
+    a.min_length = min_length;
+    a.length_penalty_alpha = h->alpha;
+    a.no_repeat_ngram_size = cons && cons->no_repeat_ngram_size > 0 ? cons->no_repeat_ngram_size : 0;
+    a.repetition_penalty = rep;
+    a.steps_per_example = steps_d;
+    a.banned_tokens = banned;
+    DBSCudaSearchOptions opts{};
+    opts.extra_eos_count = static_cast<int>(h->extra_eos.size());
+    for (size_t i = 0; i < h->extra_eos.size(); ++i) opts.extra_eos_tokens[i] = h->extra_eos[i];
+    const int64_t ws_bytes = dbs_cuda_decode_workspace_size(&a);
+    need(ws_bytes > 0, "invalid decode arguments");
+    void* ws = h->arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
+    engine_check(dbs_hip::decode_for_host(x, data_type, from_logits ? 1 : 0, &a, &opts, &o, row_lse, first_invalid,
+                                          ws, ws_bytes, st),
+                 "HIP decode");
+
+    std::vector<int32_t> bad;
+    if (first_invalid) {
+        bad.resize(static_cast<size_t>(B));
+        download(bad.data(), first_invalid, bad.size(), st);
+    }
+    download(out->final_scores, o.final_scores, BK, st);
+    download(out->final_raw_scores, o.final_raw_scores, BK, st);
+    download(out->final_lengths, o.final_lengths, BK, st);
+    download(out->tokens, o.tokens, BTK, st);
+    download(out->parents, o.parents, BTK, st);
+    download(out->lengths, o.lengths, BTK, st);
+    download(out->scores, o.scores, BTK, st);
+    download(out->raw_scores, o.raw_scores, BTK, st);
+    download(out->from_logprob, o.from_logprob, BTK, st);
+    if (ex) download(ex->row_lse, row_lse, BTK, st);
+    hip_check(hipStreamSynchronize(st), "HIP decode");
+    // validate_inputs: the first example whose search read a NaN/+inf row,
+    // reported at that row (reference src/decoder.cpp:143-171)
+    for (int b = 0; b < static_cast<int>(bad.size()); ++b) {
+        if (bad[static_cast<size_t>(b)] < 0) continue;
+        const int t = bad[static_cast<size_t>(b)] / K, k = bad[static_cast<size_t>(b)] % K;
+        example_error(b, std::string(from_logits ? "logits contain NaN or +inf" : "log_probs contains NaN or +inf") +
+                             " (step " + std::to_string(t) + ", beam " + std::to_string(k) + ")");
+    }
+}
+
+// The checks of a trace handed to a backward (reference src/decoder.cpp:
+// 947-963): indexes in range over each example's own steps.
+void check_trace(int B, int T, int K, int V, const std::vector<int32_t>& steps_b, const int32_t* parents,
+                 const int32_t* tokens, const int32_t* lengths) {
+    for (int b = 0; b < B; ++b) {
+        const size_t base = static_cast<size_t>(b) * T * K;
+        const size_t n = static_cast<size_t>(steps_b[static_cast<size_t>(b)]) * K;
+        for (size_t i = base; i < base + n; ++i) {
+            if (parents[i] < -1 || parents[i] >= K || tokens[i] < -1 || tokens[i] >= V || lengths[i] < 0)
+                example_error(b, "decode trace is out of range (parents, tokens or lengths)");
+        }
+    }
+}
+
+struct Grads {
+    const float* final_scores = nullptr;
+    const float* final_raw = nullptr;
+    const float* scores = nullptr;
+    const float* raw = nullptr;
+};
+
+// The backward of a batch into the host buffer grad [B, T, K, V] (+=): the
+// per-slot path gradients from the device, then the entries they name, or
+// with logits the device's gradient rows of every (example, step, parent)
+// row that an entry lands in.
+void backward_batch(DBSDecoderHandle* h, int B, int T, int V, const int32_t* steps_per_example,
+                    const int32_t* parents, const int32_t* tokens, const int32_t* lengths, const uint8_t* flp,
+                    const Grads& g, const void* logits, int logits_type, const float* row_lse, float* grad) {
+    const int K = h->beam_size;
+    const size_t trace = mul(static_cast<size_t>(T), static_cast<size_t>(K), "batch stride overflow");
+    const size_t row_block = mul(trace, static_cast<size_t>(V), "batch stride overflow");
+    (void)mul(row_block, static_cast<size_t>(B), "batch size overflow");
+    const std::vector<int32_t> steps_b = steps_of(steps_per_example, B, T);
+    check_trace(B, T, K, V, steps_b, parents, tokens, lengths);
+    check_engine_limits(h, V);
+
+    std::lock_guard<std::mutex> lock(h->run_mutex);
+    const hipStream_t st = stream_of(h);
+    const size_t BK = static_cast<size_t>(B) * K, BTK = static_cast<size_t>(B) * trace;
+    DBSCudaDecodeArgs a{};
+    a.batch_size = B;
+    a.steps = T;
+    a.beam_size = K;
+    a.vocab_size = V;
+    a.eos_token = -1;
+    a.length_penalty_alpha = h->alpha;
+    a.repetition_penalty = 1.0f;
+    a.steps_per_example = upload(h, kSteps, steps_per_example, static_cast<size_t>(B), st);
+    DBSCudaBackwardInputs in{};
+    in.parents = upload(h, kParents, parents, BTK, st);
+    in.tokens = upload(h, kTokens, tokens, BTK, st);
+    in.lengths = upload(h, kLengths, lengths, BTK, st);
+    in.from_logprob = upload(h, kFromLogprob, flp, BTK, st);
+    in.grad_final_scores = upload(h, kGradFinal, g.final_scores, BK, st);
+    in.grad_final_raw_scores = upload(h, kGradFinalRaw, g.final_raw, BK, st);
+    in.grad_scores = upload(h, kGradScores, g.scores, BTK, st);
+    in.grad_raw_scores = upload(h, kGradRaw, g.raw, BTK, st);
+    float* draws_d = static_cast<float*>(h->arena.get(kDraws, sizeof(float) * BTK));
+    engine_check(dbs_hip::path_draws_for_host(&a, &in, draws_d, st), "HIP path gradient");
+    std::vector<float> draws(BTK);
+    download(draws.data(), draws_d, BTK, st);
+    hip_check(hipStreamSynchronize(st), "HIP path gradient");
+
+    // (b, t, parent) row and token of every slot with an entry: distinct
+    // slots of one step select distinct (parent, token) pairs, so each entry
+    // is one slot's draw (reference src/decoder.cpp:540-548, 668-683)
+    auto entry_of = [&](size_t i, size_t& row, int& token) -> bool {
+        if (draws[i] == 0.0f || parents[i] < 0 || !flp[i] || tokens[i] < 0) return false;
+        const size_t bt = i / static_cast<size_t>(K);  // b * T + t
+        row = bt * static_cast<size_t>(K) + static_cast<size_t>(parents[i]);
+        token = tokens[i];
+        return true;
+    };
+    if (!logits) {
+        for (size_t i = 0; i < BTK; ++i) {
+            size_t row = 0;
+            int token = 0;
+            if (entry_of(i, row, token)) grad[row * static_cast<size_t>(V) + static_cast<size_t>(token)] += draws[i];
+        }
+        return;
+    }
+    // From logits: the device writes each gradient row (g - softmax(row) *
+    // sum(g), entries summed in token order; zero rows elsewhere), and the
+    // rows with an entry are added here in full (reference
+    // src/decoder.hpp:212-242).
+    in.logits = upload(h, kInputs, static_cast<const unsigned char*>(logits), BTK * V * dtype_bytes(logits_type), st);
+    in.logits_type = logits_type;
+    in.row_lse = upload(h, kRowLse, row_lse, BTK, st);
+    float* dense = static_cast<float*>(h->arena.get(kDense, sizeof(float) * BTK * static_cast<size_t>(V)));
+    const int64_t ws_bytes = dbs_cuda_backward_workspace_size(&a);
+    need(ws_bytes > 0, "invalid backward arguments");
+    void* ws = h->arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
+    engine_check(dbs_hip_backward_dense(&a, &in, dense, DBS_HIP_GRAD_F32, ws, ws_bytes, st), "HIP backward");
+    std::vector<size_t> rows;
+    for (size_t i = 0; i < BTK; ++i) {
+        size_t row = 0;
+        int token = 0;
+        if (entry_of(i, row, token)) rows.push_back(row);
+    }
+    std::sort(rows.begin(), rows.end());
+    rows.erase(std::unique(rows.begin(), rows.end()), rows.end());
+    std::vector<float> buf(rows.size() * static_cast<size_t>(V));
+    for (size_t j = 0; j < rows.size(); ++j)
+        download(buf.data() + j * V, dense + rows[j] * V, static_cast<size_t>(V), st);
+    hip_check(hipStreamSynchronize(st), "HIP backward");
+    for (size_t j = 0; j < rows.size(); ++j) {
+        float* dst = grad + rows[j] * static_cast<size_t>(V);
+        const float* src = buf.data() + j * static_cast<size_t>(V);
+        for (int v = 0; v < V; ++v) dst[v] += src[v];
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+DBS_EXPORT int dbs_abi_version(void) { return DBS_ABI_VERSION; }
+
+DBS_EXPORT const char* dbs_version_string(void) { return "2.3.0"; }
+
+DBS_EXPORT const char* dbs_last_global_error(void) { return t_error.c_str(); }
+
+DBS_EXPORT const char* dbs_selected_kernel_name(void) { return "hip-gfx950"; }
+
+// Options and their defaults as the reference (reference src/c_api.cpp:
+// 160-189, src/decoder.cpp:697-721).
+DBS_EXPORT int dbs_create_ex(DBSOptionsC o, DBSDecoderHandle** out_handle) {
+    if (out_handle) *out_handle = nullptr;
+    return run(nullptr, [&] {
+        need(out_handle != nullptr, "out_handle cannot be null");
+        auto finite_non_negative = [](float x) { return std::isfinite(x) && x >= 0.0f; };
+        need(o.beam_size >= 0, "beam_size cannot be negative");
+        need(o.eos_token >= -1, "eos_token must be -1 (disabled) or a token id");
+        need(finite_non_negative(o.selected_temperature),
+             "selected_temperature must be finite and non-negative (0 selects the default)");
+        need(finite_non_negative(o.soft_topk_temperature),
+             "soft_topk_temperature must be finite and non-negative (0 selects the default)");
+        need(o.relaxed_pool_multiplier >= 0, "relaxed_pool_multiplier cannot be negative");
+        need(o.vocab_block >= 0, "vocab_block cannot be negative");
+        need(finite_non_negative(o.length_penalty_alpha), "length_penalty_alpha must be finite and non-negative");
+        need(finite_non_negative(o.soft_topk_tolerance),
+             "soft_topk_tolerance must be finite and non-negative (0 selects the default)");
+        need(o.soft_topk_max_iters >= 0, "soft_topk_max_iters cannot be negative");
+        need(o.min_length >= 0, "min_length cannot be negative");
+        need(o.max_dense_gradient_elements >= 0, "max_dense_gradient_elements cannot be negative");
+        auto* h = new DBSDecoderHandle;
+        h->beam_size = o.beam_size > 0 ? o.beam_size : 8;
+        h->eos_token = o.eos_token;
+        h->alpha = o.length_penalty_alpha;
+        h->min_length = o.min_length;
+        h->validate = o.validate_inputs != 0 ? 1 : 0;
+        h->pool_multiplier = o.relaxed_pool_multiplier;
+        *out_handle = h;
+    });
+}
+
+DBS_EXPORT DBSDecoderHandle* dbs_create(DBSOptionsC options) {
+    DBSDecoderHandle* h = nullptr;
+    return dbs_create_ex(options, &h) == DBS_OK ? h : nullptr;
+}
+
+DBS_EXPORT void dbs_destroy(DBSDecoderHandle* handle) { delete handle; }
+
+DBS_EXPORT const char* dbs_last_error(DBSDecoderHandle* handle) {
+    if (!handle) return dbs_last_global_error();
+    // a per-thread copy, so the pointer stays valid while other threads
+    // record errors on the handle
+    static thread_local std::string copy;
+    std::lock_guard<std::mutex> lock(handle->error_mutex);
+    copy = handle->error;
+    return copy.c_str();
+}
+
+// reference src/c_api.cpp:368-379, src/decoder.cpp:701-706
+DBS_EXPORT int dbs_set_extra_eos_tokens(DBSDecoderHandle* handle, const int32_t* tokens, int count) {
+    return run(handle, [&] {
+        need(handle != nullptr, "decoder handle cannot be null");
+        need(count >= 0 && (count == 0 || tokens != nullptr), "tokens cannot be null when count > 0");
+        for (int i = 0; i < count; ++i) need(tokens[i] >= 0, "extra EOS tokens must be token ids");
+        need(count == 0 || handle->eos_token >= 0,
+             "extra EOS tokens need EOS handling: set eos_token to one of the EOS tokens");
+        std::lock_guard<std::mutex> lock(handle->run_mutex);
+        handle->extra_eos.assign(tokens, tokens + count);
+    });
+}
+
+DBS_EXPORT int dbs_decode_batch_into(DBSDecoderHandle* handle, const float* log_probs, int batch_size, int steps,
+                                     int vocab_size, const int32_t* steps_per_example,
+                                     const DBSAdvancedConstraintsC* constraints, int num_threads,
+                                     const DBSDecodeOutputsC* outputs) {
+    (void)num_threads;
+    return run(handle, [&] {
+        decode_batch(handle, log_probs, DBS_DTYPE_F32, false, batch_size, steps, vocab_size, steps_per_example,
+                     constraints, outputs, nullptr);
+    });
+}
+
+DBS_EXPORT int dbs_decode_batch_into_ex(DBSDecoderHandle* handle, const void* inputs, int data_type, int from_logits,
+                                        int batch_size, int steps, int vocab_size, const int32_t* steps_per_example,
+                                        const DBSAdvancedConstraintsC* constraints, int num_threads,
+                                        const DBSDecodeOutputsExC* outputs) {
+    (void)num_threads;
+    return run(handle, [&] {
+        need(outputs != nullptr, "outputs cannot be null");
+        decode_batch(handle, inputs, data_type, from_logits != 0, batch_size, steps, vocab_size, steps_per_example,
+                     constraints, &outputs->base, outputs);
+    });
+}
+
+DBS_EXPORT int dbs_backward_batch_into(DBSDecoderHandle* handle, int batch_size, int steps, int vocab_size,
+                                       const int32_t* steps_per_example, const int32_t* parents,
+                                       const int32_t* tokens, const int32_t* lengths, const uint8_t* from_logprob,
+                                       const float* grad_final_scores, int num_threads, float* grad_log_probs) {
+    (void)num_threads;
+    return run(handle, [&] {
+        need(handle != nullptr, "decoder handle cannot be null");
+        need(parents && tokens && lengths && from_logprob,
+             "parents, tokens, lengths and from_logprob cannot be null");
+        need(grad_final_scores && grad_log_probs, "grad_final_scores and grad_log_probs cannot be null");
+        need(batch_size > 0 && steps > 0 && vocab_size > 0, "batch_size, steps and vocab_size must be positive");
+        Grads g;
+        g.final_scores = grad_final_scores;
+        backward_batch(handle, batch_size, steps, vocab_size, steps_per_example, parents, tokens, lengths,
+                       from_logprob, g, nullptr, 0, nullptr, grad_log_probs);
+    });
+}
+
+DBS_EXPORT int dbs_backward_batch_into_ex(DBSDecoderHandle* handle, const DBSBackwardInputsC* in, int num_threads,
+                                          float* grad_inputs) {
+    (void)num_threads;
+    return run(handle, [&] {
+        need(handle != nullptr, "decoder handle cannot be null");
+        need(in != nullptr && grad_inputs != nullptr, "inputs and grad_inputs cannot be null");
+        need(!in->reserved[0] && !in->reserved[1] && !in->reserved[2] && !in->reserved[3],
+             "reserved fields must be NULL");
+        need(in->parents && in->tokens && in->lengths && in->from_logprob,
+             "parents, tokens, lengths and from_logprob cannot be null");
+        need(in->batch_size > 0 && in->steps > 0 && in->vocab_size > 0 && in->pool_size >= 0,
+             "batch_size, steps and vocab_size must be positive and pool_size non-negative");
+        const bool pool_grads = in->grad_pool_scores || in->grad_pool_raw_scores;
+        need(!pool_grads || (in->pool_size > 0 && in->pool_parents && in->pool_tokens && in->pool_lengths &&
+                             in->pool_from_logprob),
+             "pool gradients need pool_size > 0 and the pool trace");
+        need(!pool_grads, "relaxed-pool gradients are not served by libdbs_hip (the HIP engine)");
+        if (in->logits) {
+            check_dtype(in->logits_type);
+            need(in->row_lse != nullptr, "row_lse cannot be null with logits");
+        }
+        Grads g;
+        g.final_scores = in->grad_final_scores;
+        g.final_raw = in->grad_final_raw_scores;
+        g.scores = in->grad_scores;
+        g.raw = in->grad_raw_scores;
+        backward_batch(handle, in->batch_size, in->steps, in->vocab_size, in->steps_per_example, in->parents,
+                       in->tokens, in->lengths, in->from_logprob, g, in->logits, in->logits_type, in->row_lse,
+                       grad_inputs);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,31 @@
+// SPDX-License-Identifier: MIT
+//
+// Device entry points that the host ABI (host_abi.cpp) drives, inside
+// libdbs_hip: the device ABI's decode with one more output, and the path
+// walk alone.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "dbs_cuda.h"
+
+namespace dbs_hip {
+
+// dbs_cuda_decode_ex2, plus first_invalid (device int32 [B] or null): the
+// first row holding NaN or +inf that example b's search read, t * K + k in
+// reading order, or -1. Returns a DBS_CUDA_STATUS_*.
+int decode_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
+                    const DBSCudaSearchOptions* options, const DBSCudaDecodeOutputs* outputs, float* row_lse,
+                    int32_t* first_invalid, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+// The per-slot path gradients draws [B, T, K] of the surrogate backward for
+// every gradient input of `in` (final scores, final raw scores, scores, raw
+// scores; logits are not read): slot (b, t, k) gets the gradient of the
+// log-prob entry it selected, 0 where it selected none. Returns a
+// DBS_CUDA_STATUS_*.
+int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, float* draws,
+                        hipStream_t stream);
+
+}  // namespace dbs_hip

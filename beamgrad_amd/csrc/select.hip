@@ -94,6 +94,7 @@ struct Lds {
 
 struct State {
     int gave_up;  // a wait of the overlapped decode gave up
+    int first_bad;  // the first invalid row read (t * K + k), else INT_MAX
     int count;
     int any_fail;
     int rcount;
@@ -471,6 +472,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     if (tid == 0) {
         st.invalid = 0;
         st.gave_up = 0;
+        st.first_bad = 0x7fffffff;
     }
     __syncthreads();
 
@@ -560,7 +562,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                     info.bound = bits_f32(lo1);
                     info.invalid = hi1 - 1u;
                 }
-                if (info.invalid) atomicOr(&st.invalid, 1u);
+                if (info.invalid) {
+                    atomicOr(&st.invalid, 1u);
+                    atomicMin(&st.first_bad, t * K + k);  // steps in order, beams in order within one
+                }
                 if (p.row_lse && LOGITS) p.row_lse[trace0 + k] = info.lse;
                 cnt = M > 0 ? info.count : -1;
                 bound = info.bound;
@@ -907,6 +912,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     // 1: a row the search read holds NaN or +inf; 2: the decode of the
     // example did not complete (an overlapped wait gave up)
     if (tid == 0 && p.invalid) p.invalid[b] = static_cast<uint8_t>(st.gave_up ? 2 : (st.invalid != 0 ? 1 : 0));
+    if (tid == 0 && p.first_invalid) p.first_invalid[b] = st.first_bad == 0x7fffffff ? -1 : st.first_bad;
 }
 
 // The prefetch needs the row pass finished before the select pass starts (not

@@ -1,0 +1,217 @@
+# SPDX-License-Identifier: MIT
+"""ctypes driver of the libdbs host C ABI (include/dbs.h) for any library that
+exports it: libdbs_hip.so (this build, on the GPU) or the reference's own CPU
+library (oracle/_ref/libdbs_ref.so). Both are called with identical arguments
+and host arrays, so a test can compare their outputs bit for bit."""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+DTYPES = {"f32": 0, "f16": 1, "bf16": 2}
+_i32p = C.POINTER(C.c_int32)
+_f32p = C.POINTER(C.c_float)
+_u8p = C.POINTER(C.c_uint8)
+
+
+class OptionsC(C.Structure):
+    _fields_ = [("beam_size", C.c_int), ("eos_token", C.c_int), ("selected_temperature", C.c_float),
+                ("soft_topk_temperature", C.c_float), ("relaxed_pool_multiplier", C.c_int), ("vocab_block", C.c_int),
+                ("length_penalty_alpha", C.c_float), ("soft_topk_tolerance", C.c_float),
+                ("soft_topk_max_iters", C.c_int), ("min_length", C.c_int), ("validate_inputs", C.c_int),
+                ("max_dense_gradient_elements", C.c_int64), ("reserved0", C.c_int), ("reserved1", C.c_int)]
+
+
+class ConstraintsC(C.Structure):
+    _fields_ = [("banned_tokens", _u8p), ("forced_tokens", _i32p), ("min_length", C.c_int),
+                ("repetition_penalty", C.c_float), ("no_repeat_ngram_size", C.c_int), ("token_filter", C.c_void_p),
+                ("token_filter_user_data", C.c_void_p), ("batch_index", C.c_int)]
+
+
+class OutputsC(C.Structure):
+    _fields_ = [("final_scores", _f32p), ("final_raw_scores", _f32p), ("final_lengths", _i32p), ("tokens", _i32p),
+                ("parents", _i32p), ("lengths", _i32p), ("scores", _f32p), ("raw_scores", _f32p),
+                ("from_logprob", _u8p)]
+
+
+class OutputsExC(C.Structure):
+    _fields_ = [("base", OutputsC), ("pool_parents", _i32p), ("pool_tokens", _i32p), ("pool_lengths", _i32p),
+                ("pool_scores", _f32p), ("pool_raw_scores", _f32p), ("pool_from_logprob", _u8p),
+                ("row_lse", _f32p), ("reserved", C.c_void_p * 4)]
+
+
+class BackwardInputsC(C.Structure):
+    _fields_ = [("batch_size", C.c_int), ("steps", C.c_int), ("vocab_size", C.c_int), ("pool_size", C.c_int),
+                ("steps_per_example", _i32p), ("parents", _i32p), ("tokens", _i32p), ("lengths", _i32p),
+                ("from_logprob", _u8p), ("pool_parents", _i32p), ("pool_tokens", _i32p), ("pool_lengths", _i32p),
+                ("pool_from_logprob", _u8p), ("grad_final_scores", _f32p), ("grad_final_raw_scores", _f32p),
+                ("grad_scores", _f32p), ("grad_raw_scores", _f32p), ("grad_pool_scores", _f32p),
+                ("grad_pool_raw_scores", _f32p), ("logits", C.c_void_p), ("logits_type", C.c_int),
+                ("row_lse", _f32p), ("reserved", C.c_void_p * 4)]
+
+
+def _p(a, ct):
+    return None if a is None else a.ctypes.data_as(C.POINTER(ct))
+
+
+class HostError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"status {status}: {message}")
+        self.status = status
+        self.message = message
+
+
+class HostLib:
+    """One library's dbs_* entry points."""
+
+    def __init__(self, path: str):
+        self.path = path
+        L = self.lib = C.CDLL(path)
+        L.dbs_create_ex.argtypes = [OptionsC, C.POINTER(C.c_void_p)]
+        L.dbs_create_ex.restype = C.c_int
+        L.dbs_destroy.argtypes = [C.c_void_p]
+        L.dbs_destroy.restype = None
+        L.dbs_last_global_error.restype = C.c_char_p
+        L.dbs_last_error.argtypes = [C.c_void_p]
+        L.dbs_last_error.restype = C.c_char_p
+        L.dbs_set_extra_eos_tokens.argtypes = [C.c_void_p, _i32p, C.c_int]
+        L.dbs_set_extra_eos_tokens.restype = C.c_int
+        L.dbs_decode_batch_into.argtypes = [C.c_void_p, _f32p, C.c_int, C.c_int, C.c_int, _i32p,
+                                            C.POINTER(ConstraintsC), C.c_int, C.POINTER(OutputsC)]
+        L.dbs_decode_batch_into.restype = C.c_int
+        L.dbs_decode_batch_into_ex.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                               _i32p, C.POINTER(ConstraintsC), C.c_int, C.POINTER(OutputsExC)]
+        L.dbs_decode_batch_into_ex.restype = C.c_int
+        L.dbs_backward_batch_into.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _i32p, _i32p,
+                                              _u8p, _f32p, C.c_int, _f32p]
+        L.dbs_backward_batch_into.restype = C.c_int
+        L.dbs_backward_batch_into_ex.argtypes = [C.c_void_p, C.POINTER(BackwardInputsC), C.c_int, _f32p]
+        L.dbs_backward_batch_into_ex.restype = C.c_int
+        L.dbs_abi_version.restype = C.c_int
+        L.dbs_version_string.restype = C.c_char_p
+        L.dbs_selected_kernel_name.restype = C.c_char_p
+
+    # ------------------------------------------------------------------
+    def create(self, **opts) -> C.c_void_p:
+        o = OptionsC()
+        for k, v in opts.items():
+            setattr(o, k, v)
+        h = C.c_void_p()
+        status = self.lib.dbs_create_ex(o, C.byref(h))
+        if status != 0:
+            raise HostError(status, self.lib.dbs_last_global_error().decode())
+        return h
+
+    def destroy(self, h):
+        self.lib.dbs_destroy(h)
+
+    def error(self) -> str:
+        return self.lib.dbs_last_global_error().decode()
+
+    def set_extra_eos(self, h, tokens) -> int:
+        a = np.ascontiguousarray(np.asarray(tokens, np.int32))
+        return self.lib.dbs_set_extra_eos_tokens(h, _p(a, C.c_int32) if len(a) else None, len(a))
+
+    # ------------------------------------------------------------------
+    @staticmethod
+    def constraints(banned=None, min_length=-1, repetition_penalty=1.0, no_repeat_ngram_size=0, forced=None,
+                    keep=None):
+        c = ConstraintsC()
+        if banned is not None:
+            keep["banned"] = np.ascontiguousarray(np.asarray(banned, np.uint8))
+            c.banned_tokens = _p(keep["banned"], C.c_uint8)
+        if forced is not None:
+            keep["forced"] = np.ascontiguousarray(np.asarray(forced, np.int32))
+            c.forced_tokens = _p(keep["forced"], C.c_int32)
+        c.min_length = min_length
+        c.repetition_penalty = repetition_penalty
+        c.no_repeat_ngram_size = no_repeat_ngram_size
+        return c
+
+    def decode(self, h, x: np.ndarray, K: int, *, dtype="f32", from_logits=False, steps=None, constraints=None,
+               ex=True, row_lse=True, fill=None) -> tuple[int, dict]:
+        """dbs_decode_batch_into_ex (or, ex=False, dbs_decode_batch_into for
+        f32 log-probs). Outputs are pre-filled with `fill` patterns so every
+        written element is checked. Returns (status, outputs)."""
+        x = np.ascontiguousarray(x)
+        B, T, KK, V = x.shape
+        assert KK == K
+        rng = np.random.default_rng(0)
+
+        def buf(shape, dt):
+            a = np.empty(shape, dt)
+            a.view(np.uint8)[...] = rng.integers(0, 256, a.nbytes, dtype=np.uint8).reshape(a.view(np.uint8).shape)
+            return a
+
+        out = {"final_scores": buf((B, K), np.float32), "final_raw_scores": buf((B, K), np.float32),
+               "final_lengths": buf((B, K), np.int32), "tokens": buf((B, T, K), np.int32),
+               "parents": buf((B, T, K), np.int32), "lengths": buf((B, T, K), np.int32),
+               "scores": buf((B, T, K), np.float32), "raw_scores": buf((B, T, K), np.float32),
+               "from_logprob": buf((B, T, K), np.uint8)}
+        if ex and row_lse:
+            out["row_lse"] = buf((B, T, K), np.float32)
+        base = OutputsC(*(_p(out[n], ct) for n, ct in (
+            ("final_scores", C.c_float), ("final_raw_scores", C.c_float), ("final_lengths", C.c_int32),
+            ("tokens", C.c_int32), ("parents", C.c_int32), ("lengths", C.c_int32), ("scores", C.c_float),
+            ("raw_scores", C.c_float), ("from_logprob", C.c_uint8))))
+        steps_a = None if steps is None else np.ascontiguousarray(np.asarray(steps, np.int32))
+        cons = None if constraints is None else C.byref(constraints)
+        if ex:
+            o = OutputsExC()
+            o.base = base
+            if row_lse:
+                o.row_lse = _p(out["row_lse"], C.c_float)
+            status = self.lib.dbs_decode_batch_into_ex(h, x.ctypes.data_as(C.c_void_p), DTYPES[dtype],
+                                                       int(bool(from_logits)), B, T, V, _p(steps_a, C.c_int32), cons,
+                                                       0, C.byref(o))
+        else:
+            assert dtype == "f32" and not from_logits
+            status = self.lib.dbs_decode_batch_into(h, _p(x, C.c_float), B, T, V, _p(steps_a, C.c_int32), cons, 0,
+                                                    C.byref(base))
+        return status, out
+
+    def backward(self, h, trace: dict, V: int, initial: np.ndarray, *, steps=None, ex=True, grad_final=None,
+                 grad_final_raw=None, grad_scores=None, grad_raw=None, logits=None, logits_dtype="f32",
+                 row_lse=None) -> tuple[int, np.ndarray]:
+        """dbs_backward_batch_into_ex (or, ex=False, dbs_backward_batch_into
+        with the final-score gradient) accumulating into a copy of
+        `initial`. Returns (status, gradient)."""
+        keep = {}
+
+        def arr(name, a, dt):
+            if a is None:
+                return None
+            keep[name] = np.ascontiguousarray(np.asarray(a, dt))
+            return keep[name]
+
+        par = arr("par", trace["parents"], np.int32)
+        B, T, K = par.shape
+        tok = arr("tok", trace["tokens"], np.int32)
+        ln = arr("len", trace["lengths"], np.int32)
+        flp = arr("flp", trace["from_logprob"], np.uint8)
+        st = arr("steps", steps, np.int32)
+        grad = np.ascontiguousarray(np.array(initial, np.float32, copy=True))
+        if not ex:
+            gf = arr("gf", grad_final, np.float32)
+            status = self.lib.dbs_backward_batch_into(h, B, T, V, _p(st, C.c_int32), _p(par, C.c_int32),
+                                                      _p(tok, C.c_int32), _p(ln, C.c_int32), _p(flp, C.c_uint8),
+                                                      _p(gf, C.c_float), 0, _p(grad, C.c_float))
+            return status, grad
+        inp = BackwardInputsC()
+        inp.batch_size, inp.steps, inp.vocab_size, inp.pool_size = B, T, V, 0
+        inp.steps_per_example = _p(st, C.c_int32)
+        inp.parents, inp.tokens = _p(par, C.c_int32), _p(tok, C.c_int32)
+        inp.lengths, inp.from_logprob = _p(ln, C.c_int32), _p(flp, C.c_uint8)
+        for name, field, g in (("gf", "grad_final_scores", grad_final), ("gfr", "grad_final_raw_scores",
+                                                                        grad_final_raw),
+                               ("gs", "grad_scores", grad_scores), ("gr", "grad_raw_scores", grad_raw)):
+            setattr(inp, field, _p(arr(name, g, np.float32), C.c_float))
+        if logits is not None:
+            keep["logits"] = np.ascontiguousarray(logits)
+            inp.logits = keep["logits"].ctypes.data_as(C.c_void_p)
+            inp.logits_type = DTYPES[logits_dtype]
+            inp.row_lse = _p(arr("lse", row_lse, np.float32), C.c_float)
+        status = self.lib.dbs_backward_batch_into_ex(h, C.byref(inp), 0, _p(grad, C.c_float))
+        return status, grad
