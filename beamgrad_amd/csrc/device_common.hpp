@@ -27,6 +27,32 @@ __device__ __forceinline__ float load_one(const void* base, int64_t i) {
     }
 }
 
+// Element i of a device array (per-example options, masks, beam state), read
+// as global memory (a generic pointer compiles to flat loads, which may also
+// touch LDS) and waited for right here, on the path that reads it: a load
+// left outstanding where paths join makes the compiler wait for every
+// outstanding global access at the next use of its register, which in the
+// streaming row pass would drain the LDS-DMA loads in flight on every row.
+template <class T>
+__device__ __forceinline__ T gload(const T* a, int64_t i) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 1, "32-bit or byte elements");
+    const T x = ((const __attribute__((address_space(1))) T*)a)[i];
+    uint32_t u;
+    if constexpr (sizeof(T) == 4) {
+        __builtin_memcpy(&u, &x, 4);
+    } else {
+        u = static_cast<uint32_t>(x);
+    }
+    asm volatile("" : "+v"(u));
+    if constexpr (sizeof(T) == 4) {
+        T y;
+        __builtin_memcpy(&y, &u, 4);
+        return y;
+    } else {
+        return static_cast<T>(u);
+    }
+}
+
 __device__ __forceinline__ bool in_eos_set(const DecodeParams& p, int32_t v) {
     for (int i = 0; i < p.n_eos; ++i)
         if (p.eos_set[i] == v) return true;
@@ -35,30 +61,30 @@ __device__ __forceinline__ bool in_eos_set(const DecodeParams& p, int32_t v) {
 
 // Options of example b: its EOS token (-1: none), minimum length and beams
 // (reference cuda/dbs_cuda.cu:148-155 reads the same per-example arrays).
-__device__ __forceinline__ int eos_of(const DecodeParams& p, int b) { return p.eos_pe ? p.eos_pe[b] : p.eos; }
+__device__ __forceinline__ int eos_of(const DecodeParams& p, int b) { return p.eos_pe ? gload(p.eos_pe, b) : p.eos; }
 __device__ __forceinline__ int min_length_of(const DecodeParams& p, int b) {
-    return p.minlen_pe ? p.minlen_pe[b] : p.min_length;
+    return p.minlen_pe ? gload(p.minlen_pe, b) : p.min_length;
 }
-__device__ __forceinline__ int beams_of(const DecodeParams& p, int b) { return p.beam_pe ? p.beam_pe[b] : p.K; }
+__device__ __forceinline__ int beams_of(const DecodeParams& p, int b) { return p.beam_pe ? gload(p.beam_pe, b) : p.K; }
 
 // Whether token v ends a hypothesis of example b: its EOS token or an extra
 // one, where the example has EOS handling at all.
 __device__ __forceinline__ bool is_eos_of(const DecodeParams& p, int b, int32_t v) {
     if (!p.eos_pe) return in_eos_set(p, v);  // the set holds the EOS token and the extra ones
-    const int e = p.eos_pe[b];
+    const int e = gload(p.eos_pe, b);
     return e >= 0 && (v == e || in_eos_set(p, v));
 }
 
 // Statically excluded tokens of a row: banned (shared or per example) and the
 // EOS tokens while the new length is below min_length.
 __device__ __forceinline__ bool static_masked(const DecodeParams& p, int b, int v, bool mask_eos) {
-    if (p.banned && p.banned[v]) return true;
-    if (p.banned_pe && p.banned_pe[static_cast<int64_t>(b) * p.V + v]) return true;
+    if (p.banned && gload(p.banned, v)) return true;
+    if (p.banned_pe && gload(p.banned_pe, static_cast<int64_t>(b) * p.V + v)) return true;
     if (mask_eos && is_eos_of(p, b, v)) return true;
     return false;
 }
 
-__device__ __forceinline__ int example_steps(const DecodeParams& p, int b) { return p.steps ? p.steps[b] : p.T; }
+__device__ __forceinline__ int example_steps(const DecodeParams& p, int b) { return p.steps ? gload(p.steps, b) : p.T; }
 
 __device__ __forceinline__ int wave_sum(int v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
@@ -86,10 +112,10 @@ __device__ __forceinline__ bool row_is_read(const DecodeParams& p, int64_t r, in
     if (p.step_mode) {
         b = static_cast<int>(r / K);
         if (static_cast<int>(r % K) >= beams_of(p, b)) return false;  // past the example's beams
-        const float praw = p.st_raw[r];
+        const float praw = gload(p.st_raw, r);
         if (!(praw < kInf && praw > -kInf)) return false;  // dead beam
-        if (eos_of(p, b) >= 0 && p.st_fin[r]) return false;  // finished
-        new_len = p.st_len[r] + 1;
+        if (eos_of(p, b) >= 0 && gload(p.st_fin, r)) return false;  // finished
+        new_len = gload(p.st_len, r) + 1;
         return true;
     }
     b = static_cast<int>(r / (static_cast<int64_t>(p.T) * K));
@@ -116,7 +142,12 @@ __device__ __forceinline__ int64_t row_of_ticket(const DecodeParams& p, int64_t 
 // thread and share).
 __device__ __forceinline__ int64_t take_ticket(const DecodeParams& p, int64_t after, int64_t stride) {
     if (!p.row_ticket) return after + stride;
-    return static_cast<int64_t>(__hip_atomic_fetch_add(p.row_ticket, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    // (an opaque per-lane offset of 0: the compiler's wavefront-wide atomic
+    // combining would wait for the result right away)
+    uint32_t zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    return static_cast<int64_t>(
+        __hip_atomic_fetch_add(p.row_ticket + zero, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
 // Words of the overlapped decode (the row pass's RowInfo and shortlists, read

@@ -76,32 +76,48 @@ DBS_HD float exp_nonpositive_nb(float x) {
     return in ? e : 0.0f;
 }
 
+// Constants of log_ge1 as given (Plain), or made opaque by an xor with a
+// run-time zero (Opaque: a caller inside a persistent loop keeps them from
+// being hoisted into registers for the whole loop).
+struct PlainConst {
+    DBS_HD double operator()(double c) const { return c; }
+};
+struct OpaqueConst {
+    uint64_t zero;
+    DBS_HD double operator()(double c) const {
+        return __builtin_bit_cast(double, __builtin_bit_cast(uint64_t, c) ^ zero);
+    }
+};
+
 // ln(x), x >= 1, in double.
-DBS_HD double log_ge1(double x) {
+template <class K>
+DBS_HD double log_ge1_with(double x, K k) {
     int e = 0;
     double m = __builtin_frexp(x, &e);
-    if (m < 0.70710678118654752440) {
-        m = m * 2.0;
+    if (m < k(0.70710678118654752440)) {
+        m = m * k(2.0);
         e -= 1;
     }
-    const double s = (m - 1.0) / (m + 1.0);
+    const double one = k(1.0);
+    const double s = (m - one) / (m + one);
     const double z = s * s;
-    double p = 1.0 / 23.0;
-    p = p * z + 1.0 / 21.0;
-    p = p * z + 1.0 / 19.0;
-    p = p * z + 1.0 / 17.0;
-    p = p * z + 1.0 / 15.0;
-    p = p * z + 1.0 / 13.0;
-    p = p * z + 1.0 / 11.0;
-    p = p * z + 1.0 / 9.0;
-    p = p * z + 1.0 / 7.0;
-    p = p * z + 1.0 / 5.0;
-    p = p * z + 1.0 / 3.0;
-    p = p * z + 1.0;
-    const double log_m = (2.0 * s) * p;
+    double p = k(1.0 / 23.0);
+    p = p * z + k(1.0 / 21.0);
+    p = p * z + k(1.0 / 19.0);
+    p = p * z + k(1.0 / 17.0);
+    p = p * z + k(1.0 / 15.0);
+    p = p * z + k(1.0 / 13.0);
+    p = p * z + k(1.0 / 11.0);
+    p = p * z + k(1.0 / 9.0);
+    p = p * z + k(1.0 / 7.0);
+    p = p * z + k(1.0 / 5.0);
+    p = p * z + k(1.0 / 3.0);
+    p = p * z + one;
+    const double log_m = (k(2.0) * s) * p;
     const double de = static_cast<double>(e);
-    return de * 6.93147180369123816490e-01 + (de * 1.90821492927058770002e-10 + log_m);
+    return de * k(6.93147180369123816490e-01) + (de * k(1.90821492927058770002e-10) + log_m);
 }
+DBS_HD double log_ge1(double x) { return log_ge1_with(x, PlainConst{}); }
 
 // exp(y), y >= 0, in double.
 DBS_HD double exp_ge0(double y) {
@@ -149,6 +165,10 @@ DBS_HD float length_penalty(int length, float alpha) {
 
 DBS_HD float logsumexp_from(float max, float lane_sum) {
     return max + static_cast<float>(log_ge1(static_cast<double>(lane_sum)));
+}
+// The same, its constants opaque (see OpaqueConst).
+DBS_HD float logsumexp_from_opaque(float max, float lane_sum, uint64_t zero) {
+    return max + static_cast<float>(log_ge1_with(static_cast<double>(lane_sum), OpaqueConst{zero}));
 }
 
 // Softmax probability of x in a row with logsumexp lse; 0 for non-finite x.

@@ -34,6 +34,9 @@ __device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint32_t pk_sub_sat_i16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(__builtin_bit_cast(v2i16, a), __builtin_bit_cast(v2i16, b)));
 }
+__device__ __forceinline__ uint32_t pk_add_u16(uint32_t a, uint32_t b) {  // wrapping
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2u16, a) + __builtin_bit_cast(v2u16, b));
+}
 __device__ __forceinline__ uint32_t pk_sign_fill_i16(uint32_t a) {
     const v2i16 fifteen = {15, 15};
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2i16, a) >> fifteen);
@@ -136,28 +139,38 @@ struct RowSlot {
     int b, len;
 };
 
+// TICKETS false: the workgroup's fixed stride even where tickets are handed
+// out (a kernel whose rows all cost the same).
+template <bool TICKETS = true>
+__device__ __forceinline__ int64_t next_index(const DecodeParams& p, int64_t q) {
+    return TICKETS ? take_ticket(p, q, gridDim.x) : q + gridDim.x;
+}
+
+template <bool TICKETS = true>
 __device__ __forceinline__ int64_t first_ticket(const DecodeParams& p) {
-    return p.row_ticket ? take_ticket(p, 0, 0) : static_cast<int64_t>(blockIdx.x);
+    return (TICKETS && p.row_ticket) ? take_ticket(p, 0, 0) : static_cast<int64_t>(blockIdx.x);
 }
 
 // From processing index q on, the first row the search reads (q is left at
 // it), or rows when none is left.
+template <bool TICKETS = true>
 __device__ __forceinline__ int64_t find_read_row(const DecodeParams& p, int64_t rows, int64_t& q, int& b, int& len) {
     while (q < rows) {
         const int64_t rr = row_of_ticket(p, q);
         if (row_is_read(p, rr, b, len)) return rr;
-        q = take_ticket(p, q, gridDim.x);
+        q = next_index<TICKETS>(p, q);
     }
     return rows;
 }
 
 // Thread 0: the row after processing index q (advanced) into slot.
+template <bool TICKETS = true>
 __device__ __forceinline__ void publish_next_row(const DecodeParams& p, int64_t rows, int64_t& q, RowSlot& slot) {
     int b = 0, len = 0;
     int64_t rr = rows;
     if (q < rows) {
-        q = take_ticket(p, q, gridDim.x);
-        rr = find_read_row(p, rows, q, b, len);
+        q = next_index<TICKETS>(p, q);
+        rr = find_read_row<TICKETS>(p, rows, q, b, len);
     }
     slot.r = rr;
     slot.b = b;

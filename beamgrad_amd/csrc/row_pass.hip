@@ -55,17 +55,13 @@ __device__ __forceinline__ void load4(const void* row, int v, int V, float (&x)[
 // Row pass
 // ---------------------------------------------------------------------------
 
+// One row (one wavefront): row r, read by the search for example b with new
+// length new_len.
 template <int DT, bool LOGITS, bool VEC>
-__global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
-    __shared__ uint64_t s_key[kSurvivorCap];
-    __shared__ float s_x[kSurvivorCap];
-    __shared__ int s_count;
-
+__device__ void row_pass_one(const DecodeParams& p, int64_t r, int b, int new_len, uint64_t* s_key, float* s_x,
+                             int& s_count) {
     const int lane = static_cast<int>(threadIdx.x);
-    const int64_t r = row_of_ticket(p, blockIdx.x);
     const int V = p.V;
-    int b, new_len;
-    if (!row_is_read(p, r, b, new_len)) return;
     const bool mask_eos = new_len < min_length_of(p, b);
     const size_t esz = DT == 0 ? 4 : 2;
     const char* row = static_cast<const char*>(p.x) + static_cast<size_t>(r) * static_cast<size_t>(V) * esz;
@@ -139,6 +135,34 @@ __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
     finish_row_wave<LOGITS, false>(p, r, lse, theta, any_bad, s_key, s_x, s_count, lane, b, mask_eos);
 }
 
+template <int DT, bool LOGITS, bool VEC>
+__global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
+    __shared__ uint64_t s_key[kSurvivorCap];
+    __shared__ float s_x[kSurvivorCap];
+    __shared__ int s_count;
+    const int64_t r = row_of_ticket(p, blockIdx.x);
+    int b, new_len;
+    if (!row_is_read(p, r, b, new_len)) return;
+    row_pass_one<DT, LOGITS, VEC>(p, r, b, new_len, s_key, s_x, s_count);
+}
+
+// The rows a persistent row pass left to this kernel (p.fixup_rows, count in
+// *p.fixup_count), one wavefront each, grid-strided.
+template <int DT, bool LOGITS, bool VEC>
+__global__ __launch_bounds__(kRowThreads) void row_fixup_kernel(DecodeParams p) {
+    __shared__ uint64_t s_key[kSurvivorCap];
+    __shared__ float s_x[kSurvivorCap];
+    __shared__ int s_count;
+    const int64_t n = static_cast<int64_t>(*p.fixup_count);
+    for (int64_t i = blockIdx.x; i < n; i += gridDim.x) {
+        const int64_t r = p.fixup_rows[i];
+        int b, new_len;
+        if (!row_is_read(p, r, b, new_len)) continue;
+        row_pass_one<DT, LOGITS, VEC>(p, r, b, new_len, s_key, s_x, s_count);
+        __syncthreads();
+    }
+}
+
 
 }  // namespace
 
@@ -147,6 +171,7 @@ std::atomic<int> g_row_pass_kind{-1};
 bool row_pass_persistent(const DecodeParams& p) {
     const int kind = g_row_pass_kind.load(std::memory_order_relaxed);
     if ((kind == -1 || kind == 3) && row_logprob_eligible(p)) return false;
+    if ((kind == -1 || kind == 4) && row_stream_eligible(p)) return true;
     if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return true;
     return (kind == -1 || kind == 2) && row_pipe_eligible(p);
 }
@@ -159,6 +184,18 @@ hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream) {
     KernelTimer timer(kKindRowPass, stream);
     const int kind = g_row_pass_kind.load(std::memory_order_relaxed);
     if ((kind == -1 || kind == 3) && row_logprob_eligible(p)) return launch_row_logprob(p, rows, stream);
+    if ((kind == -1 || kind == 4) && row_stream_eligible(p)) {
+        // the streaming pass, then the rows it left (NaN/+inf, no term table)
+        hipError_t e = launch_clear(p.fixup_count, sizeof(unsigned long long), stream);
+        if (e == hipSuccess) e = launch_row_stream(p, rows, stream);
+        if (e != hipSuccess) return e;
+        const int64_t grid = rows < 1024 ? rows : 1024;
+        if (vec) hipLaunchKernelGGL((row_fixup_kernel<2, true, true>), dim3(static_cast<unsigned>(grid)),
+                                    dim3(kRowThreads), 0, stream, p);
+        else hipLaunchKernelGGL((row_fixup_kernel<2, true, false>), dim3(static_cast<unsigned>(grid)),
+                                dim3(kRowThreads), 0, stream, p);
+        return hipGetLastError();
+    }
     if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return launch_row_resident(p, rows, stream);
     if ((kind == -1 || kind == 2) && row_pipe_eligible(p)) return launch_row_pipe(p, rows, stream);
     const dim3 grid(static_cast<unsigned>(rows));
