@@ -1,6 +1,13 @@
 # SPDX-License-Identifier: MIT
-"""Search options, with the reference's fields, defaults and validation
-(reference python/beamgrad/_options.py:53-172)."""
+"""Search options: ``BeamOptions`` with the reference's field names, defaults,
+accepted values and error messages (reference
+python/beamgrad/_options.py:53-172).
+
+Every field has one normalizer here. It returns the value to store (a plain
+``int``, ``float``, ``bool`` or tuple of ``int``) or raises the field's
+``ValueError``; ``__post_init__`` applies them in field order, so the first
+bad field reported is the same one the reference reports.
+"""
 
 from __future__ import annotations
 
@@ -11,46 +18,128 @@ from dataclasses import dataclass
 
 # Largest beam the HIP engine runs (DBS_CUDA_MAX_BEAM in include/dbs_cuda.h).
 CUDA_MAX_BEAM = 1024
+# Integer options travel to the engine as 32-bit ints; larger ones are
+# rejected, never wrapped.
 INT32_MAX = 2**31 - 1
 
 
 def _is_int(value) -> bool:
-    # bool is an int subclass, but not a count
+    """An integral number that is not a bool (NumPy integer scalars count)."""
     return isinstance(value, numbers.Integral) and not isinstance(value, bool)
 
 
-def _finite(value) -> float | None:
-    if not isinstance(value, numbers.Real) or isinstance(value, bool):
+def _int_within(value, lo: int, hi: int) -> int | None:
+    return int(value) if _is_int(value) and lo <= value <= hi else None
+
+
+def _finite_real(value) -> float | None:
+    """``float(value)`` for a finite real that is not a bool, else None (ints
+    past the float range included)."""
+    if isinstance(value, bool) or not isinstance(value, numbers.Real):
         return None
     try:
-        out = float(value)
+        as_float = float(value)
     except OverflowError:
         return None
-    return out if math.isfinite(out) else None
+    return as_float if math.isfinite(as_float) else None
 
 
-def _token_list(value, what: str):
-    if hasattr(value, "tolist"):
-        value = value.tolist()
-    if isinstance(value, (str, bytes)) or not isinstance(value, Iterable):
-        raise ValueError(f"{what} must be a sequence of token ids, got {value!r}")
-    return tuple(value)
+def _sequence(value) -> tuple | None:
+    """A sequence given as a list, tuple, array or tensor, as a tuple; None
+    for a string, bytes or anything not iterable."""
+    items = value.tolist() if hasattr(value, "tolist") else value
+    if isinstance(items, (str, bytes)) or not isinstance(items, Iterable):
+        return None
+    return tuple(items)
 
 
-def _normalize_eos(value) -> int | tuple[int, ...]:
+def _all_token_ids(items: tuple) -> bool:
+    return all(_int_within(t, 0, INT32_MAX) is not None for t in items)
+
+
+def _beam_size(value) -> int:
+    n = _int_within(value, 1, INT32_MAX)
+    if n is None:
+        raise ValueError(f"beam_size must be a positive int (at most 2**31 - 1), got {value!r}")
+    return n
+
+
+def _eos_token(value) -> int | tuple[int, ...]:
+    """-1, one token id, or two or more distinct ids in the order given (a
+    sequence naming one distinct id collapses to that id)."""
     if _is_int(value):
-        if not -1 <= value <= INT32_MAX:
+        n = _int_within(value, -1, INT32_MAX)
+        if n is None:
             raise ValueError(f"eos_token must be -1 (disabled) or a token id, got {value!r}")
-        return int(value)
-    if hasattr(value, "tolist"):
-        value = value.tolist()
-    if isinstance(value, (str, bytes)) or not isinstance(value, Iterable):
+        return n
+    items = _sequence(value)
+    if items is None:
         raise ValueError(f"eos_token must be -1 (disabled), a token id or a sequence of token ids, got {value!r}")
-    tokens = tuple(value)
-    if not tokens or any(not _is_int(t) or not 0 <= t <= INT32_MAX for t in tokens):
+    if not items or not _all_token_ids(items):
         raise ValueError(f"eos_token must be a non-empty sequence of token ids, got {value!r}")
-    distinct = tuple(dict.fromkeys(int(t) for t in tokens))
-    return distinct[0] if len(distinct) == 1 else distinct
+    seen: list[int] = []
+    for t in items:
+        if int(t) not in seen:
+            seen.append(int(t))
+    return seen[0] if len(seen) == 1 else tuple(seen)
+
+
+def _min_length(value) -> int:
+    n = _int_within(value, 0, INT32_MAX)
+    if n is None:
+        raise ValueError(f"min_length must be a non-negative int (at most 2**31 - 1), got {value!r}")
+    return n
+
+
+def _alpha(value) -> float:
+    a = _finite_real(value)
+    if a is None or a < 0.0:
+        raise ValueError(f"length_penalty_alpha must be a finite, non-negative number, got {value!r}")
+    return a
+
+
+def _validate(value) -> bool:
+    if not isinstance(value, bool):
+        raise ValueError(f"validate_inputs must be a bool, got {value!r}")
+    return value
+
+
+def _banned(value) -> tuple[int, ...] | None:
+    """None, or the banned ids as a tuple (an empty one becomes None)."""
+    if value is None:
+        return None
+    items = _sequence(value)
+    if items is None:
+        raise ValueError(f"banned_tokens must be a sequence of token ids, got {value!r}")
+    if not _all_token_ids(items):
+        raise ValueError(f"banned_tokens must hold non-negative int token ids, got {items!r}")
+    return tuple(int(t) for t in items) or None
+
+
+def _ngram(value) -> int:
+    n = _int_within(value, 0, INT32_MAX)
+    if n is None:
+        raise ValueError(f"no_repeat_ngram_size must be a non-negative int (at most 2**31 - 1), got {value!r}")
+    return n
+
+
+def _penalty(value) -> float:
+    r = _finite_real(value)
+    if r is None or r <= 0.0:
+        raise ValueError(f"repetition_penalty must be a finite, positive number, got {value!r}")
+    return r
+
+
+_NORMALIZERS = (
+    ("beam_size", _beam_size),
+    ("eos_token", _eos_token),
+    ("min_length", _min_length),
+    ("length_penalty_alpha", _alpha),
+    ("validate_inputs", _validate),
+    ("banned_tokens", _banned),
+    ("no_repeat_ngram_size", _ngram),
+    ("repetition_penalty", _penalty),
+)
 
 
 @dataclass(frozen=True)
@@ -78,63 +167,44 @@ class BeamOptions:
     repetition_penalty: float = 1.0
 
     def __post_init__(self) -> None:
-        if not _is_int(self.beam_size) or not 1 <= self.beam_size <= INT32_MAX:
-            raise ValueError(f"beam_size must be a positive int (at most 2**31 - 1), got {self.beam_size!r}")
-        object.__setattr__(self, "eos_token", _normalize_eos(self.eos_token))
-        if not _is_int(self.min_length) or not 0 <= self.min_length <= INT32_MAX:
-            raise ValueError(f"min_length must be a non-negative int (at most 2**31 - 1), got {self.min_length!r}")
-        alpha = _finite(self.length_penalty_alpha)
-        if alpha is None or alpha < 0.0:
-            raise ValueError(
-                f"length_penalty_alpha must be a finite, non-negative number, got {self.length_penalty_alpha!r}")
-        if not isinstance(self.validate_inputs, bool):
-            raise ValueError(f"validate_inputs must be a bool, got {self.validate_inputs!r}")
-        if self.banned_tokens is not None:
-            banned = _token_list(self.banned_tokens, "banned_tokens")
-            if any(not _is_int(t) or not 0 <= t <= INT32_MAX for t in banned):
-                raise ValueError(f"banned_tokens must hold non-negative int token ids, got {banned!r}")
-            object.__setattr__(self, "banned_tokens", tuple(int(t) for t in banned) or None)
-        if not _is_int(self.no_repeat_ngram_size) or not 0 <= self.no_repeat_ngram_size <= INT32_MAX:
-            raise ValueError(
-                f"no_repeat_ngram_size must be a non-negative int (at most 2**31 - 1), got {self.no_repeat_ngram_size!r}")
-        penalty = _finite(self.repetition_penalty)
-        if penalty is None or penalty <= 0.0:
-            raise ValueError(f"repetition_penalty must be a finite, positive number, got {self.repetition_penalty!r}")
-        for name in ("beam_size", "min_length", "no_repeat_ngram_size"):
-            object.__setattr__(self, name, int(getattr(self, name)))
-        object.__setattr__(self, "length_penalty_alpha", alpha)
-        object.__setattr__(self, "repetition_penalty", penalty)
+        normalized = {name: norm(getattr(self, name)) for name, norm in _NORMALIZERS}
+        for name, value in normalized.items():
+            object.__setattr__(self, name, value)
 
     @property
     def eos_tokens(self) -> tuple[int, ...]:
-        if isinstance(self.eos_token, tuple):
-            return self.eos_token
-        return () if self.eos_token < 0 else (self.eos_token,)
+        """Every EOS id in the order given; () when EOS handling is off."""
+        eos = self.eos_token
+        if isinstance(eos, tuple):
+            return eos
+        return (eos,) if eos >= 0 else ()
 
     def eos_ids(self, vocab_size: int) -> tuple[int, ...]:
-        outside = [t for t in self.eos_tokens if t >= vocab_size]
-        if outside:
-            raise ValueError(f"eos_token {outside[0]} is outside the vocabulary (size {vocab_size})")
+        """``eos_tokens``, each checked to lie below ``vocab_size``."""
+        for t in self.eos_tokens:
+            if t >= vocab_size:
+                raise ValueError(f"eos_token {t} is outside the vocabulary (size {vocab_size})")
         return self.eos_tokens
 
     def native_eos(self) -> tuple[int, list[int]]:
-        """(eos_token, extra_eos) as the operators take them."""
-        tokens = self.eos_tokens
-        return (tokens[0], list(tokens[1:])) if tokens else (-1, [])
+        """(eos_token, extra_eos) as the operators take them: the first id (-1
+        when off) and the rest."""
+        first, *rest = self.eos_tokens or (-1,)
+        return first, list(rest)
 
     def banned_ids(self, vocab_size: int) -> tuple[int, ...] | None:
-        if not self.banned_tokens:
-            return None
-        if max(self.banned_tokens) >= vocab_size:
-            raise ValueError(
-                f"banned_tokens {self.banned_tokens} include ids outside the vocabulary (size {vocab_size})")
-        return self.banned_tokens
+        """The banned ids, checked to lie below ``vocab_size``; None if none."""
+        ids = self.banned_tokens
+        if ids and any(t >= vocab_size for t in ids):
+            raise ValueError(f"banned_tokens {ids} include ids outside the vocabulary (size {vocab_size})")
+        return ids or None
 
     def banned_mask(self, vocab_size: int) -> list[int] | None:
+        """The banned ids as a 0/1 list of ``vocab_size`` entries; None if none."""
         ids = self.banned_ids(vocab_size)
         if ids is None:
             return None
-        mask = [0] * vocab_size
-        for token in ids:
-            mask[token] = 1
-        return mask
+        marks = bytearray(vocab_size)
+        for t in ids:
+            marks[t] = 1
+        return list(marks)

@@ -171,8 +171,8 @@ std::atomic<int> g_row_pass_kind{-1};
 bool row_pass_persistent(const DecodeParams& p) {
     const int kind = g_row_pass_kind.load(std::memory_order_relaxed);
     if ((kind == -1 || kind == 3) && row_logprob_eligible(p)) return false;
-    if ((kind == -1 || kind == 4) && row_stream_eligible(p)) return true;
     if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return true;
+    if ((kind == -1 || kind == 4) && row_stream_eligible(p)) return true;
     return (kind == -1 || kind == 2) && row_pipe_eligible(p);
 }
 
@@ -184,6 +184,7 @@ hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream) {
     KernelTimer timer(kKindRowPass, stream);
     const int kind = g_row_pass_kind.load(std::memory_order_relaxed);
     if ((kind == -1 || kind == 3) && row_logprob_eligible(p)) return launch_row_logprob(p, rows, stream);
+    if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return launch_row_resident(p, rows, stream);
     if ((kind == -1 || kind == 4) && row_stream_eligible(p)) {
         // the streaming pass, then the rows it left (NaN/+inf, no term table)
         hipError_t e = launch_clear(p.fixup_count, sizeof(unsigned long long), stream);
@@ -196,7 +197,6 @@ hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream) {
                                 dim3(kRowThreads), 0, stream, p);
         return hipGetLastError();
     }
-    if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return launch_row_resident(p, rows, stream);
     if ((kind == -1 || kind == 2) && row_pipe_eligible(p)) return launch_row_pipe(p, rows, stream);
     const dim3 grid(static_cast<unsigned>(rows));
 #define DBS_ROW_PASS(DT, LG)                                                                                 \

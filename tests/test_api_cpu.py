@@ -36,6 +36,57 @@ def test_options_validation():
     assert o.banned_mask(4) == [0, 1, 1, 0]
 
 
+@pytest.mark.parametrize("kw, message", [
+    (dict(beam_size=2**31), "beam_size must be a positive int (at most 2**31 - 1), got 2147483648"),
+    (dict(beam_size=2.0), "beam_size must be a positive int (at most 2**31 - 1), got 2.0"),
+    (dict(beam_size=2, eos_token=2**31), "eos_token must be -1 (disabled) or a token id, got 2147483648"),
+    (dict(beam_size=2, eos_token="3"),
+     "eos_token must be -1 (disabled), a token id or a sequence of token ids, got '3'"),
+    (dict(beam_size=2, eos_token=[]), "eos_token must be a non-empty sequence of token ids, got []"),
+    (dict(beam_size=2, eos_token=[1, -1]), "eos_token must be a non-empty sequence of token ids, got [1, -1]"),
+    (dict(beam_size=2, min_length=-1), "min_length must be a non-negative int (at most 2**31 - 1), got -1"),
+    (dict(beam_size=2, length_penalty_alpha=10**400),
+     "length_penalty_alpha must be a finite, non-negative number, got " + repr(10**400)),
+    (dict(beam_size=2, length_penalty_alpha=True),
+     "length_penalty_alpha must be a finite, non-negative number, got True"),
+    (dict(beam_size=2, validate_inputs=None), "validate_inputs must be a bool, got None"),
+    (dict(beam_size=2, banned_tokens=5), "banned_tokens must be a sequence of token ids, got 5"),
+    (dict(beam_size=2, banned_tokens=[1, 2.0]), "banned_tokens must hold non-negative int token ids, got (1, 2.0)"),
+    (dict(beam_size=2, no_repeat_ngram_size=-3),
+     "no_repeat_ngram_size must be a non-negative int (at most 2**31 - 1), got -3"),
+    (dict(beam_size=2, repetition_penalty=float("nan")), "repetition_penalty must be a finite, positive number, got nan"),
+    # the first bad field in field order is the one reported
+    (dict(beam_size=0, min_length=-1), "beam_size must be a positive int"),
+    (dict(beam_size=1, min_length=-1, repetition_penalty=0), "min_length must be a non-negative int"),
+])
+def test_options_error_messages(kw, message):
+    with pytest.raises(ValueError) as err:
+        bg.BeamOptions(**kw)
+    assert str(err.value).startswith(message)
+
+
+def test_options_normalized_values():
+    o = bg.BeamOptions(beam_size=np.int32(4), eos_token=torch.tensor([9, 9]), min_length=np.int16(2),
+                       length_penalty_alpha=np.float32(0.5), banned_tokens=[], no_repeat_ngram_size=np.uint8(3),
+                       repetition_penalty=2)
+    assert (o.beam_size, o.eos_token, o.min_length, o.banned_tokens, o.no_repeat_ngram_size) == (4, 9, 2, None, 3)
+    assert all(type(v) is int for v in (o.beam_size, o.eos_token, o.min_length, o.no_repeat_ngram_size))
+    assert type(o.length_penalty_alpha) is float and type(o.repetition_penalty) is float
+    assert o.eos_tokens == (9,) and o.native_eos() == (9, [])
+    off = bg.BeamOptions(beam_size=1)
+    assert off.eos_tokens == () and off.native_eos() == (-1, []) and off.eos_ids(3) == ()
+    assert off.banned_ids(3) is None and off.banned_mask(3) is None
+    many = bg.BeamOptions(beam_size=1, eos_token=(3, 1, 3, 2), banned_tokens=(0, 4))
+    assert many.eos_token == (3, 1, 2) and many.native_eos() == (3, [1, 2]) and many.eos_ids(4) == (3, 1, 2)
+    with pytest.raises(ValueError, match=r"eos_token 3 is outside the vocabulary \(size 3\)"):
+        many.eos_ids(3)
+    with pytest.raises(ValueError, match=r"include ids outside the vocabulary \(size 4\)"):
+        many.banned_ids(4)
+    assert many.banned_ids(5) == (0, 4) and many.banned_mask(5) == [1, 0, 0, 0, 1]
+    with pytest.raises(Exception):
+        many.beam_size = 3  # frozen
+
+
 def test_cpu_tensors_fail_loudly():
     opts = bg.BeamOptions(beam_size=2)
     with pytest.raises(RuntimeError, match="GPU"):
