@@ -198,8 +198,14 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     if (e != hipSuccess) return e;
     Aux* aux = nullptr;
     const int mode = g_overlap.load(std::memory_order_relaxed);
-    const bool want = allow_overlap && !p.step_mode && p.T > 1 &&
-                      (mode == 1 || (mode == -1 && (p.constrained || row_pass_persistent(p))));
+    bool want = allow_overlap && !p.step_mode && p.T > 1 &&
+                (mode == 1 || (mode == -1 && (p.constrained || row_pass_persistent(p))));
+    // Under stream capture the two passes run one after the other: a graph
+    // may start its branches in any order, and a select pass started before
+    // the row pass would wait for rows nobody is producing.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (want && hipStreamIsCapturing(stream, &capture) == hipSuccess && capture != hipStreamCaptureStatusNone)
+        want = false;
     if (want) {
         e = aux_for(device, stream, aux);
         if (e != hipSuccess) return e;

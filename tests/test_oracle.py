@@ -378,3 +378,49 @@ def test_backtracked_paths_reproduce_raw_scores(oracle, seed):
                 beam = int(out["parents"][b, t, beam])
             assert abs(total - float(out["final_raw_scores"][b, k])) <= 1e-5 * max(1.0, abs(total))
             assert beam == 0
+
+
+def _forward_paths(tokens, parents, steps):
+    """The backtrack's result built forwards, independently of its backward
+    walk: after step t, slot k holds its parent slot's sequence (every entry
+    -1 when the parent is -1, i.e. the slot is dead or descends from nothing)
+    with tokens[t, k] appended; the final beams are the slots after the
+    example's last step, padded with -1."""
+    B, T, K = tokens.shape
+    out = np.full((B, K, T), -1, np.int64)
+    for b in range(B):
+        n = T if steps is None else int(steps[b])
+        seqs = [[] for _ in range(K)]
+        for t in range(n):
+            seqs = [([-1] * t if parents[b, t, k] < 0 else list(seqs[parents[b, t, k]])) + [int(tokens[b, t, k])]
+                    for k in range(K)]
+        for k in range(K):
+            out[b, k, :n] = seqs[k]
+    return out
+
+
+@pytest.mark.parametrize("seed", range(0, 12))
+def test_backtrack_dead_beams_against_forward_construction(oracle, seed):
+    """The backtrack's dead-beam branch (a parent of -1 ends the walk; every
+    earlier step of that beam holds -1) pinned by brute force: the sequences
+    built forwards from the parent pointers. Traces come from decodes where
+    beams die (K above the number of paths: V^t < K at early steps, and rows
+    that are all -inf) and from arbitrary pointer tables with -1 anywhere."""
+    rng = np.random.default_rng(6100 + seed)
+    B, T = 3, 5
+    K = int(rng.choice([4, 8, 16]))
+    V = int(rng.choice([2, 3]))
+    x = log_softmax(rng.normal(size=(B, T, K, V)).astype(np.float32))
+    x[rng.random((B, T, K)) < 0.15] = -np.inf  # whole rows with no finite entry
+    steps = [T, 3, 1] if seed % 2 else None
+    out = oracle.decode(x, eos_token=int(rng.integers(-1, V)), alpha=0.5, steps=steps)
+    assert (out["parents"] < 0).any()  # dead beams occur
+    got = oracle.backtrack(out["tokens"], out["parents"], steps)
+    assert np.array_equal(got, _forward_paths(out["tokens"], out["parents"], steps))
+    dead = ~np.isfinite(out["final_raw_scores"])
+    assert (got[dead] == -1).all()
+    # arbitrary pointers: a walk may end at any step
+    tokens = rng.integers(0, 100, size=(B, T, K))
+    parents = rng.integers(-1, K, size=(B, T, K))
+    for st in (None, [T, 2, 1]):
+        assert np.array_equal(oracle.backtrack(tokens, parents, st), _forward_paths(tokens, parents, st))
