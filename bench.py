@@ -7,11 +7,13 @@ resident in HBM: for the headline workload (config C2) that is
 ``backtrack`` on bf16 logits [B=32, T=64, K=8, V=151936] with EOS 151643,
 length penalty 1.0 and min_length 4. ``value`` is candidate elements per
 second over the timed steps (rows read by the search x V, the reference's
-count); the dominant kernel's HBM roofline fraction and the reference CPU
-library's throughput on a bounded sample of the same workload are reported
-beside it.
+count). Beside it: the row pass's HBM roofline fraction (kernel time from the
+engine's HIP events on its own stream), the reference CPU library on the same
+batch (num_threads = 0, median of 5 runs), and under ``c5`` the second half
+of the metric: the C5 forward + minimum-risk loss + backward step latency with
+the forward's and the backward's (dense gradient's) roofline.
 
-    python bench.py [--steps K] [--warmup W] [--config c1..c5] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--config c1..c5] [--no-cpu-baseline] [--no-c5]
 """
 
 from __future__ import annotations
@@ -110,24 +112,36 @@ def rows_read(out, eos_set: tuple[int, ...]) -> int:
     return int(raw.shape[0] + live.sum().item())
 
 
-def cpu_baseline(name: str, wl: dict, rows_per_example: float, budget_s: float = 10.0) -> dict | None:
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(name: str, wl: dict, rows_per_example: float, runs: int = 5) -> dict | None:
     """The reference's CPU library (oracle/_ref) or, without it, the oracle,
-    timed on this host's cores over the same batch (C5: decode + backward
-    with the same final-score gradient), repeated for about `budget_s`
-    seconds of CPU work."""
+    on this host's cores over the same batch (C5: decode + backward with the
+    same final-score gradient): num_threads = 0 (one thread per hardware
+    thread), one warm-up, then the median of ``runs`` timed runs."""
     from oracle import oracle as orc
 
     cfg = CONFIGS[name]
-    threads = min(16, len(os.sched_getaffinity(0)))
     x = wl["x"].detach()
     host = x.cpu().numpy() if x.dtype == torch.float32 else x.view(torch.int16).cpu().numpy().view(np.uint16)
     kw = dict(dtype=cfg["dtype"], from_logits=cfg["from_logits"], eos_token=cfg["eos"], min_length=cfg["min_length"],
               alpha=cfg["alpha"], no_repeat_ngram_size=cfg.get("ngram", 0), repetition_penalty=cfg.get("rep", 1.0),
-              steps=None if wl["steps"] is None else wl["steps"].cpu().numpy(), num_threads=threads)
+              steps=None if wl["steps"] is None else wl["steps"].cpu().numpy(), num_threads=0)
     if orc.reference_available():
         impl, kind = orc.Reference(), "reference"
+        kernel_name = impl.kernel_name()
     else:
         impl, kind = orc.Oracle(), "port"
+        kernel_name = None
     if wl["banned"] is not None:
         banned = wl["banned"].cpu().numpy()
         if kind == "reference":
@@ -141,55 +155,73 @@ def cpu_baseline(name: str, wl: dict, rows_per_example: float, budget_s: float =
         def run():
             tr = impl.decode(host, **kw)
             impl.backward(tr, cfg["V"], alpha=cfg["alpha"], grad_final=g_final, logits=host, logits_dtype=cfg["dtype"],
-                          row_lse=tr["row_lse"], num_threads=threads)
+                          row_lse=tr["row_lse"], num_threads=0)
         what = "dbs_decode_batch_into_ex + dbs_backward_batch_into_ex"
     else:
         run = lambda: impl.decode(host, **kw)  # noqa: E731
         what = "dbs_decode_batch_into_ex"
     run()  # warm-up
-    reps, total = 0, 0.0
-    while total < budget_s:
+    times = []
+    for _ in range(runs):
         t0 = time.perf_counter()
         run()
-        total += time.perf_counter() - t0
-        reps += 1
-    cand = rows_per_example * cfg["B"] * cfg["V"] * reps
-    return {"value": cand / total, "unit": "candidate elements/s", "cores": threads, "kind": kind,
-            "ms_per_step": total / reps * 1e3,
-            "sample": f"the whole batch ({cfg['B']} examples, T={cfg['T']}) run {reps} times ({total:.1f} s) "
-                      f"through {what}, {threads} threads, after a warm-up"}
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    cand = rows_per_example * cfg["B"] * cfg["V"]
+    nproc = os.cpu_count() or 1
+    return {"value": cand / med, "unit": "candidate elements/s", "cores": nproc, "kind": kind,
+            "ms_per_step": med * 1e3, "num_threads": 0, "nproc": nproc,
+            "cpu_affinity": len(os.sched_getaffinity(0)), "cpu_model": _cpu_model(),
+            "dbs_selected_kernel_name": kernel_name,
+            "sample": f"the whole batch ({cfg['B']} examples, T={cfg['T']}) through {what} with num_threads=0 "
+                      f"(one thread per hardware thread), median of {runs} runs after a warm-up "
+                      f"(runs: {', '.join(f'{1e3 * t:.1f}' for t in times)} ms)"}
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--copy-probe", action="store_true",
-                    help="also run a plain device copy of 1 GiB (the PMC byte-counter calibration)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py measures one GPU: this build's hot path runs on a single MI355X "
-              "(examples are independent and would shard over GPUs with no exchange). Run with --gpus 1.",
-              file=sys.stderr)
-        return 2
+def _read_kernels(lib, steps: int) -> tuple[dict, float]:
+    """Per-kind kernel averages the engine timed with HIP events on its own
+    streams (dbs_hip_profile_read), and rescanned rows per step."""
+    import ctypes as C
 
+    kernels = {}
+    for kind, name in enumerate(("row_pass", "select", "path_walk", "dense_gradient", "backtrack")):
+        ms, n = C.c_double(), C.c_int64()
+        lib.dbs_hip_profile_read(kind, C.byref(ms), C.byref(n))
+        if n.value:
+            kernels[name] = {"avg_ms": ms.value / n.value, "launches": n.value}
+    ms, n = C.c_double(), C.c_int64()
+    lib.dbs_hip_profile_read(5, C.byref(ms), C.byref(n))
+    return kernels, n.value / steps
+
+
+def _traffic(config: str) -> float | None:
+    """HBM bytes per row-pass launch from the committed PMC summary."""
+    tfile = os.path.join(ROOT, "profiles", f"row_pass_{config}_traffic.txt")
+    if not os.path.exists(tfile):
+        return None
+    for line in open(tfile):
+        if line.startswith("traffic_bytes_per_launch"):
+            return float(line.split("=")[1])
+    return None
+
+
+def measure(name: str, steps: int, warmup: int, copy_probe: bool = False) -> dict:
+    """W untimed and K timed steps of one config on the current stream,
+    bracketed by synchronisations; the engine's kernel timers run only over
+    the timed steps."""
     import beamgrad_amd as bg
     from beamgrad_amd import _abi
 
-    cfg = CONFIGS[args.config]
+    cfg = CONFIGS[name]
     B, T, K, V = cfg["B"], cfg["T"], cfg["K"], cfg["V"]
-    wl = workload(args.config)
+    wl = workload(name)
     x = wl["x"]
     opts = bg.BeamOptions(beam_size=K, eos_token=cfg["eos"], min_length=cfg["min_length"],
                           length_penalty_alpha=cfg["alpha"], no_repeat_ngram_size=cfg.get("ngram", 0),
                           repetition_penalty=cfg.get("rep", 1.0))
-    eos_set = opts.eos_tokens
     torch.cuda.synchronize()
 
-    if args.config == "c5":
+    if name == "c5":
         x.requires_grad_(True)
 
         def step():
@@ -198,19 +230,19 @@ def main() -> int:
             result = bg.search(x, opts, from_logits=True)
             loss = bg.losses.minimum_risk(result, wl["costs"])
             loss.backward()
-            return result.trace, result.sequences
+            return result.trace
     else:
         def step():
             out = bg.decode(x, opts, wl["steps"], from_logits=cfg["from_logits"], banned_mask=wl["banned"])
-            seq = bg.backtrack(out)
-            return out, seq
+            bg.backtrack(out)
+            return out
 
-    for _ in range(args.warmup):
-        out, _ = step()
+    for _ in range(warmup):
+        out = step()
     torch.cuda.synchronize()
-    n_rows = rows_read(out, eos_set)
+    n_rows = rows_read(out, opts.eos_tokens)
 
-    if args.copy_probe:
+    if copy_probe:
         src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
         dst = torch.empty_like(src)
         dst.copy_(src)
@@ -224,41 +256,86 @@ def main() -> int:
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(args.steps):
-        out, seq = step()
+    for _ in range(steps):
+        out = step()
     stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    gpu_ms = start.elapsed_time(stop)
-    import ctypes as C
-
-    kernels = {}
-    for kind, name in enumerate(("row_pass", "select", "path_walk", "dense_gradient", "backtrack")):
-        ms, n = C.c_double(), C.c_int64()
-        lib.dbs_hip_profile_read(kind, C.byref(ms), C.byref(n))
-        if n.value:
-            kernels[name] = {"avg_ms": ms.value / n.value, "launches": n.value}
-    ms, n = C.c_double(), C.c_int64()
-    lib.dbs_hip_profile_read(5, C.byref(ms), C.byref(n))
-    rescans_per_step = n.value / args.steps
+    kernels, rescans = _read_kernels(lib, steps)
     lib.dbs_hip_profile_enable(0)
 
-    ms_per_step = gpu_ms / args.steps
+    ms_per_step = start.elapsed_time(stop) / steps
     elem = 4 if cfg["dtype"] == "f32" else 2
-    cand_per_step = n_rows * V
-    value = cand_per_step / (ms_per_step / 1e3)
-    alg_bytes = cand_per_step * elem
-    rp = kernels["row_pass"]["avg_ms"]
-    achieved = alg_bytes / (rp / 1e3) / 1e9
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"row_pass_{args.config}_traffic.txt")
-    if os.path.exists(tfile):
-        for line in open(tfile):
-            if line.startswith("traffic_bytes_per_launch"):
-                traffic = float(line.split("=")[1])
+    alg_bytes = n_rows * V * elem
+    m = {"name": name, "cfg": cfg, "wl": wl, "out": out, "ms_per_step": ms_per_step, "kernels": kernels,
+         "rows_read": n_rows, "alg_bytes": alg_bytes, "value": n_rows * V / (ms_per_step / 1e3),
+         "rescans": rescans, "wall_s": wall}
+    if name == "c5":
+        m["rows_with_gradient"] = rows_with_gradient(out, V, cfg["alpha"])
+    return m
+
+
+def rows_with_gradient(trace, V: int, alpha: float) -> int:
+    """R_g: the logits rows (b, t, parent) some final beam's path takes a
+    token from, i.e. the rows whose softmax the backward reads."""
+    ones = torch.ones(trace.final_scores.shape, dtype=torch.float32, device=trace.tokens.device)
+    draws = torch.ops.beamgrad.final_scores_path_gradient(
+        ones, trace.parents.int(), trace.tokens.int(), trace.lengths.int(), trace.from_logprob.to(torch.uint8), None,
+        V, float(alpha))
+    b, t, k = torch.nonzero(draws, as_tuple=True)
+    parents = trace.parents[b, t, k]
+    keys = (b * trace.parents.shape[1] + t) * trace.parents.shape[2] + parents
+    return int(torch.unique(keys).numel())
+
+
+def hbm_roofline(bytes_per_launch: float, avg_ms: float, kernel: str, traffic=None) -> dict:
+    achieved = bytes_per_launch / (avg_ms / 1e3) / 1e9
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+            "traffic": traffic, "kernel": kernel, "algorithmic_bytes": bytes_per_launch}
+
+
+def c5_summary(m: dict) -> dict:
+    """The fwd+bwd half of the metric on C5: step latency and the backward's
+    (dense gradient) roofline: bf16 gradient writes plus the logits rows with
+    a path gradient read once."""
+    cfg = m["cfg"]
+    B, T, K, V = cfg["B"], cfg["T"], cfg["K"], cfg["V"]
+    bwd_bytes = B * T * K * V * 2 + m["rows_with_gradient"] * V * 2
+    out = {"workload": f"C5: {cfg['desc']}", "ms_per_step": m["ms_per_step"],
+           "kernels_ms": {k: round(v["avg_ms"], 4) for k, v in m["kernels"].items()},
+           "rows_read": m["rows_read"], "rows_with_gradient": m["rows_with_gradient"]}
+    if "row_pass" in m["kernels"]:
+        out["forward_roofline"] = hbm_roofline(m["alg_bytes"], m["kernels"]["row_pass"]["avg_ms"], "row_pass")
+    if "dense_gradient" in m["kernels"]:
+        out["backward_roofline"] = hbm_roofline(bwd_bytes, m["kernels"]["dense_gradient"]["avg_ms"], "dense_gradient")
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-c5", action="store_true", help="skip the C5 fwd+bwd fields of the default C2 line")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain device copy of 1 GiB (the PMC byte-counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build's hot path runs on a single MI355X "
+              "(examples are independent and would shard over GPUs with no exchange). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    m = measure(args.config, args.steps, args.warmup, args.copy_probe)
+    cfg = m["cfg"]
+    B, T, K, V = cfg["B"], cfg["T"], cfg["K"], cfg["V"]
+    kernels = m["kernels"]
+    ms_per_step = m["ms_per_step"]
     result = {
         "metric": METRIC,
-        "value": value,
+        "value": m["value"],
         "unit": "candidate elements/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -270,20 +347,23 @@ def main() -> int:
         "dtype": cfg["dtype"],
         "data": "synthetic (seeded, generated on the GPU)",
         "config": {"workload": f"{args.config.upper()}: {cfg['desc']}", "B": B, "T": T, "K": K, "V": V,
-                   "from_logits": cfg["from_logits"], "rows_read_per_step": n_rows,
-                   "step_hbm_gbs": alg_bytes / (ms_per_step / 1e3) / 1e9,
-                   "step_hbm_frac": alg_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS,
+                   "from_logits": cfg["from_logits"], "rows_read_per_step": m["rows_read"],
+                   "step_hbm_gbs": m["alg_bytes"] / (ms_per_step / 1e3) / 1e9,
+                   "step_hbm_frac": m["alg_bytes"] / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS,
                    "kernels_ms": {k: round(v["avg_ms"], 4) for k, v in kernels.items()},
-                   "rescanned_rows_per_step": rescans_per_step,
-                   "wall_s": round(wall, 3)},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": "row_pass",
-                     "algorithmic_bytes": alg_bytes},
+                   "rescanned_rows_per_step": m["rescans"],
+                   "wall_s": round(m["wall_s"], 3)},
+        "roofline": hbm_roofline(m["alg_bytes"], kernels["row_pass"]["avg_ms"], "row_pass", _traffic(args.config)),
         "cpu_baseline": None,
     }
+    if args.config == "c5":
+        result["c5"] = c5_summary(m)
     if not args.no_cpu_baseline:
-        del out, seq
-        result["cpu_baseline"] = cpu_baseline(args.config, wl, n_rows / B)
+        result["cpu_baseline"] = cpu_baseline(args.config, m["wl"], m["rows_read"] / B)
+    if args.config == "c2" and not args.no_c5:
+        del m
+        torch.cuda.empty_cache()
+        result["c5"] = c5_summary(measure("c5", max(3, args.steps // 2), 2))
     print(json.dumps(result), flush=True)
     return 0
 
