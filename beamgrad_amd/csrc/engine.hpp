@@ -173,6 +173,9 @@ bool row_pipe_eligible(const DecodeParams& p);
 // registers (65536 < V <= 153600, V % 8 == 0, 16-byte aligned).
 bool row_stream_eligible(const DecodeParams& p);
 hipError_t launch_row_stream(const DecodeParams& p, int64_t rows, hipStream_t stream);
+// bfloat16 logits, both segments of a 512-thread workgroup relaying (row_relay.hip)
+bool row_relay_eligible(const DecodeParams& p);
+hipError_t launch_row_relay(const DecodeParams& p, int64_t rows, hipStream_t stream);
 bool row_logprob_eligible(const DecodeParams& p);
 hipError_t launch_row_logprob(const DecodeParams& p, int64_t rows, hipStream_t stream);
 extern std::atomic<int> g_row_pass_kind;  // dbs_hip_set_row_pass

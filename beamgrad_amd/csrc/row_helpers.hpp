@@ -93,6 +93,59 @@ __device__ __forceinline__ bool table_fits(float m, int& ulo) {
     return !(d >= -87.0f);
 }
 
+// Transposes one chunk: lane L holds 16 bytes = lanes 8 (L % 8) .. + 7 of
+// stripe L / 8; it gets back its own lane L of the 8 stripes, packed two
+// stripes per register (lower stripe in the low half). The chunk goes through
+// the wavefront's 1 KB slot, (stripe i, lane L) at byte 128 i + 2 L, read back
+// with two transposing reads: within each 16-lane group, lane i receives
+// element i % 4 of the 8 bytes addressed by lanes 4 k + i / 4 (k = 0..3), so
+// lane L = 16 G + a addresses (stripe 4 h + a / 4, lanes 16 G + 4 (a % 4) ..).
+// The write and the reads go through the compiler's LDS operations, so the
+// next chunk's transpose can start before this one's results are used.
+__device__ __forceinline__ void transpose_chunk(unsigned char* slot, int L, uint32_t x0, uint32_t x1, uint32_t x2,
+                                                uint32_t x3, uint32_t (&R)[4]) {
+    typedef short v4i16 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) unsigned char lds_u8;
+    const int G = L >> 4, a = L & 15;
+    lds_u8* base = (lds_u8*)slot;
+    *reinterpret_cast<__attribute__((address_space(3))) v4u32*>(base + 16 * L) = v4u32{x0, x1, x2, x3};
+    lds_u8* rd = base + 128 * (a >> 2) + 32 * G + 8 * (a & 3);
+    const v4i16 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4i16*>(rd));
+    const v4i16 t1 =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4i16*>(rd + 512));
+    const v2u32 u0 = __builtin_bit_cast(v2u32, t0), u1 = __builtin_bit_cast(v2u32, t1);
+    R[0] = u0.x;
+    R[1] = u0.y;
+    R[2] = u1.x;
+    R[3] = u1.y;
+}
+
+// The term table with a fixed base: slot k >= 1 of each sign holds magnitude
+// kFixedBase - 1 + k (the bfloat16 pattern 0x3300 is 2^-25), slot 0 every
+// smaller magnitude. The slot of a pattern then does not depend on the row,
+// so it can be computed as soon as the pattern is in registers. It fits a row
+// with maximum m when 1 <= m (every |x| < 2^-25 <= half an ulp of m gives
+// fl(x - m) = -m, slot 0's exp(-m)) and m's pattern lies below the last slot
+// (a positive pattern never clamps; +inf and +NaN clamp to the last positive
+// slot, which holds 0, as do -inf, -NaN and every magnitude >= 127.5 in the
+// last negative slot: exp(-127.5 - m) is 0).
+constexpr uint32_t kFixedBase = 0x3300u;
+__device__ __forceinline__ bool table_fits_fixed(float m) {
+    if (!(m >= 1.0f && m < kInf)) return false;
+    const uint32_t mp = f32_bits(m) >> 16;
+    return mp < kFixedBase - 1 + (kLutHalf - 1);
+}
+
+// Byte offsets into the fixed-base table of a register's two bfloat16
+// patterns (low half, high half): slot = min(max(magnitude - (base - 1), 0),
+// 4095), plus 4096 for a negative pattern, times 4.
+__device__ __forceinline__ uint32_t term_offsets(uint32_t R) {
+    uint32_t idx = pk_sub_sat_u16(R & 0x7fff7fffu, (kFixedBase - 1u) * 0x10001u);
+    idx = pk_min_u16(idx, 0x0fff0fffu);
+    idx |= (R >> 3) & 0x10001000u;
+    return pk_shl2_u16(idx);
+}
+
 // Inverse of key16.
 __device__ __forceinline__ uint32_t key_pattern(int key) {
     return static_cast<uint16_t>(key < 0 ? (key ^ 0x7fff) : key);

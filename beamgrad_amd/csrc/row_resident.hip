@@ -50,33 +50,6 @@ constexpr int kMaxStripes = 2 * 8 * kResChunks;  // 608 stripes: V <= 155648
 constexpr int kResLds = 2 * kLutHalf * 4 + 8 * 1024 + 256 * 4 + kSurvivorCap * 12 + 2 * 256 * 4 + 64 + 16;
 static_assert(kResLds <= 160 * 1024, "LDS of the resident row pass");
 
-// Transposes one chunk: lane L holds 16 bytes = lanes 8 (L % 8) .. + 7 of
-// stripe L / 8; it gets back its own lane L of the 8 stripes, packed two
-// stripes per register (lower stripe in the low half). The chunk goes through
-// the wavefront's 1 KB slot, (stripe i, lane L) at byte 128 i + 2 L, read back
-// with two transposing reads: within each 16-lane group, lane i receives
-// element i % 4 of the 8 bytes addressed by lanes 4 k + i / 4 (k = 0..3), so
-// lane L = 16 G + a addresses (stripe 4 h + a / 4, lanes 16 G + 4 (a % 4) ..).
-// The write and the reads go through the compiler's LDS operations, so the
-// next chunk's transpose can start before this one's results are used.
-__device__ __forceinline__ void transpose_chunk(unsigned char* slot, int L, uint32_t x0, uint32_t x1, uint32_t x2,
-                                                uint32_t x3, uint32_t (&R)[4]) {
-    typedef short v4i16 __attribute__((ext_vector_type(4)));
-    typedef __attribute__((address_space(3))) unsigned char lds_u8;
-    const int G = L >> 4, a = L & 15;
-    lds_u8* base = (lds_u8*)slot;
-    *reinterpret_cast<__attribute__((address_space(3))) v4u32*>(base + 16 * L) = v4u32{x0, x1, x2, x3};
-    lds_u8* rd = base + 128 * (a >> 2) + 32 * G + 8 * (a & 3);
-    const v4i16 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4i16*>(rd));
-    const v4i16 t1 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<__attribute__((address_space(3))) v4i16*>(rd + 512));
-    const v2u32 u0 = __builtin_bit_cast(v2u32, t0), u1 = __builtin_bit_cast(v2u32, t1);
-    R[0] = u0.x;
-    R[1] = u0.y;
-    R[2] = u1.x;
-    R[3] = u1.y;
-}
-
 template <int DT, bool LOGITS>
 __global__ __launch_bounds__(kResThreads) void row_resident_kernel(DecodeParams p, int64_t rows) {
     __shared__ __attribute__((aligned(16))) float lut[2 * kLutHalf];

@@ -100,7 +100,7 @@ def row_pass(hip):
     hip.lib.dbs_hip_set_row_pass(-1)
 
 
-@pytest.mark.parametrize("kind", [2, 1, 0])
+@pytest.mark.parametrize("kind", [2, 1, 0, 5])
 @pytest.mark.parametrize("seed", range(0, 30))
 def test_decode_16bit_row_passes(hip, oracle, row_pass, seed, kind):
     row_pass(kind)
@@ -143,13 +143,16 @@ def _bf16_exact(values):
     return v
 
 
-@pytest.mark.parametrize("m", [1.0, 1.5, 2.0, 4.0, 0.98828125, 0.5, 7.5, 2.0 ** 20, 1.5 * 2.0 ** 99,
-                               (2.0 - 2.0 ** -7) * 2.0 ** 127])
-def test_logsumexp_table_edges(hip, oracle, m):
-    """Rows whose terms sit at the edges of the per-row bfloat16 term table:
-    magnitudes around 2^(E-25) (where fl(x - max) stops depending on x), +-0,
-    subnormals, terms at exp(-87) and just past it, -inf, and maxima at and
-    below 1 (the Cephes fallback)."""
+@pytest.mark.parametrize("m", [1.0, 1.5, 2.0, 4.0, 0.98828125, 0.5, 7.5, 63.5, 126.0, 127.0, 200.0, 2.0 ** 20,
+                               1.5 * 2.0 ** 99, (2.0 - 2.0 ** -7) * 2.0 ** 127])
+@pytest.mark.parametrize("kind", [-1, 5])
+def test_logsumexp_table_edges(hip, oracle, row_pass, m, kind):
+    """Rows whose terms sit at the edges of the bfloat16 term tables:
+    magnitudes around 2^(E-25) (where fl(x - max) stops depending on x) and
+    around 2^-25 (the fixed-base table's first slot), +-0, subnormals, terms
+    at exp(-87) and just past it, magnitudes around 127.5 (the fixed-base
+    table's last slot), -inf, maxima at and below 1 and from 127 up (the
+    Cephes fallback)."""
     rng = np.random.default_rng(int(abs(np.log2(m)) * 1000) + 7)
     V = 4104
     m = float(_bf16_exact([m])[0])
@@ -158,6 +161,10 @@ def test_logsumexp_table_edges(hip, oracle, m):
     for k in range(-28, -20):
         t = 2.0 ** (E + k)
         specials += [t, -t, t * 1.0078125, -t * 1.0078125, t * 0.9921875, -t * 0.9921875]
+    for k in (-26, -25, -24):
+        t = 2.0 ** k
+        specials += [t, -t, t * 1.0078125, -t * 1.0078125, t * 0.9921875, -t * 0.9921875]
+    specials += [-126.5, -127.0, -127.5, -128.0, -200.0]
     specials += [0.0, -0.0, 1e-40, -1e-40, 2.0 ** -133, -(2.0 ** -133), -np.inf]
     for d in (86.0, 86.5, 87.0, 87.5, 88.0, 120.0, 127.0, 128.0, 130.0):
         specials += [m - d]
@@ -175,6 +182,7 @@ def test_logsumexp_table_edges(hip, oracle, m):
 
     xin = to_bits(x, "bf16")
     kw = dict(from_logits=True, eos_token=3, min_length=2, alpha=1.0)
+    row_pass(kind)
     want = oracle.decode(xin, dtype="bf16", **kw)
     got = hip.decode(xin, "bf16", **kw)
     diff = first_difference(got, want)

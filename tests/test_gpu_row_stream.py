@@ -1,21 +1,18 @@
 # SPDX-License-Identifier: MIT
-"""GPU parity of the streaming row pass (bfloat16 logits rows of 65537 to
-153600 entries, V % 8 == 0) against the CPU oracle, bit for bit on every
-decode output (tokens, parents, lengths, scores, final scores, row
-logsumexp, NaN/+inf flags).
+"""GPU parity of the persistent bfloat16 logits row passes against the CPU
+oracle, bit for bit on every decode output (tokens, parents, lengths, scores,
+final scores, row logsumexp, NaN/+inf flags): the streaming pass (kind 4,
+rows of 65537 to 153600 entries, V % 8 == 0; rows its table cannot take go to
+a fixup kernel) and the two-segment relay (kind 5, rows up to 155648
+entries; rows its fixed-base table cannot take fold from memory).
 
-The kernel is persistent over rows: each workgroup folds one row while the
-next streams into its registers, finishes the previous row's shortlist and
-builds the next row's term table. Rows the table cannot take (a NaN or +inf,
-a maximum below 1) go to a fixup kernel. The cases cover: random shapes and
-options (EOS, extra EOS, min_length, banned tokens, n-gram blocking,
-repetition penalty, per-example steps); a partial last chunk of 2048
-entries; many rows per workgroup; rows that need the fixup (NaN of either
-sign, +inf, maximum in (0, 1), every value negative, every value -inf); rows
-whose values are mostly +-0, or with fewer positive values than the shortlist
-holds;
-ties at the top past the survivor capacity; shortlist sizes 0, 1, 3 and the
-largest (K = 64); the overlapped decode."""
+The cases cover: random shapes and options (EOS, extra EOS, min_length,
+banned tokens, n-gram blocking, repetition penalty, per-example steps); a
+partial last chunk; many rows per workgroup; rows off the table path (NaN of
+either sign, +inf, maximum in (0, 1), every value negative, every value
+-inf); rows whose values are mostly +-0, or with fewer positive values than
+the shortlist holds; ties at the top past the survivor capacity; shortlist
+sizes 0, 1, 3 and the largest (K = 64); the overlapped decode."""
 
 import numpy as np
 import pytest
@@ -27,12 +24,13 @@ pytestmark = pytest.mark.gpu
 _VOCABS = [65544, 70000, 100008, 128256, 131072, 131080, 151936, 153600]
 
 
-@pytest.fixture
-def stream(hip):
-    """The streaming row pass, chosen explicitly (kind 4)."""
-    assert hip.lib.dbs_hip_set_row_pass(4) == -1
+@pytest.fixture(params=[4, 5], ids=["stream", "relay"])
+def stream(hip, request):
+    """The persistent bfloat16 logits row passes, chosen explicitly: the
+    streaming pass (kind 4) and the two-segment relay (kind 5)."""
+    prev = hip.lib.dbs_hip_set_row_pass(request.param)
     yield hip
-    hip.lib.dbs_hip_set_row_pass(-1)
+    hip.lib.dbs_hip_set_row_pass(prev)
 
 
 def _check(hip, oracle, xin, kw, label, **extra):
