@@ -13,21 +13,21 @@
 // segment 1's. The segments relay each other over a row:
 //
 //   phase 0  segment 1 transposes its part of the row (arrived in registers
-//            during the previous row) and takes its maxima; both segments
-//            exchange them: row maximum, NaN/+inf flag, the shortlist
-//            threshold (the M-th largest thread maximum) and the row's term
-//            table (fixed base, table_fits_fixed);
-//   phase A  segment 0 folds its stripes (the registers hold table offsets:
+//            during the previous row) and takes its maxima, while one
+//            wavefront of segment 0 finishes the previous row (lane tree,
+//            logsumexp, shortlist, RowInfo); both segments exchange the
+//            maxima: row maximum, NaN/+inf flag, the shortlist threshold (the
+//            M-th largest thread maximum) and the row's term table (fixed
+//            base, table_fits_fixed);
+//   phase A  segment 0 records its chunks that may hold survivors (x >=
+//            theta), folds its stripes (the registers hold table offsets:
 //            extract, look up, add) and streams its part of the next row
 //            into the registers it has passed; segment 1 turns its registers
-//            into table offsets, collects its survivors (x >= theta, from
-//            chunks whose key reaches theta, re-read from the cached row)
-//            and one of its wavefronts finishes the previous row (lane tree,
-//            logsumexp, shortlist, RowInfo);
+//            into table offsets and records its survivor chunks;
 //   phase B  segment 1 continues the lane chains over its stripes and
-//            streams its part of the next row; segment 0 collects its
-//            survivors, then transposes, keys and converts its part of the
-//            next row.
+//            streams its part of the next row;
+//            segment 0 transposes, keys and converts its part of the next
+//            row.
 //
 // Rows the fixed-base table does not cover (NaN/+inf, maximum below 1 or from
 // 127.5 up, every value negative) take their maximum and terms from the row
@@ -47,7 +47,7 @@ constexpr int kRlRegs = 152;                    // packed element pairs per thre
 constexpr int kRlChunks = kRlRegs / 4;          // 8-stripe chunks per thread
 constexpr int kRlStripes = 2 * 8 * kRlChunks;   // 608 stripes: V <= 155648
 constexpr uint32_t kBf16NegInf = 0xff80u;
-constexpr int kFinisher = 4;                    // the wavefront of segment 1 that finishes rows
+constexpr int kFinisher = 0;                    // the wavefront of segment 0 that finishes rows
 constexpr int kRecCap = 32;                     // survivor records per wavefront and row
 constexpr int kCkGroups = (kRlChunks + 7) / 8;  // chunk keys read eight at a time
 
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
     // table offsets) where its key reaches theta, kRecCap per wavefront
     __shared__ __attribute__((aligned(16))) uint4 s_rec[2][8 * kRecCap];
     __shared__ int s_rtok[2][8 * kRecCap];
-    __shared__ int s_nrec[2][8];
+    __shared__ __attribute__((aligned(16))) int s_nrec[2][8];
     __shared__ __attribute__((aligned(16))) int s_hist[2 * 256];
     __shared__ int s_wkey[8], s_wbad[8];
     __shared__ RowSlot s_rows[2];
@@ -164,36 +164,71 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         for (int c = 0; c < kRlChunks; ++c) issue_chunk(rs, voff, c);
     };
 
-    // ---- arrival: the segment's chunks transposed to lanes (elements past
-    // the row become -inf), the thread's packed signed and unsigned pattern
-    // maxima, and per chunk the largest signed pattern (the chunk's maximum
-    // where it is >= +0) in s_ck ----
+    // ---- arrival: the segment's chunks transposed to lanes (a lane's 16
+    // bytes past the row, V % 8 == 0, go in as -inf), the thread's packed
+    // signed and unsigned pattern maxima, per chunk the largest signed
+    // pattern (the chunk's maximum where it is >= +0) in s_ck, and the
+    // registers turned into table offsets (term_offsets) ----
     uint32_t t_smax = 0x80008000u, t_umax = 0u;
+    // the lane's loaded 16 bytes of chunk c are past the row from c = c_lim
+    // on (element 256 (s_begin + 8 c + l / 8) + 64 wv + 8 (l % 8) >= end)
+    auto lane_c_lim = [&]() __attribute__((always_inline)) -> int {
+        int lr = l;
+        asm volatile("" : "+v"(lr));
+        const int end_r = min(V, 256 * (s_begin + per));
+        const int first = 256 * (s_begin + (lr >> 3)) + 64 * wv + 8 * (lr & 7);
+        int c_lim = (end_r - first + 2047) >> 11;
+        asm volatile("" : "+v"(c_lim));
+        return c_lim;
+    };
+    // the maxima of the loaded registers as they are (each thread's values
+    // are then 8 lanes of 38 stripes: any partition of the row serves the
+    // row maximum and the shortlist threshold)
+    auto keys_loaded = [&]() __attribute__((always_inline)) {
+        const int c_lim = lane_c_lim();
+        uint32_t smax = 0x80008000u, umax = 0u;
+        unrolled<kRlChunks>([&](auto cc) __attribute__((always_inline)) {
+            constexpr int c = decltype(cc)::value;
+            const bool in = c < c_lim;
+            const uint32_t a = in ? reg[4 * c] : kBf16NegInf * 0x10001u;
+            const uint32_t b2 = in ? reg[4 * c + 1] : kBf16NegInf * 0x10001u;
+            const uint32_t c2 = in ? reg[4 * c + 2] : kBf16NegInf * 0x10001u;
+            const uint32_t d = in ? reg[4 * c + 3] : kBf16NegInf * 0x10001u;
+            smax = pk_max_i16(smax, pk_max_i16(pk_max_i16(a, b2), pk_max_i16(c2, d)));
+            umax = pk_max_u16(umax, pk_max_u16(pk_max_u16(a, b2), pk_max_u16(c2, d)));
+            asm volatile("" : "+v"(smax), "+v"(umax));  // chunk by chunk: no masked copies kept
+        });
+        t_smax = smax;
+        t_umax = umax;
+    };
     auto arrive = [&]() __attribute__((always_inline)) {
-        int jr = j, lr = l, end_r = min(V, 256 * (s_begin + per));
-        asm volatile("" : "+v"(jr), "+v"(lr));
-        asm volatile("" : "+s"(end_r));
+        int lr = l;
+        asm volatile("" : "+v"(lr));
+        const int c_lim = lane_c_lim();
+        // chunk c's registers masked in place just before its transpose
+        auto mask_chunk = [&](int c) __attribute__((always_inline)) {
+            const bool in = c < c_lim;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                reg[4 * c + q] = in ? reg[4 * c + q] : kBf16NegInf * 0x10001u;
+                asm volatile("" : "+v"(reg[4 * c + q]));
+            }
+        };
         uint32_t smax = 0x80008000u, umax = 0u;
         // two chunks' transposes in flight (chunk c's values in T[c % 2]);
         // one slot serves both: a wavefront's LDS operations run in order
         uint32_t T[2][4];
         uint32_t ckp[4];  // the keys of eight chunks, two per register, written together
+        mask_chunk(0);
         transpose_chunk(stage, lr, reg[0], reg[1], reg[2], reg[3], T[0]);
+        mask_chunk(1);
         transpose_chunk(stage, lr, reg[4], reg[5], reg[6], reg[7], T[1]);
         unrolled<kRlChunks>([&](auto cc) __attribute__((always_inline)) {
             constexpr int c = decltype(cc)::value;
-            uint32_t R4[4] = {T[c & 1][0], T[c & 1][1], T[c & 1][2], T[c & 1][3]};
-            if constexpr (c + 2 < kRlChunks)
+            const uint32_t R4[4] = {T[c & 1][0], T[c & 1][1], T[c & 1][2], T[c & 1][3]};
+            if constexpr (c + 2 < kRlChunks) {
+                mask_chunk(c + 2);
                 transpose_chunk(stage, lr, reg[4 * c + 8], reg[4 * c + 9], reg[4 * c + 10], reg[4 * c + 11], T[c & 1]);
-            const int sb = s_begin + 8 * c;
-            if (256 * (sb + 8) > end_r) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const bool lo_out = 256 * (sb + 2 * q) + jr >= end_r;
-                    const bool hi_out = 256 * (sb + 2 * q + 1) + jr >= end_r;
-                    R4[q] = (lo_out ? kBf16NegInf : (R4[q] & 0xffffu)) |
-                            (hi_out ? (kBf16NegInf << 16) : (R4[q] & 0xffff0000u));
-                }
             }
             const uint32_t kc = pk_max_i16(pk_max_i16(R4[0], R4[1]), pk_max_i16(R4[2], R4[3]));
             smax = pk_max_i16(smax, kc);
@@ -207,18 +242,15 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
                 for (int u = ((c & 7) >> 1) + 1; u < 4; ++u) ckp[u] = 0x80008000u;  // chunks past the last
                 *reinterpret_cast<uint4*>(&s_ck[c >> 3][tid][0]) = make_uint4(ckp[0], ckp[1], ckp[2], ckp[3]);
             }
+            asm volatile("" : "+v"(smax), "+v"(umax));  // the maxima taken here: the patterns die here
 #pragma unroll
-            for (int q = 0; q < 4; ++q) reg[4 * c + q] = R4[q];
+            for (int q = 0; q < 4; ++q) {
+                reg[4 * c + q] = term_offsets(R4[q]);
+                asm volatile("" : "+v"(reg[4 * c + q]));
+            }
         });
         t_smax = smax;
         t_umax = umax;
-    };
-    // ---- the registers as table offsets (term_offsets), taken here ----
-    auto convert = [&]() __attribute__((always_inline)) {
-#pragma unroll
-        for (int k = 0; k < kRlRegs; ++k) reg[k] = term_offsets(reg[k]);
-#pragma unroll
-        for (int k = 0; k < kRlRegs; ++k) asm volatile("" : "+v"(reg[k]));
     };
 
     // ---- the segment's part of a lane chain from the table offsets; the
@@ -309,21 +341,33 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
             keys[4 * g + 2] = kq.z;
             keys[4 * g + 3] = kq.w;
         }
-        unrolled<kRlChunks>([&](auto cc) __attribute__((always_inline)) {
-            constexpr int c = decltype(cc)::value;
-            const int ck = static_cast<int16_t>(keys[c >> 1] >> (16 * (c & 1)));
-            const bool flagged = any_thread && ck >= tk;
-            const uint64_t bal = __ballot(flagged);
-            if (bal != 0) {
-                const int slot = n + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
-                                         static_cast<uint32_t>(bal >> 32),
-                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
-                if (flagged && slot < kRecCap) {
-                    out[slot] = make_uint4(reg[4 * c], reg[4 * c + 1], reg[4 * c + 2], reg[4 * c + 3]);
-                    tok_out[slot] = 256 * (s_begin + 8 * c) + j;
+        // eight chunks at a time: a group is passed over unless one of its
+        // keys reaches tk on some lane (the packed maximum of its keys)
+        unrolled<kCkGroups>([&](auto gg) __attribute__((always_inline)) {
+            constexpr int g = decltype(gg)::value;
+            const uint32_t gm = pk_max_i16(pk_max_i16(keys[4 * g], keys[4 * g + 1]),
+                                           pk_max_i16(keys[4 * g + 2], keys[4 * g + 3]));
+            const int gk = max(static_cast<int>(static_cast<int16_t>(gm & 0xffffu)),
+                               static_cast<int>(static_cast<int16_t>(gm >> 16)));
+            if (!__any(any_thread && gk >= tk)) return;
+            unrolled<8>([&](auto ii) __attribute__((always_inline)) {
+                constexpr int c = 8 * g + decltype(ii)::value;
+                if constexpr (c < kRlChunks) {
+                    const int ck = static_cast<int16_t>(keys[c >> 1] >> (16 * (c & 1)));
+                    const bool flagged = any_thread && ck >= tk;
+                    const uint64_t bal = __ballot(flagged);
+                    if (bal != 0) {
+                        const int slot = n + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                                 static_cast<uint32_t>(bal >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
+                        if (flagged && slot < kRecCap) {
+                            out[slot] = make_uint4(reg[4 * c], reg[4 * c + 1], reg[4 * c + 2], reg[4 * c + 3]);
+                            tok_out[slot] = 256 * (s_begin + 8 * c) + j;
+                        }
+                        n += __popcll(bal);
+                    }
                 }
-                n += __popcll(bal);
-            }
+            });
         });
         if (l == 0) s_nrec[pb][wave] = n;
     };
@@ -341,9 +385,13 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         info.invalid = bad ? 1u : 0u;
         info.bound = -kInf;
         info.count = 0;
+        // the eight wavefronts' record counts, read once
+        const int4 n_lo = *reinterpret_cast<const int4*>(&s_nrec[pb][0]);
+        const int4 n_hi = *reinterpret_cast<const int4*>(&s_nrec[pb][4]);
+        const int nrec[8] = {n_lo.x, n_lo.y, n_lo.z, n_lo.w, n_hi.x, n_hi.y, n_hi.z, n_hi.w};
         bool overflow = full;
-#pragma unroll 1
-        for (int w = 0; w < 8; ++w) overflow = overflow || s_nrec[pb][w] > kRecCap;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) overflow = overflow || nrec[w] > kRecCap;
         if (M > 0 && lse != -kInf && !overflow) {
             const uint32_t thr = 4u * static_cast<uint32_t>(tk - static_cast<int>(kFixedBase - 1u));
             // the eight wavefronts' lists read as one (list w from prefix[w]),
@@ -351,7 +399,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
             int prefix[9];
             prefix[0] = 0;
 #pragma unroll
-            for (int w = 0; w < 8; ++w) prefix[w + 1] = prefix[w] + __builtin_amdgcn_readfirstlane(s_nrec[pb][w]);
+            for (int w = 0; w < 8; ++w) prefix[w + 1] = prefix[w] + __builtin_amdgcn_readfirstlane(nrec[w]);
             const int total = prefix[8];
             const bool check = p.banned != nullptr || p.banned_pe != nullptr || mask;
             int n = 0;
@@ -366,25 +414,46 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
                 const uint4 q = has ? s_rec[pb][src] : make_uint4(0u, 0u, 0u, 0u);
                 const int t0 = has ? s_rtok[pb][src] : 0;
                 const uint32_t R[4] = {q.x, q.y, q.z, q.w};
+                // the record's survivors as a bit mask (element e = stripe
+                // 8c + e), placed after those of the lanes below (a prefix
+                // sum of the counts, bit plane by bit plane)
+                uint32_t hits = 0;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const uint32_t a = (R[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-                    const int v = t0 + 256 * e;
-                    bool hit = has && a >= thr && a < 4u * kLutHalf;
-                    if (check && hit) hit = !static_masked(p, bb, v, mask);
-                    const uint64_t bal = __ballot(hit);
-                    if (bal != 0) {
-                        const float x = bf16_to_f32(static_cast<uint16_t>((a >> 2) + (kFixedBase - 1u)));
-                        const int slot = n + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
-                                                 static_cast<uint32_t>(bal >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
-                        if (hit && slot < kSurvivorCap) {
-                            s_key[slot] = survivor_key(x, v);
-                            s_x[slot] = x;
-                        }
-                        n += __popcll(bal);
+                    hits |= (has && a >= thr && a < 4u * kLutHalf) ? (1u << e) : 0u;
+                }
+                if (check) {
+#pragma unroll 1
+                    for (uint32_t h = hits; h != 0; h &= h - 1) {
+                        const int e = __ffs(h) - 1;
+                        if (static_masked(p, bb, t0 + 256 * e, mask)) hits &= ~(1u << e);
                     }
                 }
+                const int cnt = __popc(hits);
+                int before = 0, pass_total = 0;
+#pragma unroll
+                for (int bit = 0; bit < 4; ++bit) {
+                    const uint64_t plane = __ballot((cnt >> bit) & 1);
+                    before += static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                  static_cast<uint32_t>(plane >> 32),
+                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(plane), 0u)))
+                              << bit;
+                    pass_total += __popcll(plane) << bit;
+                }
+                int slot = n + before;
+#pragma unroll 1
+                for (uint32_t h = hits; h != 0; h &= h - 1, ++slot) {
+                    const int e = __ffs(h) - 1;
+                    const uint32_t w2 = e < 4 ? (e < 2 ? R[0] : R[1]) : (e < 6 ? R[2] : R[3]);
+                    const uint32_t a = (w2 >> (16 * (e & 1))) & 0xffffu;
+                    if (slot < kSurvivorCap) {
+                        const float x = bf16_to_f32(static_cast<uint16_t>((a >> 2) + (kFixedBase - 1u)));
+                        s_key[slot] = survivor_key(x, t0 + 256 * e);
+                        s_x[slot] = x;
+                    }
+                }
+                n += pass_total;
             }
             if (n > kSurvivorCap) {
                 overflow = true;
@@ -400,7 +469,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
                     const int i = i0 + l;
                     const uint64_t ki = i < n ? s_key[i] : ~0ull;
                     int rank = 0;
-#pragma unroll 1
+#pragma unroll 4
                     for (int jp = 0; jp < npair; ++jp) {
                         const uint4 a = k2[jp];
                         rank += static_cast<int>(((static_cast<uint64_t>(a.y) << 32) | a.x) > ki) +
@@ -425,32 +494,33 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         signal_row_done(p, rr, l);
     };
 
-    // ---- the previous row, finished by wavefront kFinisher in phase A ----
-    bool pend = false;
-    int64_t pend_r = 0;
-    float pend_m = 0.0f, pend_theta = 0.0f;
-    bool pend_bad = false, pend_lse = false, pend_mask = false, pend_full = false;
-    int pend_b = 0, pend_par = 0, pend_tk = 1;
-    auto finish_pending = [&]() __attribute__((always_inline)) {
+    // ---- a row's lane tree, logsumexp, shortlist and RowInfo (wavefront
+    // kFinisher, once both chains are done) ----
+    auto finish_row = [&](int pb, int64_t rr, float m, float theta, int tk, bool full, bool bad, bool do_lse, int bb,
+                          bool mask) __attribute__((always_inline)) {
         float lse = -kInf;
-        if (pend_lse) {
+        if (do_lse) {
             float a[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) a[e] = s_acc[pend_par][4 * l + e];
-            lse = logsumexp_from(pend_m, lane_tree_sum(a, l));
+            for (int e = 0; e < 4; ++e) a[e] = s_acc[pb][4 * l + e];
+            lse = logsumexp_from(m, lane_tree_sum(a, l));
         }
-        finish_records(pend_par, pend_r, lse, pend_theta, pend_tk, pend_full, pend_bad, pend_b, pend_mask);
-        if (l < 8) s_nrec[pend_par][l] = 0;
-        pend = false;
+        finish_records(pb, rr, lse, theta, tk, full, bad, bb, mask);
+        if (l < 8) s_nrec[pb][l] = 0;
     };
 
-    // ---- prologue: the first row in flight; segment 0 takes its part now ----
+    // ---- the first row in flight; segment 0 arrives ----
     if (r < rows) issue_loads(r);
-    if (seg == 0) {
-        arrive();
-        convert();
-    }
+    if (seg == 0 && r < rows) arrive();
 
+    // Each routine has one static copy, which both segments run at
+    // different steps (the code of a row must stay in the instruction
+    // cache): phase 0, segment 1's raw maxima while wavefront kFinisher
+    // finishes the previous row; the exchange and the term table (B1, B2);
+    // then two steps h = 0, 1 closed by barriers B3 and B4: in step 0
+    // segment 1 arrives (transposes and converts) and both record their
+    // survivor chunks, and segment 0 folds its stripes; in step 1 segment
+    // 0 arrives with the next row and segment 1 folds its stripes.
     while (r < rows) {
         int bn = 0, lenn = 0;
         int64_t rn = rows;
@@ -463,7 +533,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         const uint16_t* row = static_cast<const uint16_t*>(p.x) + r * V;
 
         // ---- phase 0 ----
-        if (seg == 1) arrive();
+        if (seg == 1) keys_loaded();
         const int tkey = max(static_cast<int>(static_cast<int16_t>(t_smax & 0xffffu)),
                              static_cast<int>(static_cast<int16_t>(t_smax >> 16)));
         const int tumax = static_cast<int>(max(t_umax & 0xffffu, t_umax >> 16));
@@ -532,58 +602,38 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         if (need_m) m = memory_max(row);
         const bool do_lse = m > -kInf;
 
-        // ---- phases A and B: one lane-chain routine, run by segment 0 in
-        // phase A while segment 1 converts, collects and finishes the
-        // previous row, then by segment 1 (after the barrier closing its
-        // block) while segment 0 collects and takes its part of the next
-        // row. A row the table does not cover runs the chain for its loads
-        // only and folds from memory. ----
+        // ---- phases A and B. A row the table does not cover runs the
+        // chain for its loads only and folds from memory. ----
         if (tickets) {
             int bt = 0, lt = 0;
             rn = read_row_slot(s_rows[par ^ 1], bt, lt);  // published before the first barrier
             bn = bt;
             lenn = lt;
         }
-        if (seg == 1) {
-            convert();
-            if (wave == kFinisher && pend) finish_pending();
-            lds_barrier();
+#pragma unroll 1
+        for (int h = 0; h < 2; ++h) {
+            if ((h == 0) == (seg == 1) && (h == 0 || rn < rows)) arrive();
+            if (h == 0 && records) {
+                const int tk_thread = max(static_cast<int>(static_cast<int16_t>(t_smax & 0xffffu)),
+                                          static_cast<int>(static_cast<int16_t>(t_smax >> 16)));
+                take_records(par, tk, tk_thread);
+            }
+            if ((h == 0) == (seg == 0)) {
+                const float a0 = seg == 0 ? 0.0f : s_acc[par][j];
+                float acc = chain_table(a0, rn);
+                if (!fast) acc = do_lse ? chain_memory(a0, m, row) : a0;
+                s_acc[par][j] = acc;
+            }
+            lds_barrier();  // h = 0: B3, h = 1: B4
+            if (h == 0 && seg == 0) s_hist2[tid] = 0;  // every wavefront has its b2
         }
-        // the segment's survivors, then its part of the lane chains
-        if (records) take_records(par, tk, tkey);
-        {
-            const float a0 = seg == 0 ? 0.0f : s_acc[par][j];
-            float acc = chain_table(a0, rn);
-            if (!fast) acc = do_lse ? chain_memory(a0, m, row) : a0;
-            s_acc[par][j] = acc;
-        }
-        if (seg == 0) {
-            lds_barrier();
-            s_hist2[tid] = 0;  // every wavefront has its b2
-            arrive();
-            convert();
-        }
-        lds_barrier();
+        if (wave == kFinisher) finish_row(par, r, m, theta, tk, full, any_bad, do_lse, b, mask_eos);
 
-        if (wave == kFinisher) {
-            pend = true;
-            pend_r = r;
-            pend_m = m;
-            pend_theta = theta;
-            pend_bad = any_bad;
-            pend_lse = do_lse;
-            pend_mask = mask_eos;
-            pend_full = full;
-            pend_tk = tk;
-            pend_b = b;
-            pend_par = par;
-        }
         r = rn;
         b = bn;
         new_len = lenn;
         par ^= 1;
     }
-    if (wave == kFinisher && pend) finish_pending();
 }
 
 int g_relay_cus[64];
