@@ -118,9 +118,18 @@ __device__ __forceinline__ bool row_is_read(const DecodeParams& p, int64_t r, in
         new_len = gload(p.st_len, r) + 1;
         return true;
     }
-    b = static_cast<int>(r / (static_cast<int64_t>(p.T) * K));
-    const int t = static_cast<int>((r / K) % p.T);
-    const int k = static_cast<int>(r % K);
+    int t = 0, k = 0;
+    if (r < 0x7fffffff) {  // 32-bit quotients (the usual case)
+        const uint32_t r32 = static_cast<uint32_t>(r), K32 = static_cast<uint32_t>(K);
+        const uint32_t bt = r32 / K32;
+        k = static_cast<int>(r32 - bt * K32);
+        b = static_cast<int>(bt / static_cast<uint32_t>(p.T));
+        t = static_cast<int>(bt - static_cast<uint32_t>(b) * static_cast<uint32_t>(p.T));
+    } else {
+        b = static_cast<int>(r / (static_cast<int64_t>(p.T) * K));
+        t = static_cast<int>((r / K) % p.T);
+        k = static_cast<int>(r % K);
+    }
     if (t >= example_steps(p, b) || (t == 0 && k != 0) || k >= beams_of(p, b)) return false;
     new_len = t + 1;  // every unfinished live beam has length t at step t
     return true;

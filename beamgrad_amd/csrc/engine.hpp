@@ -175,6 +175,9 @@ bool row_stream_eligible(const DecodeParams& p);
 hipError_t launch_row_stream(const DecodeParams& p, int64_t rows, hipStream_t stream);
 // bfloat16 logits, both segments of a 512-thread workgroup relaying (row_relay.hip)
 bool row_relay_eligible(const DecodeParams& p);
+// The relay row pass is the default for the rows it fills (it always folds
+// its full register capacity, so shorter rows take the resident pass).
+bool row_relay_preferred(const DecodeParams& p);
 hipError_t launch_row_relay(const DecodeParams& p, int64_t rows, hipStream_t stream);
 bool row_logprob_eligible(const DecodeParams& p);
 hipError_t launch_row_logprob(const DecodeParams& p, int64_t rows, hipStream_t stream);

@@ -171,7 +171,7 @@ std::atomic<int> g_row_pass_kind{-1};
 bool row_pass_persistent(const DecodeParams& p) {
     const int kind = g_row_pass_kind.load(std::memory_order_relaxed);
     if ((kind == -1 || kind == 3) && row_logprob_eligible(p)) return false;
-    if (kind == 5 && row_relay_eligible(p)) return true;
+    if ((kind == 5 || (kind == -1 && row_relay_preferred(p))) && row_relay_eligible(p)) return true;
     if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return true;
     if ((kind == -1 || kind == 4) && row_stream_eligible(p)) return true;
     return (kind == -1 || kind == 2) && row_pipe_eligible(p);
@@ -185,7 +185,8 @@ hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream) {
     KernelTimer timer(kKindRowPass, stream);
     const int kind = g_row_pass_kind.load(std::memory_order_relaxed);
     if ((kind == -1 || kind == 3) && row_logprob_eligible(p)) return launch_row_logprob(p, rows, stream);
-    if (kind == 5 && row_relay_eligible(p)) return launch_row_relay(p, rows, stream);
+    if ((kind == 5 || (kind == -1 && row_relay_preferred(p))) && row_relay_eligible(p))
+        return launch_row_relay(p, rows, stream);
     if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return launch_row_resident(p, rows, stream);
     if ((kind == -1 || kind == 4) && row_stream_eligible(p)) {
         // the streaming pass, then the rows it left (NaN/+inf, no term table)

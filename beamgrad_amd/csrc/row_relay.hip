@@ -63,7 +63,9 @@ __device__ __forceinline__ void unrolled(F&& f) {
     unrolled_seq(f, std::make_integer_sequence<int, N>{});
 }
 
-template <bool kUnused>
+// Chunks below kMaskFrom are inside the row on every lane of both segments
+// (the launch checks it): only the later ones are masked.
+template <int kMaskFrom>
 __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, int64_t rows) {
     // (the table first: at LDS address 0 its offsets need no base added)
     __shared__ __attribute__((aligned(1024))) float lut[2 * kLutHalf];
@@ -116,11 +118,14 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(rr) >> 32));
         return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
     };
-    int64_t q_next = 0;  // thread 0's processing index (tickets)
+    // tickets are drawn by a thread of segment 1, which has time to spare
+    // in phase 0 (segment 0's wavefront kFinisher is then busy)
+    constexpr int kPublisher = 256;
+    int64_t q_next = 0;  // the publisher's processing index (tickets)
     int b = 0, new_len = 0, par = 0;
     int64_t r = rows;
     if (tickets) {
-        if (tid == 0) {
+        if (tid == kPublisher) {
             q_next = first_ticket(p);
             int b0 = 0, len0 = 0;
             s_rows[0].r = find_read_row(p, rows, q_next, b0, len0);
@@ -181,6 +186,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         asm volatile("" : "+v"(c_lim));
         return c_lim;
     };
+
     // the maxima of the loaded registers as they are (each thread's values
     // are then 8 lanes of 38 stripes: any partition of the row serves the
     // row maximum and the shortlist threshold)
@@ -189,11 +195,14 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         uint32_t smax = 0x80008000u, umax = 0u;
         unrolled<kRlChunks>([&](auto cc) __attribute__((always_inline)) {
             constexpr int c = decltype(cc)::value;
-            const bool in = c < c_lim;
-            const uint32_t a = in ? reg[4 * c] : kBf16NegInf * 0x10001u;
-            const uint32_t b2 = in ? reg[4 * c + 1] : kBf16NegInf * 0x10001u;
-            const uint32_t c2 = in ? reg[4 * c + 2] : kBf16NegInf * 0x10001u;
-            const uint32_t d = in ? reg[4 * c + 3] : kBf16NegInf * 0x10001u;
+            uint32_t a = reg[4 * c], b2 = reg[4 * c + 1], c2 = reg[4 * c + 2], d = reg[4 * c + 3];
+            if constexpr (c >= kMaskFrom) {
+                const bool in = c < c_lim;
+                a = in ? a : kBf16NegInf * 0x10001u;
+                b2 = in ? b2 : kBf16NegInf * 0x10001u;
+                c2 = in ? c2 : kBf16NegInf * 0x10001u;
+                d = in ? d : kBf16NegInf * 0x10001u;
+            }
             smax = pk_max_i16(smax, pk_max_i16(pk_max_i16(a, b2), pk_max_i16(c2, d)));
             umax = pk_max_u16(umax, pk_max_u16(pk_max_u16(a, b2), pk_max_u16(c2, d)));
             asm volatile("" : "+v"(smax), "+v"(umax));  // chunk by chunk: no masked copies kept
@@ -206,7 +215,9 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         asm volatile("" : "+v"(lr));
         const int c_lim = lane_c_lim();
         // chunk c's registers masked in place just before its transpose
-        auto mask_chunk = [&](int c) __attribute__((always_inline)) {
+        auto mask_chunk = [&](auto cc) __attribute__((always_inline)) {
+            constexpr int c = decltype(cc)::value;
+            if constexpr (c < kMaskFrom) return;
             const bool in = c < c_lim;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -219,15 +230,15 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         // one slot serves both: a wavefront's LDS operations run in order
         uint32_t T[2][4];
         uint32_t ckp[4];  // the keys of eight chunks, two per register, written together
-        mask_chunk(0);
+        mask_chunk(std::integral_constant<int, 0>{});
         transpose_chunk(stage, lr, reg[0], reg[1], reg[2], reg[3], T[0]);
-        mask_chunk(1);
+        mask_chunk(std::integral_constant<int, 1>{});
         transpose_chunk(stage, lr, reg[4], reg[5], reg[6], reg[7], T[1]);
         unrolled<kRlChunks>([&](auto cc) __attribute__((always_inline)) {
             constexpr int c = decltype(cc)::value;
             const uint32_t R4[4] = {T[c & 1][0], T[c & 1][1], T[c & 1][2], T[c & 1][3]};
             if constexpr (c + 2 < kRlChunks) {
-                mask_chunk(c + 2);
+                mask_chunk(std::integral_constant<int, c + 2>{});
                 transpose_chunk(stage, lr, reg[4 * c + 8], reg[4 * c + 9], reg[4 * c + 10], reg[4 * c + 11], T[c & 1]);
             }
             const uint32_t kc = pk_max_i16(pk_max_i16(R4[0], R4[1]), pk_max_i16(R4[2], R4[3]));
@@ -327,8 +338,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
     // hold x >= theta) is recorded with its first token, the wavefront's
     // records placed by ballot (no atomics) ----
     auto take_records = [&](int pb, int tk, int tkey) __attribute__((always_inline)) {
-        const bool any_thread = tkey >= tk;
-        if (!__any(any_thread)) return;
+        if (!__any(tkey >= tk)) return;  // no chunk of the wavefront reaches tk
         int n = 0;
         uint4* out = s_rec[pb] + kRecCap * wave;
         int* tok_out = s_rtok[pb] + kRecCap * wave;
@@ -349,13 +359,13 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
                                            pk_max_i16(keys[4 * g + 2], keys[4 * g + 3]));
             const int gk = max(static_cast<int>(static_cast<int16_t>(gm & 0xffffu)),
                                static_cast<int>(static_cast<int16_t>(gm >> 16)));
-            if (!__any(any_thread && gk >= tk)) return;
+            if (__builtin_amdgcn_ballot_w64(gk >= tk) == 0) return;
             unrolled<8>([&](auto ii) __attribute__((always_inline)) {
                 constexpr int c = 8 * g + decltype(ii)::value;
                 if constexpr (c < kRlChunks) {
                     const int ck = static_cast<int16_t>(keys[c >> 1] >> (16 * (c & 1)));
-                    const bool flagged = any_thread && ck >= tk;
-                    const uint64_t bal = __ballot(flagged);
+                    const bool flagged = ck >= tk;
+                    const uint64_t bal = __builtin_amdgcn_ballot_w64(flagged);
                     if (bal != 0) {
                         const int slot = n + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
                                                  static_cast<uint32_t>(bal >> 32),
@@ -372,19 +382,21 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         if (l == 0) s_nrec[pb][wave] = n;
     };
 
-    // ---- a row's shortlist from its records (one wavefront): the
+    // ---- a row's shortlist from its records, in two parts (one
+    // wavefront). finish_extract, once the records are complete: the
     // survivors (positive, slot reaching tk's, so x >= theta; not statically
-    // masked), each placed by its rank (the count of survivor keys above its
-    // own; keys are distinct), the bound at rank M (else theta), the
-    // RowInfo. More records or survivors than kept: no shortlist. ----
-    auto finish_records = [&](int pb, int64_t rr, float lse, float theta, int tk, bool full, bool bad, int bb,
-                              bool mask) __attribute__((always_inline)) {
-        const bool coherent = p.step_done != nullptr;
-        RowInfo info;
-        info.lse = lse;
-        info.invalid = bad ? 1u : 0u;
-        info.bound = -kInf;
-        info.count = 0;
+    // masked) into s_key and s_x. finish_publish, once the row's logsumexp is
+    // known: each survivor ranked by the count of survivor keys above its own
+    // (keys are distinct), the entries of rank < M, the bound at rank M (else
+    // theta), the RowInfo. More records or survivors than kept: no
+    // shortlist. ----
+    struct Extracted {
+        int n;          // survivors, keys in s_key and values in s_x
+        bool overflow;  // no shortlist
+    };
+    auto finish_extract = [&](int pb, int tk, bool full, bool live, int bb, bool mask) __attribute__((always_inline)) {
+        Extracted st;
+        st.n = 0;
         // the eight wavefronts' record counts, read once
         const int4 n_lo = *reinterpret_cast<const int4*>(&s_nrec[pb][0]);
         const int4 n_hi = *reinterpret_cast<const int4*>(&s_nrec[pb][4]);
@@ -392,7 +404,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         bool overflow = full;
 #pragma unroll
         for (int w = 0; w < 8; ++w) overflow = overflow || nrec[w] > kRecCap;
-        if (M > 0 && lse != -kInf && !overflow) {
+        if (M > 0 && live && !overflow) {
             const uint32_t thr = 4u * static_cast<uint32_t>(tk - static_cast<int>(kFixedBase - 1u));
             // the eight wavefronts' lists read as one (list w from prefix[w]),
             // 64 records a pass, one per lane
@@ -455,63 +467,64 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
                 }
                 n += pass_total;
             }
-            if (n > kSurvivorCap) {
-                overflow = true;
-            } else {
-                if ((n & 1) && l == 0) s_key[n] = 0;  // a zero key pads the pairs read below
-                wave_sync();
-                ShortEntry* out = p.shortlist + rr * M;
-                const uint4* k2 = reinterpret_cast<const uint4*>(s_key);
-                const int npair = (n + 1) >> 1;
-                float bound_x = -kInf;
-#pragma unroll 1
-                for (int i0 = 0; i0 < n; i0 += 64) {
-                    const int i = i0 + l;
-                    const uint64_t ki = i < n ? s_key[i] : ~0ull;
-                    int rank = 0;
-#pragma unroll 4
-                    for (int jp = 0; jp < npair; ++jp) {
-                        const uint4 a = k2[jp];
-                        rank += static_cast<int>(((static_cast<uint64_t>(a.y) << 32) | a.x) > ki) +
-                                static_cast<int>(((static_cast<uint64_t>(a.w) << 32) | a.z) > ki);
-                    }
-                    const float x = i < n ? s_x[i] : 0.0f;
-                    if (i < n && rank < M) {
-                        const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(ki & 0xffffffffu));
-                        publish_entry(out, rank, x - lse, tok, coherent);
-                    }
-                    const uint64_t at_m = __ballot(i < n && rank == M);
-                    if (at_m != 0) bound_x = __shfl(x, __ffsll(static_cast<long long>(at_m)) - 1);
-                }
-                info.count = n < M ? n : M;
-                const float bx = n > M ? bound_x : theta;
-                info.bound = bx > -kInf ? bx - lse : -kInf;
-                wave_sync();
-            }
+            st.n = n;
+            if (n > kSurvivorCap) overflow = true;
+            else if ((n & 1) && l == 0) s_key[n] = 0;  // a zero key pads the pairs read when ranking
         }
-        if (M > 0 && lse != -kInf && overflow) info.count = -1;
+        st.overflow = overflow;
+        return st;
+    };
+    auto finish_publish = [&](const Extracted& st, int64_t rr, float lse, float theta, bool bad) __attribute__((always_inline)) {
+        const bool coherent = p.step_done != nullptr;
+        RowInfo info;
+        info.lse = lse;
+        info.invalid = bad ? 1u : 0u;
+        info.bound = -kInf;
+        info.count = 0;
+        const int n = st.n;
+        if (M > 0 && lse != -kInf && !st.overflow) {
+            ShortEntry* out = p.shortlist + rr * M;
+            float bound_x = -kInf;
+            const uint4* k2 = reinterpret_cast<const uint4*>(s_key);
+            const int npair = (n + 1) >> 1;
+#pragma unroll 1
+            for (int i0 = 0; i0 < n; i0 += 64) {
+                const int i = i0 + l;
+                const uint64_t ki = i < n ? s_key[i] : ~0ull;
+                int rank = 0;
+#pragma unroll 8
+                for (int jp = 0; jp < npair; ++jp) {
+                    const uint4 a = k2[jp];
+                    rank += static_cast<int>(((static_cast<uint64_t>(a.y) << 32) | a.x) > ki) +
+                            static_cast<int>(((static_cast<uint64_t>(a.w) << 32) | a.z) > ki);
+                }
+                const float x = i < n ? s_x[i] : 0.0f;
+                if (i < n && rank < M) {
+                    const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(ki & 0xffffffffu));
+                    publish_entry(out, rank, x - lse, tok, coherent);
+                }
+                const uint64_t at_m = __ballot(i < n && rank == M);
+                if (at_m != 0) bound_x = __shfl(x, __ffsll(static_cast<long long>(at_m)) - 1);
+            }
+            info.count = n < M ? n : M;
+            const float bx = n > M ? bound_x : theta;
+            info.bound = bx > -kInf ? bx - lse : -kInf;
+        }
+        if (M > 0 && lse != -kInf && st.overflow) info.count = -1;
         if (l == 0) publish_rowinfo(p.rowinfo + rr, info, coherent);
         signal_row_done(p, rr, l);
     };
 
-    // ---- a row's lane tree, logsumexp, shortlist and RowInfo (wavefront
-    // kFinisher, once both chains are done) ----
-    auto finish_row = [&](int pb, int64_t rr, float m, float theta, int tk, bool full, bool bad, bool do_lse, int bb,
-                          bool mask) __attribute__((always_inline)) {
-        float lse = -kInf;
-        if (do_lse) {
-            float a[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) a[e] = s_acc[pb][4 * l + e];
-            lse = logsumexp_from(m, lane_tree_sum(a, l));
-        }
-        finish_records(pb, rr, lse, theta, tk, full, bad, bb, mask);
-        if (l < 8) s_nrec[pb][l] = 0;
-    };
+    Extracted fin;
 
     // ---- the first row in flight; segment 0 arrives ----
     if (r < rows) issue_loads(r);
     if (seg == 0 && r < rows) arrive();
+    // segment 0 finds each next row one step ahead, where it has time (the
+    // row after the one it streams in)
+    int64_t r_ahead = rows;
+    int b_ahead = 0, len_ahead = 0;
+    if (!tickets && seg == 0) r_ahead = next_read_row(r + gridDim.x, b_ahead, len_ahead);
 
     // Each routine has one static copy, which both segments run at
     // different steps (the code of a row must stay in the instruction
@@ -525,9 +538,13 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         int bn = 0, lenn = 0;
         int64_t rn = rows;
         if (tickets) {
-            if (tid == 0) publish_next_row(p, rows, q_next, s_rows[par ^ 1]);
-        } else {
+            if (tid == kPublisher) publish_next_row(p, rows, q_next, s_rows[par ^ 1]);
+        } else if (seg == 1) {
             rn = next_read_row(r + gridDim.x, bn, lenn);
+        } else {
+            rn = r_ahead;
+            bn = b_ahead;
+            lenn = len_ahead;
         }
         const bool mask_eos = new_len < min_length_of(p, b);
         const uint16_t* row = static_cast<const uint16_t*>(p.x) + r * V;
@@ -571,7 +588,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
             // positive slots above m hold 0
             const uint32_t mp = f32_bits(m) >> 16;
             const float em = exp_nonpositive(-m);
-#pragma unroll 1
+#pragma unroll 4
             for (int i = 0; i < 2 * kLutHalf / kRlThreads; ++i) {
                 const bool neg = i >= kLutHalf / kRlThreads;
                 const int k = tid + kRlThreads * (i % (kLutHalf / kRlThreads));
@@ -613,6 +630,9 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
 #pragma unroll 1
         for (int h = 0; h < 2; ++h) {
             if ((h == 0) == (seg == 1) && (h == 0 || rn < rows)) arrive();
+            // the row's records are complete (B3): its survivors
+            if (h == 1 && wave == kFinisher) fin = finish_extract(par, tk, full, do_lse, b, mask_eos);
+            if (h == 1 && seg == 0 && !tickets && rn < rows) r_ahead = next_read_row(rn + gridDim.x, b_ahead, len_ahead);
             if (h == 0 && records) {
                 const int tk_thread = max(static_cast<int>(static_cast<int16_t>(t_smax & 0xffffu)),
                                           static_cast<int>(static_cast<int16_t>(t_smax >> 16)));
@@ -627,7 +647,19 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
             lds_barrier();  // h = 0: B3, h = 1: B4
             if (h == 0 && seg == 0) s_hist2[tid] = 0;  // every wavefront has its b2
         }
-        if (wave == kFinisher) finish_row(par, r, m, theta, tk, full, any_bad, do_lse, b, mask_eos);
+        // ---- the row's end (phase 0 of the next row): its lane tree,
+        // logsumexp, ranked shortlist and RowInfo ----
+        if (wave == kFinisher) {
+            float lse = -kInf;
+            if (do_lse) {
+                float a[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) a[e] = s_acc[par][4 * l + e];
+                lse = logsumexp_from(m, lane_tree_sum(a, l));
+            }
+            finish_publish(fin, r, lse, theta, any_bad);
+            if (l < 8) s_nrec[par][l] = 0;
+        }
 
         r = rn;
         b = bn;
@@ -649,6 +681,8 @@ bool row_relay_eligible(const DecodeParams& p) {
     return p.M <= 256;
 }
 
+bool row_relay_preferred(const DecodeParams& p) { return (p.V + 255) / 256 >= (3 * kRlStripes) / 4; }
+
 hipError_t launch_row_relay(const DecodeParams& p, int64_t rows, hipStream_t stream) {
     int device = 0;
     hipError_t e = hipGetDevice(&device);
@@ -663,8 +697,23 @@ hipError_t launch_row_relay(const DecodeParams& p, int64_t rows, hipStream_t str
     // one workgroup per CU, less the CUs left to an overlapped select pass
     const int64_t cus = g_relay_cus[device] - p.reserve_cus > 0 ? g_relay_cus[device] - p.reserve_cus : 1;
     const int64_t grid = rows < cus ? rows : cus;
-    hipLaunchKernelGGL((row_relay_kernel<true>), dim3(static_cast<unsigned>(grid)), dim3(kRlThreads), 0, stream, p,
-                       rows);
+    // the first chunk that may reach past the row on some lane: segment 0
+    // ends at stripe per (or the row), segment 1 at the row's end; wavefront
+    // 3's lane 63 starts a chunk's 16-byte groups last
+    const int S = (p.V + 255) / 256;
+    const int per = ((((S + 1) / 2) + 7) / 8) * 8;
+    int first_partial = kRlChunks;
+    for (int sg = 0; sg < 2; ++sg) {
+        const int end_r = p.V < 256 * (sg * per + per) ? p.V : 256 * (sg * per + per);
+        const int c_all = (end_r - (256 * (sg * per + 7) + 64 * 3 + 56) + 2047) >> 11;
+        first_partial = c_all < first_partial ? c_all : first_partial;
+    }
+    if (first_partial >= kRlChunks - 4)
+        hipLaunchKernelGGL((row_relay_kernel<kRlChunks - 4>), dim3(static_cast<unsigned>(grid)), dim3(kRlThreads), 0,
+                           stream, p, rows);
+    else
+        hipLaunchKernelGGL((row_relay_kernel<0>), dim3(static_cast<unsigned>(grid)), dim3(kRlThreads), 0, stream, p,
+                           rows);
     return hipGetLastError();
 }
 
