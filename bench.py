@@ -321,7 +321,13 @@ def main() -> int:
     ap.add_argument("--no-c5", action="store_true", help="skip the C5 fwd+bwd fields of the default C2 line")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain device copy of 1 GiB (the PMC byte-counter calibration)")
+    ap.add_argument("--serial", action="store_true",
+                    help="run the select pass after the row pass, not beside it (for PMC counter passes, "
+                         "which serialize kernels)")
     args = ap.parse_args()
+    if args.serial:
+        from beamgrad_amd import _abi
+        _abi.load().dbs_hip_set_decode_overlap(0)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build's hot path runs on a single MI355X "
               "(examples are independent and would shard over GPUs with no exchange). Run with --gpus 1.",

@@ -122,12 +122,16 @@ DBS_CUDA_EXPORT int dbs_hip_profile_read(int kernel, double* total_ms, int64_t* 
 /* Row-pass kernel choice for tests and measurements (no counterpart in the
  * reference; every choice gives the same results): -1 automatic (the
  * default: for log-prob rows the one-read log-prob kernel where it applies;
- * else the resident 16-bit kernel where it applies, else the pipelined
- * 16-bit kernel, else the two-pass kernel), 0 two-pass, 1 resident 16-bit
- * (V % 8 == 0, 16-byte aligned rows), 2 pipelined 16-bit (any V), 3 one-read
- * log-prob rows (any dtype, rows up to 163824 bytes).
- * A kernel that does not apply to a decode falls back to the two-pass one.
- * Returns the previous choice, or -2 for an invalid argument. */
+ * else, for bfloat16 logits rows of 116481 to 155648 entries, the relay
+ * kernel; else the resident 16-bit kernel where it applies, else the
+ * streaming 16-bit kernel, else the pipelined 16-bit kernel, else the
+ * two-pass kernel), 0 two-pass, 1 resident 16-bit (V % 8 == 0, 16-byte
+ * aligned rows), 2 pipelined 16-bit (any V), 3 one-read log-prob rows (any
+ * dtype, rows up to 163824 bytes), 4 streaming 16-bit (V % 8 == 0, 16-byte
+ * aligned rows), 5 relay for bfloat16 logits (V % 8 == 0, 16-byte aligned
+ * rows, V <= 155648). A kernel that does not apply to a decode falls back to
+ * the two-pass one. Returns the previous choice, or -2 for an invalid
+ * argument. */
 DBS_CUDA_EXPORT int dbs_hip_set_row_pass(int kind);
 
 /* Whether a multi-step decode runs its select pass alongside the row pass, on
