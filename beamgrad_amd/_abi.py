@@ -113,6 +113,7 @@ SIGNATURES = {
                                          C.c_void_p, C.c_int64, C.c_void_p]),
     "dbs_hip_backtrack": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                     C.c_void_p]),
+    "dbs_hip_widen_trace": (C.c_int, [C.c_void_p] * 6 + [C.c_int] * 3 + [C.c_void_p] * 7),
     "dbs_hip_backtrack_i64": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p,
                                         C.c_void_p]),
     "dbs_hip_profile_enable": (C.c_int, [C.c_int]),

@@ -744,6 +744,37 @@ DBS_CUDA_EXPORT int dbs_hip_backtrack(const int32_t* tokens, const int32_t* pare
                   launch_backtrack(tokens, parents, steps_per_example, batch_size, steps, beam_size, sequences, stream));
 }
 
+DBS_CUDA_EXPORT int dbs_hip_widen_trace(const int32_t* final_lengths, const int32_t* tokens, const int32_t* parents,
+                                        const int32_t* lengths, const uint8_t* from_logprob,
+                                        const int32_t* steps_per_example, int batch_size, int steps, int beam_size,
+                                        int64_t* final_lengths64, int64_t* tokens64, int64_t* parents64,
+                                        int64_t* lengths64, uint8_t* from_logprob_bool, int64_t* steps64,
+                                        void* stream_ptr) {
+    if (!final_lengths || !tokens || !parents || !lengths || !from_logprob || !final_lengths64 || !tokens64 ||
+        !parents64 || !lengths64 || !from_logprob_bool || !steps64 || batch_size <= 0 || steps <= 0 ||
+        beam_size <= 0)
+        return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    WidenTrace w{};
+    w.final_len = final_lengths;
+    w.tokens = tokens;
+    w.parents = parents;
+    w.lengths = lengths;
+    w.flp = from_logprob;
+    w.steps = steps_per_example;
+    w.final_len64 = final_lengths64;
+    w.tokens64 = tokens64;
+    w.parents64 = parents64;
+    w.lengths64 = lengths64;
+    w.flp_bool = from_logprob_bool;
+    w.steps64 = steps64;
+    w.n_final = static_cast<int64_t>(batch_size) * beam_size;
+    w.n_trace = w.n_final * steps;
+    w.n_steps = batch_size;
+    w.T = steps;
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    return finish(stream, launch_widen_trace(w, stream));
+}
+
 DBS_CUDA_EXPORT int dbs_hip_backtrack_i64(const int64_t* tokens, const int64_t* parents,
                                           const int64_t* steps_per_example, int batch_size, int steps, int beam_size,
                                           int64_t* sequences, void* stream_ptr) {

@@ -31,6 +31,22 @@ __global__ void fill_f32_kernel(float* dst, float value, int64_t n) {
     for (int64_t j = i; j < n; j += stride) dst[j] = value;
 }
 
+// The decode trace in the dtypes torch returns it in: the int32 indices as
+// int64, the from-log-prob flags as bool, and the per-example steps (T where
+// none were given), in one launch.
+__global__ __launch_bounds__(256) void widen_trace_kernel(WidenTrace w) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    for (int64_t i = first; i < w.n_trace; i += stride) {
+        w.tokens64[i] = w.tokens[i];
+        w.parents64[i] = w.parents[i];
+        w.lengths64[i] = w.lengths[i];
+        w.flp_bool[i] = w.flp[i] != 0 ? 1 : 0;
+    }
+    for (int64_t i = first; i < w.n_final; i += stride) w.final_len64[i] = w.final_len[i];
+    for (int64_t i = first; i < w.n_steps; i += stride) w.steps64[i] = w.steps ? w.steps[i] : w.T;
+}
+
 // Zeroes n16 16-byte words.
 __global__ void clear_kernel(uint4* dst, int64_t n16) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -244,6 +260,16 @@ hipError_t launch_clear(void* dst, size_t bytes, hipStream_t stream) {
     const int64_t blocks = (n16 + 255) / 256;
     hipLaunchKernelGGL(clear_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)), dim3(256), 0, stream,
                        static_cast<uint4*>(dst), n16);
+    return hipGetLastError();
+}
+
+hipError_t launch_widen_trace(const WidenTrace& w, hipStream_t stream) {
+    const int64_t n = w.n_trace > w.n_final ? (w.n_trace > w.n_steps ? w.n_trace : w.n_steps)
+                                            : (w.n_final > w.n_steps ? w.n_final : w.n_steps);
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(widen_trace_kernel, dim3(static_cast<unsigned>(blocks < 2048 ? blocks : 2048)), dim3(256), 0,
+                       stream, w);
     return hipGetLastError();
 }
 

@@ -193,6 +193,18 @@ hipError_t wait_timeout_counter(int reset, unsigned long long* value);
 
 // Elementwise helpers.
 hipError_t launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream);
+
+// A decode trace's int32 / uint8 outputs widened for torch (int64, bool), and
+// the per-example steps (T where steps is null).
+struct WidenTrace {
+    const int32_t *final_len, *tokens, *parents, *lengths, *steps;
+    const uint8_t* flp;
+    int64_t *final_len64, *tokens64, *parents64, *lengths64, *steps64;
+    uint8_t* flp_bool;
+    int64_t n_final, n_trace, n_steps;
+    int T;
+};
+hipError_t launch_widen_trace(const WidenTrace& w, hipStream_t stream);
 hipError_t launch_clear(void* dst, size_t bytes, hipStream_t stream);
 hipError_t launch_length_penalty(const int32_t* lengths, int64_t n, float alpha, float* out, hipStream_t stream);
 hipError_t launch_check_steps(const int32_t* steps, int B, int T, int32_t* status, hipStream_t stream);

@@ -249,8 +249,9 @@ def measure(name: str, steps: int, warmup: int, copy_probe: bool = False) -> dic
         torch.cuda.synchronize()
         del src, dst
 
+    # the timed steps run uninstrumented; a second loop of as many steps
+    # records each kernel's launches with HIP events (kernels_ms, roofline)
     lib = _abi.load()
-    lib.dbs_hip_profile_enable(1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start = torch.cuda.Event(enable_timing=True)
@@ -261,6 +262,10 @@ def measure(name: str, steps: int, warmup: int, copy_probe: bool = False) -> dic
     stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    lib.dbs_hip_profile_enable(1)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
     kernels, rescans = _read_kernels(lib, steps)
     lib.dbs_hip_profile_enable(0)
 

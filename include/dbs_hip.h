@@ -106,6 +106,30 @@ DBS_CUDA_EXPORT int dbs_hip_backtrack_i64(
     int64_t* sequences,
     void* stream);
 
+/* A decode trace's outputs in the dtypes torch returns them in, in one
+ * launch: final_lengths [B, K], tokens, parents and lengths [B, T, K] as
+ * int64, from_logprob [B, T, K] as 0/1 bytes (torch bool), and the
+ * per-example steps [B] as int64 (steps where steps_per_example is null).
+ * No counterpart in the reference (its Python wrapper converts each output
+ * with its own torch operation); for the torch operator beamgrad::decode_trace. */
+DBS_CUDA_EXPORT int dbs_hip_widen_trace(
+    const int32_t* final_lengths,
+    const int32_t* tokens,
+    const int32_t* parents,
+    const int32_t* lengths,
+    const uint8_t* from_logprob,
+    const int32_t* steps_per_example,
+    int batch_size,
+    int steps,
+    int beam_size,
+    int64_t* final_lengths64,
+    int64_t* tokens64,
+    int64_t* parents64,
+    int64_t* lengths64,
+    uint8_t* from_logprob_bool,
+    int64_t* steps64,
+    void* stream);
+
 /* Launch timing for measurement tools (no counterpart in the reference).
  * With profiling on, every kernel the library launches is bracketed by HIP
  * events on the caller's stream, and its duration is summed per kernel kind:
