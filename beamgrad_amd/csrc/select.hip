@@ -301,11 +301,48 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
     __syncthreads();
 }
 
+// compact_by_rank for n <= 64 candidates, by the first wavefront alone (one
+// barrier, after it): lane i ranks candidate i against every key, eight
+// broadcast reads in flight; a wavefront's LDS operations complete in order,
+// so its key stores precede its reads and its reads of the collector precede
+// its moves.
+__device__ __forceinline__ void compact_small(Lds& s, State& st, int K, int n) {
+    const int tid = static_cast<int>(threadIdx.x);
+    if (tid < 64) {
+        const int n8 = (n + 7) & ~7;
+        const Cand c = tid < n ? s.buf[tid] : dead_cand();
+        if (tid < n) store_key(s.key + 2 * tid, c, tid);
+        else if (tid < n8) {
+            s.key[2 * tid] = make_uint4(0u, 0u, 0u, 0u);  // below every key
+            s.key[2 * tid + 1] = make_uint4(0u, 0u, 0u, 0u);
+        }
+        const uint4 ilo = s.key[2 * tid], ihi = s.key[2 * tid + 1];
+        int rank = 0;
+        for (int j = 0; j < n8; j += 8) {
+            uint4 w[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) w[u] = s.key[2 * j + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) count_before(rank, ilo, ihi, w[2 * u], w[2 * u + 1]);
+        }
+        if (tid < n) {
+            if (rank < K) s.buf[rank] = c;
+            if (rank == K - 1 && before(c, st.thr)) st.thr = c;
+        }
+        if (tid == 0) st.count = n < K ? n : K;
+    }
+    __syncthreads();
+}
+
 // Sorts the collected candidates, keeps the best K, and raises the admission
 // threshold to the K-th kept one when that is better.
 __device__ __forceinline__ void compact(Lds& s, State& st, int K) {
     __syncthreads();
     const int n = __builtin_amdgcn_readfirstlane(st.count);
+    if (n <= 64) {
+        compact_small(s, st, K, n);
+        return;
+    }
     if (n <= kRankMax) {
         compact_by_rank(s, st, K, n);
         return;
@@ -865,17 +902,19 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         }
         __syncthreads();
         if (p.constrained && !p.step_mode) {
-            // each selected beam: its parent's prefix, then its token
+            // each selected beam: its parent's prefix, then its token (one
+            // pass over every beam's positions)
             const int nxt = cur ^ 1;
             const int P = p.prefix_cap;
-            for (int k = 0; k < K; ++k) {
-                const Cand c = k < nsel ? s.buf[k] : dead_cand();
+            for (int item = tid; item < K * P; item += kSelectThreads) {
+                const int k = item / P, i = item - k * P;
+                if (k >= nsel) continue;
+                const Cand c = s.buf[k];
                 if (c.parent < 0) continue;
                 const int Lp = s.plen[cur * K + c.parent];
-                const int32_t* src = s.prefix + (static_cast<int64_t>(cur) * K + c.parent) * P;
                 int32_t* dst = s.prefix + (static_cast<int64_t>(nxt) * K + k) * P;
-                for (int i = tid; i < Lp; i += kSelectThreads) dst[i] = src[i];
-                if (tid == 0 && c.flp && c.token >= 0) dst[Lp] = c.token;
+                if (i < Lp) dst[i] = s.prefix[(static_cast<int64_t>(cur) * K + c.parent) * P + i];
+                else if (i == Lp && c.flp && c.token >= 0) dst[Lp] = c.token;
             }
             cur = nxt;
         }
