@@ -136,14 +136,14 @@ __device__ __forceinline__ bool table_fits_fixed(float m) {
     return mp < kFixedBase - 1 + (kLutHalf - 1);
 }
 
-// Byte offsets into the fixed-base table of a register's two bfloat16
-// patterns (low half, high half): slot = min(max(magnitude - (base - 1), 0),
-// 4095), plus 4096 for a negative pattern, times 4.
-__device__ __forceinline__ uint32_t term_offsets(uint32_t R) {
+// Slots in the fixed-base table of a register's two bfloat16 patterns (low
+// half, high half): slot = min(max(magnitude - (base - 1), 0), 4095), plus
+// 4096 for a negative pattern. Five packed 16-bit operations; a lookup takes
+// the byte offset with one shift of its half (slot * 4).
+__device__ __forceinline__ uint32_t term_slots(uint32_t R) {
     uint32_t idx = pk_sub_sat_u16(R & 0x7fff7fffu, (kFixedBase - 1u) * 0x10001u);
     idx = pk_min_u16(idx, 0x0fff0fffu);
-    idx |= (R >> 3) & 0x10001000u;
-    return pk_shl2_u16(idx);
+    return idx | ((R >> 3) & 0x10001000u);
 }
 
 // Inverse of key16.

@@ -20,10 +20,10 @@
 //            M-th largest thread maximum) and the row's term table (fixed
 //            base, table_fits_fixed);
 //   phase A  segment 0 records its chunks that may hold survivors (x >=
-//            theta), folds its stripes (the registers hold table offsets:
+//            theta), folds its stripes (the registers hold table slots:
 //            extract, look up, add) and streams its part of the next row
 //            into the registers it has passed; segment 1 turns its registers
-//            into table offsets and records its survivor chunks;
+//            into table slots and records its survivor chunks;
 //   phase B  segment 1 continues the lane chains over its stripes and
 //            streams its part of the next row;
 //            segment 0 transposes, keys and converts its part of the next
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
     __shared__ uint64_t s_key[kSurvivorCap + 2];
     __shared__ float s_x[kSurvivorCap];
     // survivor records by row parity: a lane's chunk (eight patterns as
-    // table offsets) where its key reaches theta, kRecCap per wavefront
+    // table slots) where its key reaches theta, kRecCap per wavefront
     __shared__ __attribute__((aligned(16))) uint4 s_rec[2][8 * kRecCap];
     __shared__ int s_rtok[2][8 * kRecCap];
     __shared__ __attribute__((aligned(16))) int s_nrec[2][8];
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
     // bytes past the row, V % 8 == 0, go in as -inf), the thread's packed
     // signed and unsigned pattern maxima, per chunk the largest signed
     // pattern (the chunk's maximum where it is >= +0) in s_ck, and the
-    // registers turned into table offsets (term_offsets) ----
+    // registers turned into table slots (term_slots) ----
     uint32_t t_smax = 0x80008000u, t_umax = 0u;
     // the lane's loaded 16 bytes of chunk c are past the row from c = c_lim
     // on (element 256 (s_begin + 8 c + l / 8) + 64 wv + 8 (l % 8) >= end)
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
             asm volatile("" : "+v"(smax), "+v"(umax));  // the maxima taken here: the patterns die here
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                reg[4 * c + q] = term_offsets(R4[q]);
+                reg[4 * c + q] = term_slots(R4[q]);
                 asm volatile("" : "+v"(reg[4 * c + q]));
             }
         });
@@ -264,14 +264,21 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         t_umax = umax;
     };
 
-    // ---- the segment's part of a lane chain from the table offsets; the
+    // ---- the segment's part of a lane chain from the table slots; the
     // registers take the next row's chunks as the chain passes them ----
     auto chain_table = [&](float acc, int64_t rn) __attribute__((always_inline)) -> float {
         const unsigned char* lut_bytes = reinterpret_cast<const unsigned char*>(lut);
+        // the two slots' byte offsets, each with one shift of its 16-bit half
+        // (SDWA word select; the compiler picks it for the upper half only)
+        const uint32_t two = 2u;
         auto lookup = [&](int k, float& lo, float& hi) __attribute__((always_inline)) {
             const uint32_t A = reg[k];
-            lo = *reinterpret_cast<const float*>(lut_bytes + (A & 0xffffu));
-            hi = *reinterpret_cast<const float*>(lut_bytes + (A >> 16));
+            uint32_t lo_off;
+            asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
+                : "=v"(lo_off)
+                : "v"(two), "v"(A));
+            lo = *reinterpret_cast<const float*>(lut_bytes + lo_off);
+            hi = *reinterpret_cast<const float*>(lut_bytes + ((A >> 16) << 2));
         };
         const __amdgpu_buffer_rsrc_t rs_next = row_view(rn);
         const int voff_next = lane_offset();
@@ -405,7 +412,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
 #pragma unroll
         for (int w = 0; w < 8; ++w) overflow = overflow || nrec[w] > kRecCap;
         if (M > 0 && live && !overflow) {
-            const uint32_t thr = 4u * static_cast<uint32_t>(tk - static_cast<int>(kFixedBase - 1u));
+            const uint32_t thr = static_cast<uint32_t>(tk - static_cast<int>(kFixedBase - 1u));
             // the eight wavefronts' lists read as one (list w from prefix[w]),
             // 64 records a pass, one per lane
             int prefix[9];
@@ -433,7 +440,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const uint32_t a = (R[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-                    hits |= (has && a >= thr && a < 4u * kLutHalf) ? (1u << e) : 0u;
+                    hits |= (has && a >= thr && a < static_cast<uint32_t>(kLutHalf)) ? (1u << e) : 0u;
                 }
                 if (check) {
 #pragma unroll 1
@@ -460,7 +467,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
                     const uint32_t w2 = e < 4 ? (e < 2 ? R[0] : R[1]) : (e < 6 ? R[2] : R[3]);
                     const uint32_t a = (w2 >> (16 * (e & 1))) & 0xffffu;
                     if (slot < kSurvivorCap) {
-                        const float x = bf16_to_f32(static_cast<uint16_t>((a >> 2) + (kFixedBase - 1u)));
+                        const float x = bf16_to_f32(static_cast<uint16_t>(a + (kFixedBase - 1u)));
                         s_key[slot] = survivor_key(x, t0 + 256 * e);
                         s_x[slot] = x;
                     }
@@ -604,7 +611,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         // theta: the M-th largest thread maximum (M values reach it), raised
         // to 2^-25 where that is smaller (fewer than M values are above it;
         // then every value from 2^-25 up is a survivor and every value left
-        // out is below theta): theta is a pattern the table offsets keep
+        // out is below theta): theta is a pattern the table slots keep
         int tk = static_cast<int>(kFixedBase);
         if (select) {
             int b2 = 0, above2 = 0;
@@ -612,7 +619,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
             tk = max((b1 << 7) | b2, static_cast<int>(kFixedBase));
         }
         const float theta = M > 0 ? (select ? pattern_value<2>(static_cast<uint32_t>(tk)) : -kInf) : kInf;
-        // the shortlist comes from records of table offsets: rows on the
+        // the shortlist comes from records of table slots: rows on the
         // table path; others keep none (the select pass reads the row)
         const bool records = select && fast;
         const bool full = M > 0 && !records;

@@ -301,48 +301,11 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
     __syncthreads();
 }
 
-// compact_by_rank for n <= 64 candidates, by the first wavefront alone (one
-// barrier, after it): lane i ranks candidate i against every key, eight
-// broadcast reads in flight; a wavefront's LDS operations complete in order,
-// so its key stores precede its reads and its reads of the collector precede
-// its moves.
-__device__ __forceinline__ void compact_small(Lds& s, State& st, int K, int n) {
-    const int tid = static_cast<int>(threadIdx.x);
-    if (tid < 64) {
-        const int n8 = (n + 7) & ~7;
-        const Cand c = tid < n ? s.buf[tid] : dead_cand();
-        if (tid < n) store_key(s.key + 2 * tid, c, tid);
-        else if (tid < n8) {
-            s.key[2 * tid] = make_uint4(0u, 0u, 0u, 0u);  // below every key
-            s.key[2 * tid + 1] = make_uint4(0u, 0u, 0u, 0u);
-        }
-        const uint4 ilo = s.key[2 * tid], ihi = s.key[2 * tid + 1];
-        int rank = 0;
-        for (int j = 0; j < n8; j += 8) {
-            uint4 w[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) w[u] = s.key[2 * j + u];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) count_before(rank, ilo, ihi, w[2 * u], w[2 * u + 1]);
-        }
-        if (tid < n) {
-            if (rank < K) s.buf[rank] = c;
-            if (rank == K - 1 && before(c, st.thr)) st.thr = c;
-        }
-        if (tid == 0) st.count = n < K ? n : K;
-    }
-    __syncthreads();
-}
-
 // Sorts the collected candidates, keeps the best K, and raises the admission
 // threshold to the K-th kept one when that is better.
 __device__ __forceinline__ void compact(Lds& s, State& st, int K) {
     __syncthreads();
     const int n = __builtin_amdgcn_readfirstlane(st.count);
-    if (n <= 64) {
-        compact_small(s, st, K, n);
-        return;
-    }
     if (n <= kRankMax) {
         compact_by_rank(s, st, K, n);
         return;
