@@ -151,6 +151,31 @@ __device__ __forceinline__ uint32_t key_pattern(int key) {
     return static_cast<uint16_t>(key < 0 ? (key ^ 0x7fff) : key);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wavefront by DPP moves (row
+// shifts, then the row broadcasts of lanes 15 and 31): six dependent adds,
+// no LDS.
+__device__ __forceinline__ int wave_inclusive_sum(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
+    return x;
+}
+
+// The maximum over a wavefront's 64 lanes (every lane gets it).
+__device__ __forceinline__ int wave_max_int(int x) {
+    const int lo = static_cast<int>(0x80000000u);
+    x = max(x, __builtin_amdgcn_update_dpp(lo, x, 0x111, 0xf, 0xf, false));
+    x = max(x, __builtin_amdgcn_update_dpp(lo, x, 0x112, 0xf, 0xf, false));
+    x = max(x, __builtin_amdgcn_update_dpp(lo, x, 0x114, 0xf, 0xf, false));
+    x = max(x, __builtin_amdgcn_update_dpp(lo, x, 0x118, 0xf, 0xf, false));
+    x = max(x, __builtin_amdgcn_update_dpp(lo, x, 0x142, 0xa, 0xf, false));
+    x = max(x, __builtin_amdgcn_update_dpp(lo, x, 0x143, 0xc, 0xf, false));
+    return __builtin_amdgcn_readlane(x, 63);
+}
+
 // Over 256 bins taken in descending order, the bin holding the target-th
 // largest count-weighted key (1-based; the bins hold at least target keys),
 // and how many keys lie in the bins above it. One wavefront, every lane gets
@@ -159,11 +184,7 @@ __device__ __forceinline__ void hist_select(const int* hist, int target, int lan
     const int4 h = *reinterpret_cast<const int4*>(hist + 252 - 4 * lane);  // bins 252-4l .. 255-4l
     const int c0 = h.w, c1 = h.z, c2 = h.y, c3 = h.x;                     // descending
     const int sum = c0 + c1 + c2 + c3;
-    int incl = sum;
-    for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(incl, off);
-        if (lane >= off) incl += t;
-    }
+    const int incl = wave_inclusive_sum(sum);
     const int excl = incl - sum;
     const uint64_t mine = __ballot(excl < target && target <= incl);
     const int src = __ffsll(static_cast<long long>(mine)) - 1;

@@ -564,8 +564,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         const bool tbad = tkey >= 0x7f80 || tumax > static_cast<int>(kBf16NegInf);
         const int key15 = max(tkey, 0);  // threads whose values are all negative count as +0
         if (M > 0) atomicAdd(&s_hist1[key15 >> 7], 1);
-        int wkey = tkey;
-        for (int off = 32; off > 0; off >>= 1) wkey = max(wkey, __shfl_xor(wkey, off));
+        const int wkey = wave_max_int(tkey);
         const bool wbad = __any(tbad);
         if (l == 0) {
             s_wkey[wave] = wkey;
