@@ -392,18 +392,29 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
     // ---- a row's shortlist from its records, in two parts (one
     // wavefront). finish_extract, once the records are complete: the
     // survivors (positive, slot reaching tk's, so x >= theta; not statically
-    // masked) into s_key and s_x. finish_publish, once the row's logsumexp is
-    // known: each survivor ranked by the count of survivor keys above its own
-    // (keys are distinct), the entries of rank < M, the bound at rank M (else
-    // theta), the RowInfo. More records or survivors than kept: no
+    // masked) into s_key and s_x, and up to 64 of them ranked in the lanes
+    // (the count of survivor keys above each one's; keys are distinct).
+    // finish_publish, once the row's logsumexp is known: the entries of
+    // rank < M (ranked here when there were more than 64), the bound at rank
+    // M (else theta), the RowInfo. More records or survivors than kept: no
     // shortlist. ----
     struct Extracted {
         int n;          // survivors, keys in s_key and values in s_x
         bool overflow;  // no shortlist
+        bool in_lanes;  // n <= 64: ranked already, survivor i in lane i
+        int rank;
+        float x;
+        uint64_t key;
+        float bound_x;  // x at rank M (n > M)
     };
     auto finish_extract = [&](int pb, int tk, bool full, bool live, int bb, bool mask) __attribute__((always_inline)) {
         Extracted st;
         st.n = 0;
+        st.in_lanes = false;
+        st.rank = 0;
+        st.x = 0.0f;
+        st.key = ~0ull;
+        st.bound_x = -kInf;
         // the eight wavefronts' record counts, read once
         const int4 n_lo = *reinterpret_cast<const int4*>(&s_nrec[pb][0]);
         const int4 n_hi = *reinterpret_cast<const int4*>(&s_nrec[pb][4]);
@@ -475,8 +486,31 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
                 n += pass_total;
             }
             st.n = n;
-            if (n > kSurvivorCap) overflow = true;
-            else if ((n & 1) && l == 0) s_key[n] = 0;  // a zero key pads the pairs read when ranking
+            if (n > kSurvivorCap) {
+                overflow = true;
+            } else {
+                if ((n & 1) && l == 0) s_key[n] = 0;  // a zero key pads the pairs read when ranking
+                wave_sync();
+                if (n <= 64) {
+                    // each survivor's rank: the count of keys above its own
+                    st.in_lanes = true;
+                    const uint4* k2 = reinterpret_cast<const uint4*>(s_key);
+                    const int npair = (n + 1) >> 1;
+                    const uint64_t ki = l < n ? s_key[l] : ~0ull;
+                    int rank = 0;
+#pragma unroll 8
+                    for (int jp = 0; jp < npair; ++jp) {
+                        const uint4 a = k2[jp];
+                        rank += static_cast<int>(((static_cast<uint64_t>(a.y) << 32) | a.x) > ki) +
+                                static_cast<int>(((static_cast<uint64_t>(a.w) << 32) | a.z) > ki);
+                    }
+                    st.rank = rank;
+                    st.key = ki;
+                    st.x = l < n ? s_x[l] : 0.0f;
+                    const uint64_t at_m = __ballot(l < n && rank == M);
+                    if (at_m != 0) st.bound_x = __shfl(st.x, __ffsll(static_cast<long long>(at_m)) - 1);
+                }
+            }
         }
         st.overflow = overflow;
         return st;
@@ -491,11 +525,15 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         const int n = st.n;
         if (M > 0 && lse != -kInf && !st.overflow) {
             ShortEntry* out = p.shortlist + rr * M;
-            float bound_x = -kInf;
+            float bound_x = st.bound_x;
             const uint4* k2 = reinterpret_cast<const uint4*>(s_key);
             const int npair = (n + 1) >> 1;
+            if (st.in_lanes && l < n && st.rank < M) {
+                const int32_t tok = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(st.key & 0xffffffffu));
+                publish_entry(out, st.rank, st.x - lse, tok, coherent);
+            }
 #pragma unroll 1
-            for (int i0 = 0; i0 < n; i0 += 64) {
+            for (int i0 = 0; !st.in_lanes && i0 < n; i0 += 64) {
                 const int i = i0 + l;
                 const uint64_t ki = i < n ? s_key[i] : ~0ull;
                 int rank = 0;
