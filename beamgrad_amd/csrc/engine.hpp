@@ -134,9 +134,10 @@ struct DecodeParams {
 struct SelectLayout {
     int sort_cap;        // collector capacity (a power of two)
     int pen_len;         // length-penalty table entries (T + 2; 0 in step mode)
-    size_t off_buf, off_rbuf, off_key, off_f32, off_i32, off_sl, off_prefix, off_blk;
+    size_t off_buf, off_rbuf, off_key, off_f32, off_i32, off_sl, off_prefix, off_blk, off_sig;
     int prefix_in_lds;   // the prefixes live in LDS (else in the workspace)
     int blk_in_lds;      // the n-gram-blocked lists live in LDS (else in the workspace)
+    int sig_in_lds;      // the prefixes' token signatures are kept (LDS; needs the prefixes in LDS)
     size_t smem;
 };
 

@@ -42,10 +42,17 @@ constexpr int kLpThreads = 256;
 constexpr int kLpMaxBlocks = 40;  // 16-byte blocks per thread, at most
 constexpr int kLpBlockCap = 512;  // blocks holding survivors, at most (else the row is read in full)
 
+// Element i of a block as f32. binary16 goes through the hardware conversion,
+// exact for every finite value and the infinities (denormals are kept); a NaN
+// never reaches a shortlist (the row is flagged and read in full instead), so
+// its payload does not matter here.
 template <int DT>
 __device__ __forceinline__ float element_of(const v4u32& d, int i) {
     if constexpr (DT == 0) {
         return bits_f32(d[i]);
+    } else if constexpr (DT == 1) {
+        const uint16_t h = static_cast<uint16_t>((d[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+        return static_cast<float>(__builtin_bit_cast(_Float16, h));
     } else {
         return pattern_value<DT>((d[i >> 1] >> (16 * (i & 1))) & 0xffffu);
     }

@@ -67,12 +67,16 @@ constexpr int kRescanPerThread = 16;
 constexpr int kTauHead = 2;       // entries per row behind the second tau bound
 constexpr int kWideBeam = 16;     // beams from which the wide-beam paths pay off
 constexpr int kPfRegs = 12;       // 16-byte prefetch registers per thread (K * M <= 6144)
+constexpr int kSigWords = 64;     // 2048-bit token signature of a beam's prefix
+constexpr int kScoreFilterMaxK = 32;  // beams up to which a rank compaction first ranks by score alone
 
 struct Lds {
     Cand* buf;        // [sort_cap] the collector
     Cand* rbuf;       // [kRescanBuf] one rescanned row's candidates
     uint4* key;       // [2 * kRankMax] candidate keys of a rank compaction
-    int32_t* part;    // [kSelectThreads] partial ranks
+    int32_t* part;    // [kSelectThreads] partial ranks (or score keys)
+    int32_t* surv;    // [64] candidates left by the score pass of a rank compaction
+    int32_t* nsurv;   // [1] how many
     float* raw;       // [K] beams after the previous step
     float* nraw;      // [K] beams after this step (also scratch)
     float* rbound;    // [K]
@@ -90,6 +94,7 @@ struct Lds {
     ShortEntry* sl;   // [K, M + 1] the step's shortlists (see sl_at)
     int32_t* prefix;  // [2, K, P] (LDS) or the example's slice of the workspace
     int32_t* blk;     // [K, P] (LDS) or workspace
+    uint32_t* sig;    // [2, K, kSigWords] (LDS) prefix signatures, or null
 };
 
 struct State {
@@ -123,15 +128,20 @@ __device__ __forceinline__ float inv_of(const Lds& s, int pen_len, int l, float 
 struct PrefixView {
     const int32_t* tok;
     int len;
+    const uint32_t* sig;  // a bit set for every token of tok[0, len) (a superset filter), or null
 };
+
+// Signature bit of token v: a multiplicative hash to 11 bits.
+__device__ __forceinline__ uint32_t sig_bit(int v) { return (static_cast<uint32_t>(v) * 0x9E3779B1u) >> 21; }
 
 __device__ __forceinline__ PrefixView prefix_of(const DecodeParams& p, const Lds& s, int b, int k, int cur) {
     if (p.step_mode) {
         const int l = s.len[k];
         const int L = l < 0 ? 0 : (l < p.st_stride ? l : p.st_stride);
-        return PrefixView{p.st_prefix + (static_cast<int64_t>(b) * p.K + k) * p.st_stride, L};
+        return PrefixView{p.st_prefix + (static_cast<int64_t>(b) * p.K + k) * p.st_stride, L, nullptr};
     }
-    return PrefixView{s.prefix + (static_cast<int64_t>(cur) * p.K + k) * p.prefix_cap, s.plen[cur * p.K + k]};
+    return PrefixView{s.prefix + (static_cast<int64_t>(cur) * p.K + k) * p.prefix_cap, s.plen[cur * p.K + k],
+                      s.sig ? s.sig + (cur * p.K + k) * kSigWords : nullptr};
 }
 
 // Membership of v in a[0, n): eight independent loads in flight per round
@@ -153,6 +163,16 @@ __device__ __forceinline__ bool in_list(const int32_t* a, int n, int v) {
     return hit;
 }
 
+// Membership of v in a prefix: the signature rules most tokens out with one
+// read; the rest are searched.
+__device__ __forceinline__ bool in_prefix(const PrefixView& pre, int v) {
+    if (pre.sig) {
+        const uint32_t h = sig_bit(v);
+        if (((pre.sig[h >> 5] >> (h & 31u)) & 1u) == 0u) return false;
+    }
+    return in_list(pre.tok, pre.len, v);
+}
+
 // The candidate of token v (finite log-prob lp, statically allowed) in the
 // row of beam k; false when n-gram blocking removes it. A token of the prefix
 // pays the repetition penalty: raw = p + (lp - log(rep)) (reference
@@ -162,11 +182,11 @@ __device__ __forceinline__ bool make_cand(const DecodeParams& p, const Lds& s, c
     float value = lp;
     if (p.constrained) {
         if (p.ngram == 1) {
-            if (in_list(pre.tok, pre.len, v)) return false;
+            if (in_prefix(pre, v)) return false;
         } else if (p.ngram > 1 && in_list(s.blk + static_cast<int64_t>(k) * p.prefix_cap, s.nblk[k], v)) {
             return false;
         }
-        if (p.penalise && in_list(pre.tok, pre.len, v)) value = lp - p.log_rep;
+        if (p.penalise && in_prefix(pre, v)) value = lp - p.log_rep;
     }
     const float raw = praw + value;
     c = Cand{raw * inv_pen, raw, k, v, new_len, 1};
@@ -243,9 +263,16 @@ __device__ __forceinline__ void count_above64(int& rank, uint32_t ilo, uint32_t 
 // candidate's rank is the number of keys above its own, counted by up to four
 // waves per candidate over disjoint ranges of the others, and the candidates
 // of rank < K move to their rank.
+// Past one wavefront of candidates (few beams), a pass over the scores alone
+// (the keys' most significant word) comes first: a candidate with K or more
+// scores strictly above its own ranks K or later. Every candidate ranked
+// before a remaining one has a score at least as high and so remains too:
+// the remaining candidates' ranks among themselves are their ranks among all,
+// and when at most 64 remain one wavefront ranks them.
 __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n) {
     const int tid = static_cast<int>(threadIdx.x);
     const int n4 = (n + 3) & ~3;
+    const bool by_score = n > 64 && K <= kScoreFilterMaxK;
     Cand c = dead_cand();
     if (tid < n4) {
         if (tid < n) {
@@ -255,8 +282,54 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
             s.key[2 * tid] = make_uint4(0u, 0u, 0u, 0u);  // below every key
             s.key[2 * tid + 1] = make_uint4(0u, 0u, 0u, 0u);
         }
+        if (by_score) s.part[tid] = static_cast<int32_t>(tid < n ? ordered_key(c.score) : 0u);
     }
+    if (by_score && tid == 0) s.nsurv[0] = 0;
     __syncthreads();
+    if (by_score) {
+        if (tid < n) {
+            const uint32_t mine = ordered_key(c.score);
+            const uint4* sk = reinterpret_cast<const uint4*>(s.part);
+            int above = 0;
+            int j = 0;
+            for (; j + 4 <= n4 / 4; j += 4) {  // four reads in flight
+                uint4 w[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) w[u] = sk[j + u];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    above += (w[u].x > mine) + (w[u].y > mine) + (w[u].z > mine) + (w[u].w > mine);
+            }
+            for (; j < n4 / 4; ++j) {
+                const uint4 w = sk[j];
+                above += (w.x > mine) + (w.y > mine) + (w.z > mine) + (w.w > mine);
+            }
+            if (above < K) {
+                const int slot = atomicAdd(s.nsurv, 1);
+                if (slot < 64) s.surv[slot] = tid;
+            }
+        }
+        __syncthreads();
+        const int ns = __builtin_amdgcn_readfirstlane(s.nsurv[0]);
+        if (ns <= 64) {
+            if (tid < ns) {
+                const int i = s.surv[tid];
+                const Cand ci = s.buf[i];
+                const uint4 ilo = s.key[2 * i], ihi = s.key[2 * i + 1];
+                int rank = 0;
+                for (int j = 0; j < ns; ++j) {
+                    const int jj = s.surv[j];
+                    count_before(rank, ilo, ihi, s.key[2 * jj], s.key[2 * jj + 1]);
+                }
+                if (rank < K) s.buf[rank] = ci;
+                if (rank == K - 1 && before(ci, st.thr)) st.thr = ci;
+            }
+            if (tid == 0) st.count = n < K ? n : K;
+            __syncthreads();
+            return;
+        }
+        // many equal scores: every candidate is ranked
+    }
     // wave w counts for candidates 64 gi + lane over the gj-th part of the others
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int groups = (n + 63) >> 6;
@@ -419,6 +492,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     s.rbuf = reinterpret_cast<Cand*>(smem + L.off_rbuf);
     s.key = reinterpret_cast<uint4*>(smem + L.off_key);
     s.part = reinterpret_cast<int32_t*>(smem + L.off_key + sizeof(uint4) * 2 * kRankMax);
+    s.surv = s.part + kSelectThreads;
+    s.nsurv = s.surv + 64;
     float* f = reinterpret_cast<float*>(smem + L.off_f32);
     s.raw = f;
     s.nraw = f + K;
@@ -440,6 +515,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                                : p.prefix + static_cast<int64_t>(b) * 2 * K * p.prefix_cap;
     s.blk = L.blk_in_lds ? reinterpret_cast<int32_t*>(smem + L.off_blk)
                          : p.blocked + static_cast<int64_t>(b) * K * p.prefix_cap;
+    s.sig = L.sig_in_lds && !p.step_mode ? reinterpret_cast<uint32_t*>(smem + L.off_sig) : nullptr;
 
     const int steps_b = p.step_mode ? 1 : example_steps(p, b);
     // this example's beams (slots past them stay empty) and EOS token
@@ -469,6 +545,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         s.plen[k] = 0;
         s.plen[K + k] = 0;
     }
+    if (s.sig)
+        for (int i = tid; i < 2 * K * kSigWords; i += kSelectThreads) s.sig[i] = 0u;
     if (tid == 0) {
         st.invalid = 0;
         st.gave_up = 0;
@@ -865,15 +943,25 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         }
         __syncthreads();
         if (p.constrained && !p.step_mode) {
-            // each selected beam: its parent's prefix, then its token (one
-            // pass over every beam's positions)
+            // each selected beam: its parent's prefix, then its token, and
+            // the signature of both (one pass over every beam's positions)
             const int nxt = cur ^ 1;
             const int P = p.prefix_cap;
-            for (int item = tid; item < K * P; item += kSelectThreads) {
-                const int k = item / P, i = item - k * P;
-                if (k >= nsel) continue;
-                const Cand c = s.buf[k];
-                if (c.parent < 0) continue;
+            const int W = s.sig ? kSigWords : 0;
+            const int PW = P > W ? P : W;
+            for (int item = tid; item < K * PW; item += kSelectThreads) {
+                const int k = item / PW, i = item - k * PW;
+                const Cand c = k < nsel ? s.buf[k] : dead_cand();
+                if (i < W) {
+                    uint32_t w = 0u;
+                    if (c.parent >= 0) {
+                        w = s.sig[(cur * K + c.parent) * kSigWords + i];
+                        const uint32_t h = sig_bit(c.token);
+                        if (c.flp && c.token >= 0 && static_cast<int>(h >> 5) == i) w |= 1u << (h & 31u);
+                    }
+                    s.sig[(nxt * K + k) * kSigWords + i] = w;
+                }
+                if (i >= P || c.parent < 0) continue;
                 const int Lp = s.plen[cur * K + c.parent];
                 int32_t* dst = s.prefix + (static_cast<int64_t>(nxt) * K + k) * P;
                 if (i < Lp) dst[i] = s.prefix[(static_cast<int64_t>(cur) * K + c.parent) * P + i];
@@ -959,7 +1047,7 @@ SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool st
     L.off_rbuf = off;
     off = align(off + sizeof(Cand) * kRescanBuf);
     L.off_key = off;
-    off = align(off + sizeof(uint4) * 2 * kRankMax + sizeof(int32_t) * kSelectThreads);
+    off = align(off + sizeof(uint4) * 2 * kRankMax + sizeof(int32_t) * (kSelectThreads + 64 + 1));
     L.off_f32 = off;
     off = align(off + sizeof(float) * (3 * static_cast<size_t>(K) + 2 * static_cast<size_t>(L.pen_len)));
     L.off_i32 = off;
@@ -980,6 +1068,13 @@ SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool st
         L.blk_in_lds = 1;
         L.off_blk = off;
         off = align(off + blk_bytes);
+    }
+    const size_t sig_bytes = sizeof(uint32_t) * 2 * static_cast<size_t>(K) * kSigWords;
+    L.sig_in_lds = 0;
+    if (L.prefix_in_lds && off + sig_bytes <= budget) {
+        L.sig_in_lds = 1;
+        L.off_sig = off;
+        off = align(off + sig_bytes);
     }
     L.smem = off;
     return L;
