@@ -96,6 +96,21 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// The same maximum by DPP row shifts and row broadcasts (no LDS round trips):
+// lane 63 ends with the maximum of all lanes, read back into every lane.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    const int lo = static_cast<int>(0xff800000u);  // -inf
+    int x = static_cast<int>(f32_bits(v));
+    auto step = [&](int y) { x = static_cast<int>(f32_bits(fmaxf(bits_f32(static_cast<uint32_t>(x)), bits_f32(static_cast<uint32_t>(y))))); };
+    step(__builtin_amdgcn_update_dpp(lo, x, 0x111, 0xf, 0xf, false));  // row_shr:1
+    step(__builtin_amdgcn_update_dpp(lo, x, 0x112, 0xf, 0xf, false));  // row_shr:2
+    step(__builtin_amdgcn_update_dpp(lo, x, 0x114, 0xf, 0xf, false));  // row_shr:4
+    step(__builtin_amdgcn_update_dpp(lo, x, 0x118, 0xf, 0xf, false));  // row_shr:8
+    step(__builtin_amdgcn_update_dpp(lo, x, 0x142, 0xa, 0xf, false));  // row_bcast:15 into rows 1, 3
+    step(__builtin_amdgcn_update_dpp(lo, x, 0x143, 0xc, 0xf, false));  // row_bcast:31 into rows 2, 3
+    return bits_f32(static_cast<uint32_t>(__builtin_amdgcn_readlane(x, 63)));
+}
+
 // Orders the LDS accesses of one wavefront (its lanes run in lockstep and the
 // LDS serves a wavefront's requests in issue order).
 __device__ __forceinline__ void wave_sync() {

@@ -138,6 +138,7 @@ struct SelectLayout {
     int prefix_in_lds;   // the prefixes live in LDS (else in the workspace)
     int blk_in_lds;      // the n-gram-blocked lists live in LDS (else in the workspace)
     int sig_in_lds;      // the prefixes' token signatures are kept (LDS; needs the prefixes in LDS)
+    int sig_words;       // 32-bit words per signature (256 or 64)
     size_t smem;
 };
 

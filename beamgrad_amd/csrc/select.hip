@@ -67,7 +67,7 @@ constexpr int kRescanPerThread = 16;
 constexpr int kTauHead = 2;       // entries per row behind the second tau bound
 constexpr int kWideBeam = 16;     // beams from which the wide-beam paths pay off
 constexpr int kPfRegs = 12;       // 16-byte prefetch registers per thread (K * M <= 6144)
-constexpr int kSigWords = 64;     // 2048-bit token signature of a beam's prefix
+constexpr int kSigWordsMax = 256;  // words of a beam's prefix signature (8192 bits; 2048 when LDS is short)
 constexpr int kScoreFilterMaxK = 32;  // beams up to which a rank compaction first ranks by score alone
 
 struct Lds {
@@ -94,7 +94,9 @@ struct Lds {
     ShortEntry* sl;   // [K, M + 1] the step's shortlists (see sl_at)
     int32_t* prefix;  // [2, K, P] (LDS) or the example's slice of the workspace
     int32_t* blk;     // [K, P] (LDS) or workspace
-    uint32_t* sig;    // [2, K, kSigWords] (LDS) prefix signatures, or null
+    uint32_t* sig;    // [2, K, sig_words] (LDS) prefix signatures, or null
+    int sig_words;
+    int sig_shift;    // 32 - log2(32 sig_words): hash bits kept
 };
 
 struct State {
@@ -128,20 +130,22 @@ __device__ __forceinline__ float inv_of(const Lds& s, int pen_len, int l, float 
 struct PrefixView {
     const int32_t* tok;
     int len;
-    const uint32_t* sig;  // a bit set for every token of tok[0, len) (a superset filter), or null
+    const uint32_t* sig;  // two bits set for every token of tok[0, len) (a superset filter), or null
+    int sig_shift;
 };
 
-// Signature bit of token v: a multiplicative hash to 11 bits.
-__device__ __forceinline__ uint32_t sig_bit(int v) { return (static_cast<uint32_t>(v) * 0x9E3779B1u) >> 21; }
+// The two signature bits of token v: multiplicative hashes to 32 - shift bits.
+__device__ __forceinline__ uint32_t sig_bit0(int v, int shift) { return (static_cast<uint32_t>(v) * 0x9E3779B1u) >> shift; }
+__device__ __forceinline__ uint32_t sig_bit1(int v, int shift) { return (static_cast<uint32_t>(v) * 0x85EBCA77u + 0x165667B1u) >> shift; }
 
 __device__ __forceinline__ PrefixView prefix_of(const DecodeParams& p, const Lds& s, int b, int k, int cur) {
     if (p.step_mode) {
         const int l = s.len[k];
         const int L = l < 0 ? 0 : (l < p.st_stride ? l : p.st_stride);
-        return PrefixView{p.st_prefix + (static_cast<int64_t>(b) * p.K + k) * p.st_stride, L, nullptr};
+        return PrefixView{p.st_prefix + (static_cast<int64_t>(b) * p.K + k) * p.st_stride, L, nullptr, 0};
     }
     return PrefixView{s.prefix + (static_cast<int64_t>(cur) * p.K + k) * p.prefix_cap, s.plen[cur * p.K + k],
-                      s.sig ? s.sig + (cur * p.K + k) * kSigWords : nullptr};
+                      s.sig ? s.sig + (cur * p.K + k) * s.sig_words : nullptr, s.sig_shift};
 }
 
 // Membership of v in a[0, n): eight independent loads in flight per round
@@ -167,8 +171,8 @@ __device__ __forceinline__ bool in_list(const int32_t* a, int n, int v) {
 // read; the rest are searched.
 __device__ __forceinline__ bool in_prefix(const PrefixView& pre, int v) {
     if (pre.sig) {
-        const uint32_t h = sig_bit(v);
-        if (((pre.sig[h >> 5] >> (h & 31u)) & 1u) == 0u) return false;
+        const uint32_t h0 = sig_bit0(v, pre.sig_shift), h1 = sig_bit1(v, pre.sig_shift);
+        if ((((pre.sig[h0 >> 5] >> (h0 & 31u)) & (pre.sig[h1 >> 5] >> (h1 & 31u))) & 1u) == 0u) return false;
     }
     return in_list(pre.tok, pre.len, v);
 }
@@ -516,6 +520,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     s.blk = L.blk_in_lds ? reinterpret_cast<int32_t*>(smem + L.off_blk)
                          : p.blocked + static_cast<int64_t>(b) * K * p.prefix_cap;
     s.sig = L.sig_in_lds && !p.step_mode ? reinterpret_cast<uint32_t*>(smem + L.off_sig) : nullptr;
+    s.sig_words = L.sig_words;
+    s.sig_shift = L.sig_words == kSigWordsMax ? 19 : 21;
 
     const int steps_b = p.step_mode ? 1 : example_steps(p, b);
     // this example's beams (slots past them stay empty) and EOS token
@@ -546,7 +552,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         s.plen[K + k] = 0;
     }
     if (s.sig)
-        for (int i = tid; i < 2 * K * kSigWords; i += kSelectThreads) s.sig[i] = 0u;
+        for (int i = tid; i < 2 * K * s.sig_words; i += kSelectThreads) s.sig[i] = 0u;
     if (tid == 0) {
         st.invalid = 0;
         st.gave_up = 0;
@@ -733,9 +739,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             // read beam, the tokens that followed an earlier occurrence of its
             // last n - 1 tokens; one thread per (beam, prefix position), the
             // list in any order (it is only searched)
-            const int n = p.ngram, P = p.prefix_cap;
-            for (int item = tid; item < K * P; item += kSelectThreads) {
-                const int k = item / P, i = item - k * P;
+            // (a decode's prefixes hold at most t tokens at step t)
+            const int n = p.ngram, P = p.prefix_cap, Pt = p.step_mode ? P : min(P, t);
+            for (int item = tid; item < K * Pt; item += kSelectThreads) {
+                const int k = item / Pt, i = item - k * Pt;
                 if (s.rcount[k] == -2) continue;
                 const PrefixView pre = prefix_of(p, s, b, k, cur);
                 if (i + n > pre.len) continue;
@@ -759,7 +766,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 float best = -kInf;
                 for (int k = tid; k < K; k += 64)
                     if (s.rcount[k] >= K) best = fmaxf(best, s.raw[k] + s.sl[sl_at(k, K - 1, SL)].lp);
-                best = wave_max(best);
+                best = wave_max_dpp(best);
                 if (tid == 0) st.tau = best;
             }
             // (b) Wide beams: the K-th largest raw among the first kTauHead
@@ -812,7 +819,9 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 offer(s, st, c);
             }
         }
-        end_round(s, st, K, L.sort_cap);
+        // (at most K offers: the first round of shortlisted offers joins them
+        // unless the one-pass path below needs the count)
+        if (M > 0 && p.use_tau && K >= kWideBeam) end_round(s, st, K, L.sort_cap);
 
         // Shortlisted candidates. Unconstrained wide beams: few reach tau, and
         // when they fit the collector beside what it holds, they are offered
@@ -947,21 +956,25 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             // the signature of both (one pass over every beam's positions)
             const int nxt = cur ^ 1;
             const int P = p.prefix_cap;
-            const int W = s.sig ? kSigWords : 0;
-            const int PW = P > W ? P : W;
+            const int Pc = min(P, t + 1);  // the new prefixes' length, at most
+            const int W = s.sig ? s.sig_words : 0;
+            const int PW = Pc > W ? Pc : W;
             for (int item = tid; item < K * PW; item += kSelectThreads) {
                 const int k = item / PW, i = item - k * PW;
                 const Cand c = k < nsel ? s.buf[k] : dead_cand();
                 if (i < W) {
                     uint32_t w = 0u;
                     if (c.parent >= 0) {
-                        w = s.sig[(cur * K + c.parent) * kSigWords + i];
-                        const uint32_t h = sig_bit(c.token);
-                        if (c.flp && c.token >= 0 && static_cast<int>(h >> 5) == i) w |= 1u << (h & 31u);
+                        w = s.sig[(cur * K + c.parent) * W + i];
+                        if (c.flp && c.token >= 0) {
+                            const uint32_t h0 = sig_bit0(c.token, s.sig_shift), h1 = sig_bit1(c.token, s.sig_shift);
+                            if (static_cast<int>(h0 >> 5) == i) w |= 1u << (h0 & 31u);
+                            if (static_cast<int>(h1 >> 5) == i) w |= 1u << (h1 & 31u);
+                        }
                     }
-                    s.sig[(nxt * K + k) * kSigWords + i] = w;
+                    s.sig[(nxt * K + k) * W + i] = w;
                 }
-                if (i >= P || c.parent < 0) continue;
+                if (i >= Pc || c.parent < 0) continue;
                 const int Lp = s.plen[cur * K + c.parent];
                 int32_t* dst = s.prefix + (static_cast<int64_t>(nxt) * K + k) * P;
                 if (i < Lp) dst[i] = s.prefix[(static_cast<int64_t>(cur) * K + c.parent) * P + i];
@@ -1069,12 +1082,16 @@ SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool st
         L.off_blk = off;
         off = align(off + blk_bytes);
     }
-    const size_t sig_bytes = sizeof(uint32_t) * 2 * static_cast<size_t>(K) * kSigWords;
     L.sig_in_lds = 0;
-    if (L.prefix_in_lds && off + sig_bytes <= budget) {
-        L.sig_in_lds = 1;
-        L.off_sig = off;
-        off = align(off + sig_bytes);
+    L.sig_words = 0;
+    for (int words = kSigWordsMax; words >= kSigWordsMax / 4 && !L.sig_in_lds; words /= 4) {
+        const size_t sig_bytes = sizeof(uint32_t) * 2 * static_cast<size_t>(K) * words;
+        if (L.prefix_in_lds && off + sig_bytes <= budget) {
+            L.sig_in_lds = 1;
+            L.sig_words = words;
+            L.off_sig = off;
+            off = align(off + sig_bytes);
+        }
     }
     L.smem = off;
     return L;
