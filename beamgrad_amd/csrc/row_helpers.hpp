@@ -151,19 +151,6 @@ __device__ __forceinline__ uint32_t key_pattern(int key) {
     return static_cast<uint16_t>(key < 0 ? (key ^ 0x7fff) : key);
 }
 
-// Inclusive prefix sum over the 64 lanes of a wavefront by DPP moves (row
-// shifts, then the row broadcasts of lanes 15 and 31): six dependent adds,
-// no LDS.
-__device__ __forceinline__ int wave_inclusive_sum(int x) {
-    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
-    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
-    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
-    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
-    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
-    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
-    return x;
-}
-
 // The maximum over a wavefront's 64 lanes (every lane gets it).
 __device__ __forceinline__ int wave_max_int(int x) {
     const int lo = static_cast<int>(0x80000000u);

@@ -831,39 +831,51 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         // offers it.
         bool one_pass = false;
         if (M > 0 && p.use_tau && K >= kWideBeam) {
-            // (K <= 64 with a shortlist: one wavefront, one lane per beam; the
-            // prefixes go to consecutive collector slots by a lane scan)
+            // (K <= 64 with a shortlist: lane k of wavefront 0 measures beam
+            // k's prefix, eight entries a round; a lane scan places the
+            // prefixes at consecutive collector slots, and the four
+            // wavefronts copy them, lane k for beam k)
             if (tid < 64) {
                 const float tau = st.tau;
                 const int k = tid;
                 int n = 0;
-                float praw = -kInf;
                 if (k < K) {
-                    praw = s.raw[k];
+                    const float praw = s.raw[k];
                     const int cnt = s.rcount[k];
-                    while (n < cnt && !(praw + s.sl[sl_at(k, n, SL)].lp < tau)) ++n;
-                }
-                int incl = n;
-                for (int off = 1; off < 64; off <<= 1) {
-                    const int up = __shfl_up(incl, off);
-                    if (tid >= off) incl += up;
-                }
-                const int total = __shfl(incl, 63);
-                const int base = st.count;
-                if (base + total <= L.sort_cap && n > 0) {
-                    const int new_len = s.len[k] + 1;
-                    const float inv = inv_of(s, pen_len, new_len, p.alpha);
-                    for (int i = 0; i < n; ++i) {
-                        const ShortEntry e = s.sl[sl_at(k, i, SL)];
-                        const float raw = praw + e.lp;
-                        s.buf[base + incl - n + i] = Cand{raw * inv, raw, k, e.token, new_len, 1};
+                    for (;;) {
+                        int reach = 0;
+#pragma unroll
+                        for (int u = 0; u < 8; ++u)
+                            reach += (n + u < cnt && !(praw + s.sl[sl_at(k, n + u, SL)].lp < tau)) ? 1 : 0;
+                        n += reach;
+                        if (reach < 8) break;
                     }
                 }
+                const int incl = wave_inclusive_sum(n);
+                const int total = __builtin_amdgcn_readlane(incl, 63);
+                const int base = st.count;
+                s.part[k] = base + incl - n;  // beam k's first collector slot
+                s.part[64 + k] = n;
                 if (tid == 0) st.rcount = base + total <= L.sort_cap ? base + total : -1;
             }
             __syncthreads();
             one_pass = st.rcount >= 0;
-            if (one_pass && tid == 0) st.count = st.rcount;
+            if (one_pass) {
+                const int k = tid & 63, w = tid >> 6;
+                const int n = k < K ? s.part[64 + k] : 0;
+                if (n > w) {
+                    const int slot0 = s.part[k];
+                    const float praw = s.raw[k];
+                    const int new_len = s.len[k] + 1;
+                    const float inv = inv_of(s, pen_len, new_len, p.alpha);
+                    for (int i = w; i < n; i += 4) {
+                        const ShortEntry e = s.sl[sl_at(k, i, SL)];
+                        const float raw = praw + e.lp;
+                        s.buf[slot0 + i] = Cand{raw * inv, raw, k, e.token, new_len, 1};
+                    }
+                }
+                if (tid == 0) st.count = st.rcount;
+            }
         }
         if (M > 0 && !one_pass) {
             const float tau = st.tau;
@@ -957,22 +969,31 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             const int nxt = cur ^ 1;
             const int P = p.prefix_cap;
             const int Pc = min(P, t + 1);  // the new prefixes' length, at most
-            const int W = s.sig ? s.sig_words : 0;
-            const int PW = Pc > W ? Pc : W;
+            const int W = s.sig ? s.sig_words : 0, W4 = W / 4;  // signatures copied 16 bytes an item
+            const int PW = Pc > W4 ? Pc : W4;
             for (int item = tid; item < K * PW; item += kSelectThreads) {
                 const int k = item / PW, i = item - k * PW;
                 const Cand c = k < nsel ? s.buf[k] : dead_cand();
-                if (i < W) {
-                    uint32_t w = 0u;
+                if (i < W4) {
+                    uint4 w = make_uint4(0u, 0u, 0u, 0u);
                     if (c.parent >= 0) {
-                        w = s.sig[(cur * K + c.parent) * W + i];
+                        w = reinterpret_cast<const uint4*>(s.sig + (cur * K + c.parent) * W)[i];
                         if (c.flp && c.token >= 0) {
-                            const uint32_t h0 = sig_bit0(c.token, s.sig_shift), h1 = sig_bit1(c.token, s.sig_shift);
-                            if (static_cast<int>(h0 >> 5) == i) w |= 1u << (h0 & 31u);
-                            if (static_cast<int>(h1 >> 5) == i) w |= 1u << (h1 & 31u);
+                            auto set = [&](uint32_t h) {
+                                if (static_cast<int>(h >> 7) != i) return;
+                                const uint32_t m = 1u << (h & 31u);
+                                switch ((h >> 5) & 3u) {
+                                    case 0: w.x |= m; break;
+                                    case 1: w.y |= m; break;
+                                    case 2: w.z |= m; break;
+                                    default: w.w |= m; break;
+                                }
+                            };
+                            set(sig_bit0(c.token, s.sig_shift));
+                            set(sig_bit1(c.token, s.sig_shift));
                         }
                     }
-                    s.sig[(nxt * K + k) * W + i] = w;
+                    reinterpret_cast<uint4*>(s.sig + (nxt * K + k) * W)[i] = w;
                 }
                 if (i >= Pc || c.parent < 0) continue;
                 const int Lp = s.plen[cur * K + c.parent];
