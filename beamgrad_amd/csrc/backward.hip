@@ -27,6 +27,7 @@ namespace {
 
 constexpr int kWalkThreads = 256;
 constexpr int kDenseThreads = 256;
+constexpr int kDenseBatch = 8;  // 16-byte logits loads in flight per thread (dense gradient)
 
 __global__ __launch_bounds__(kWalkThreads) void path_walk_kernel(BackwardParams p) {
     __shared__ float next[DBS_CUDA_MAX_BEAM];
@@ -246,17 +247,32 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardP
             auto out16 = [&](float g) -> uint32_t {
                 return OT == 1 ? f32_to_f16_rne(0.0f + g) : f32_to_bf16_rne(0.0f + g);
             };
-            for (int c = tid; c < V / 8; c += kDenseThreads) {
-                const uint4 q = x4[c];
-                const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-                uint32_t o[4];
+            // kDenseBatch 16-byte loads per thread are issued before any store of
+            // the batch: the stores may alias the logits as far as the compiler
+            // knows, so a load-convert-store loop would wait out one memory
+            // latency per block.
+            const int n4 = V / 8;
+            for (int c0 = tid; c0 < n4; c0 += kDenseBatch * kDenseThreads) {
+                uint4 q[kDenseBatch];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float lo, hi;
-                    terms(w[e], lo, hi);
-                    o[e] = out16(0.0f - lo * S) | (out16(0.0f - hi * S) << 16);
+                for (int u = 0; u < kDenseBatch; ++u) {
+                    const int c = c0 + u * kDenseThreads;
+                    q[u] = c < n4 ? x4[c] : make_uint4(0u, 0u, 0u, 0u);
                 }
-                o4[c] = make_uint4(o[0], o[1], o[2], o[3]);
+#pragma unroll
+                for (int u = 0; u < kDenseBatch; ++u) {
+                    const int c = c0 + u * kDenseThreads;
+                    if (c >= n4) break;
+                    const uint32_t w[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+                    uint32_t o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float lo, hi;
+                        terms(w[e], lo, hi);
+                        o[e] = out16(0.0f - lo * S) | (out16(0.0f - hi * S) << 16);
+                    }
+                    o4[c] = make_uint4(o[0], o[1], o[2], o[3]);
+                }
             }
             __syncthreads();  // the entries' tokens land after the rest of the row
             for (int i = tid; i < ne; i += kDenseThreads) {
@@ -268,9 +284,18 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardP
             return;
         }
     }
-    for (int v = tid; v < V; v += kDenseThreads) {
-        const float xv = load_logit<DT>(x, v);
-        const float pv = softmax_probability(xv, lse);
+    for (int v0 = tid; v0 < V; v0 += kDenseBatch * kDenseThreads) {
+      float xs[kDenseBatch];
+#pragma unroll
+      for (int u = 0; u < kDenseBatch; ++u) {
+          const int v = v0 + u * kDenseThreads;
+          xs[u] = v < V ? load_logit<DT>(x, v) : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < kDenseBatch; ++u) {
+        const int v = v0 + u * kDenseThreads;
+        if (v >= V) break;
+        const float pv = softmax_probability(xs[u], lse);
         // entry value of token v, by binary search of the sorted entry tokens
         int lo = 0, hi = ne;
         while (lo < hi) {
@@ -280,6 +305,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardP
         }
         const float g = (lo < ne && e_tok[lo] == v) ? e_val[lo] : 0.0f;
         store_out<OT>(p.out, row_off + v, g - pv * S, accumulate);
+      }
     }
 }
 
