@@ -49,7 +49,7 @@ constexpr int kRlStripes = 2 * 8 * kRlChunks;   // 608 stripes: V <= 155648
 constexpr uint32_t kBf16NegInf = 0xff80u;
 constexpr int kFinisher = 0;                    // the wavefront of segment 0 that finishes rows
 constexpr int kRecCap = 32;                     // survivor records per wavefront and row
-constexpr int kCkGroups = (kRlChunks + 7) / 8;  // chunk keys read eight at a time
+constexpr int kRlChunksShort = 32;              // chunks per thread for V <= 131072
 
 // f(integral_constant<int, i>) for i = 0 .. N - 1, expanded at compile time:
 // every register of the row is indexed with a constant (a loop the compiler
@@ -64,14 +64,18 @@ __device__ __forceinline__ void unrolled(F&& f) {
 }
 
 // Chunks below kMaskFrom are inside the row on every lane of both segments
-// (the launch checks it): only the later ones are masked.
-template <int kMaskFrom>
+// (the launch checks it): only the later ones are masked. kChunks 8-stripe
+// chunks per thread cover segments of up to 8 kChunks stripes.
+template <int kChunks, int kMaskFrom>
 __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, int64_t rows) {
+    constexpr int kRegs = 4 * kChunks;             // packed element pairs per thread
+    constexpr int kGroups = (kChunks + 7) / 8;     // chunk keys read eight at a time
+    static_assert(kChunks <= kRlChunks && kMaskFrom <= kChunks, "relay chunk range");
     // (the table first: at LDS address 0 its offsets need no base added)
     __shared__ __attribute__((aligned(1024))) float lut[2 * kLutHalf];
     __shared__ __attribute__((aligned(16))) unsigned char s_stage[8 * 1024];
     // chunk keys: thread t's keys of chunks 8 g .. 8 g + 7 at s_ck[g][t]
-    __shared__ __attribute__((aligned(16))) int16_t s_ck[kCkGroups][kRlThreads][8];
+    __shared__ __attribute__((aligned(16))) int16_t s_ck[kGroups][kRlThreads][8];
     __shared__ float s_acc[2][256];
     __shared__ uint64_t s_key[kSurvivorCap + 2];
     __shared__ float s_x[kSurvivorCap];
@@ -141,7 +145,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
     // ---- loads: chunk c (8 stripes x the wavefront's 64 lanes) of the
     // thread's segment, lane l's 16 bytes of stripe 8c + l/8, lanes 64 wv +
     // 8 (l % 8) .., straight into the registers the chunk will occupy ----
-    uint32_t reg[kRlRegs];
+    uint32_t reg[kRegs];
     auto lane_offset = [&]() __attribute__((always_inline)) -> int {
         int lr = l;
         asm volatile("" : "+v"(lr));
@@ -166,7 +170,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         const __amdgpu_buffer_rsrc_t rs = row_view(rr);
         const int voff = lane_offset();
 #pragma unroll
-        for (int c = 0; c < kRlChunks; ++c) issue_chunk(rs, voff, c);
+        for (int c = 0; c < kChunks; ++c) issue_chunk(rs, voff, c);
     };
 
     // ---- arrival: the segment's chunks transposed to lanes (a lane's 16
@@ -188,12 +192,12 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
     };
 
     // the maxima of the loaded registers as they are (each thread's values
-    // are then 8 lanes of 38 stripes: any partition of the row serves the
+    // are then 8 lanes of kChunks stripes: any partition of the row serves the
     // row maximum and the shortlist threshold)
     auto keys_loaded = [&]() __attribute__((always_inline)) {
         const int c_lim = lane_c_lim();
         uint32_t smax = 0x80008000u, umax = 0u;
-        unrolled<kRlChunks>([&](auto cc) __attribute__((always_inline)) {
+        unrolled<kChunks>([&](auto cc) __attribute__((always_inline)) {
             constexpr int c = decltype(cc)::value;
             uint32_t a = reg[4 * c], b2 = reg[4 * c + 1], c2 = reg[4 * c + 2], d = reg[4 * c + 3];
             if constexpr (c >= kMaskFrom) {
@@ -234,10 +238,10 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         transpose_chunk(stage, lr, reg[0], reg[1], reg[2], reg[3], T[0]);
         mask_chunk(std::integral_constant<int, 1>{});
         transpose_chunk(stage, lr, reg[4], reg[5], reg[6], reg[7], T[1]);
-        unrolled<kRlChunks>([&](auto cc) __attribute__((always_inline)) {
+        unrolled<kChunks>([&](auto cc) __attribute__((always_inline)) {
             constexpr int c = decltype(cc)::value;
             const uint32_t R4[4] = {T[c & 1][0], T[c & 1][1], T[c & 1][2], T[c & 1][3]};
-            if constexpr (c + 2 < kRlChunks) {
+            if constexpr (c + 2 < kChunks) {
                 mask_chunk(std::integral_constant<int, c + 2>{});
                 transpose_chunk(stage, lr, reg[4 * c + 8], reg[4 * c + 9], reg[4 * c + 10], reg[4 * c + 11], T[c & 1]);
             }
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
                                                           static_cast<int>(static_cast<int16_t>(kc >> 16)))) & 0xffffu;
             if constexpr ((c & 1) == 0) ckp[(c & 7) >> 1] = ck | 0x80000000u;  // (the odd chunk's key replaces -32768)
             else ckp[(c & 7) >> 1] = (ckp[(c & 7) >> 1] & 0xffffu) | (ck << 16);
-            if constexpr ((c & 7) == 7 || c + 1 == kRlChunks) {
+            if constexpr ((c & 7) == 7 || c + 1 == kChunks) {
 #pragma unroll
                 for (int u = ((c & 7) >> 1) + 1; u < 4; ++u) ckp[u] = 0x80008000u;  // chunks past the last
                 *reinterpret_cast<uint4*>(&s_ck[c >> 3][tid][0]) = make_uint4(ckp[0], ckp[1], ckp[2], ckp[3]);
@@ -286,10 +290,10 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
 #pragma unroll
         for (int q = 0; q < 4; ++q) lookup(q, cur[2 * q], cur[2 * q + 1]);
         issue_chunk(rs_next, voff_next, 0);
-        unrolled<kRlChunks>([&](auto cc) __attribute__((always_inline)) {
+        unrolled<kChunks>([&](auto cc) __attribute__((always_inline)) {
             constexpr int k0 = 4 * decltype(cc)::value;
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (k0 + 4 < kRlRegs) {
+            if constexpr (k0 + 4 < kRegs) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) lookup(k0 + 4 + q, nxt[2 * q], nxt[2 * q + 1]);
                 issue_chunk(rs_next, voff_next, k0 / 4 + 1);
@@ -349,9 +353,9 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         int n = 0;
         uint4* out = s_rec[pb] + kRecCap * wave;
         int* tok_out = s_rtok[pb] + kRecCap * wave;
-        uint32_t keys[4 * kCkGroups];
+        uint32_t keys[4 * kGroups];
 #pragma unroll
-        for (int g = 0; g < kCkGroups; ++g) {
+        for (int g = 0; g < kGroups; ++g) {
             const uint4 kq = *reinterpret_cast<const uint4*>(&s_ck[g][tid][0]);
             keys[4 * g] = kq.x;
             keys[4 * g + 1] = kq.y;
@@ -360,7 +364,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         }
         // eight chunks at a time: a group is passed over unless one of its
         // keys reaches tk on some lane (the packed maximum of its keys)
-        unrolled<kCkGroups>([&](auto gg) __attribute__((always_inline)) {
+        unrolled<kGroups>([&](auto gg) __attribute__((always_inline)) {
             constexpr int g = decltype(gg)::value;
             const uint32_t gm = pk_max_i16(pk_max_i16(keys[4 * g], keys[4 * g + 1]),
                                            pk_max_i16(keys[4 * g + 2], keys[4 * g + 3]));
@@ -369,7 +373,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
             if (__builtin_amdgcn_ballot_w64(gk >= tk) == 0) return;
             unrolled<8>([&](auto ii) __attribute__((always_inline)) {
                 constexpr int c = 8 * g + decltype(ii)::value;
-                if constexpr (c < kRlChunks) {
+                if constexpr (c < kChunks) {
                     const int ck = static_cast<int16_t>(keys[c >> 1] >> (16 * (c & 1)));
                     const bool flagged = ck >= tk;
                     const uint64_t bal = __builtin_amdgcn_ballot_w64(flagged);
@@ -752,12 +756,19 @@ hipError_t launch_row_relay(const DecodeParams& p, int64_t rows, hipStream_t str
         const int c_all = (end_r - (256 * (sg * per + 7) + 64 * 3 + 56) + 2047) >> 11;
         first_partial = c_all < first_partial ? c_all : first_partial;
     }
-    if (first_partial >= kRlChunks - 4)
-        hipLaunchKernelGGL((row_relay_kernel<kRlChunks - 4>), dim3(static_cast<unsigned>(grid)), dim3(kRlThreads), 0,
-                           stream, p, rows);
-    else
-        hipLaunchKernelGGL((row_relay_kernel<0>), dim3(static_cast<unsigned>(grid)), dim3(kRlThreads), 0, stream, p,
-                           rows);
+    // segments of at most 256 stripes (V <= 131072) fit 32 chunks: the
+    // chunks past them would only add +0 terms
+    const dim3 g(static_cast<unsigned>(grid)), blk(kRlThreads);
+    if (per <= 8 * kRlChunksShort) {
+        if (first_partial >= kRlChunksShort - 4)
+            hipLaunchKernelGGL((row_relay_kernel<kRlChunksShort, kRlChunksShort - 4>), g, blk, 0, stream, p, rows);
+        else
+            hipLaunchKernelGGL((row_relay_kernel<kRlChunksShort, 0>), g, blk, 0, stream, p, rows);
+    } else if (first_partial >= kRlChunks - 4) {
+        hipLaunchKernelGGL((row_relay_kernel<kRlChunks, kRlChunks - 4>), g, blk, 0, stream, p, rows);
+    } else {
+        hipLaunchKernelGGL((row_relay_kernel<kRlChunks, 0>), g, blk, 0, stream, p, rows);
+    }
     return hipGetLastError();
 }
 
