@@ -30,8 +30,10 @@ constexpr int kDenseThreads = 256;
 constexpr int kDenseBatch = 8;  // 16-byte logits loads in flight per thread (dense gradient)
 
 __global__ __launch_bounds__(kWalkThreads) void path_walk_kernel(BackwardParams p) {
-    __shared__ float next[DBS_CUDA_MAX_BEAM];
-    __shared__ float prev[DBS_CUDA_MAX_BEAM];
+    __shared__ float s_sum0[DBS_CUDA_MAX_BEAM];
+    __shared__ float s_sum1[DBS_CUDA_MAX_BEAM];
+    float* next = s_sum0;  // incoming gradient of each slot from the later steps
+    float* prev = s_sum1;
     __shared__ float draw[DBS_CUDA_MAX_BEAM];
     __shared__ int32_t par[DBS_CUDA_MAX_BEAM];
     const int b = static_cast<int>(blockIdx.x);
@@ -44,31 +46,64 @@ __global__ __launch_bounds__(kWalkThreads) void path_walk_kernel(BackwardParams 
     for (int64_t i = static_cast<int64_t>(steps_b) * K + tid; i < static_cast<int64_t>(T) * K; i += kWalkThreads)
         p.draws[static_cast<int64_t>(b) * T * K + i] = 0.0f;
     __syncthreads();
-    for (int t = steps_b - 1; t >= 0; --t) {
+    // A slot's trace entries and incoming gradients do not depend on the walk,
+    // so with one slot per thread (K <= kWalkThreads) step t - 1's are loaded
+    // into registers while step t is walked: the loop waits on the barriers,
+    // not on a memory round trip per step.
+    struct SlotIn {
+        int parent = -1, len = 0, tok = -1;
+        float gs = 0.0f, graw = 0.0f;
+        bool flp = false;
+    };
+    auto load_slot = [&](int t, int k) -> SlotIn {
+        SlotIn in;
+        const int64_t slot = (static_cast<int64_t>(b) * T + t) * K + k;
+        in.parent = p.parents[slot];
+        in.len = p.lengths[slot];
+        in.tok = p.tokens[slot];
+        in.flp = p.from_logprob[slot] != 0;
+        if (p.g_scores) in.gs = p.g_scores[slot];
+        if (p.g_raw) in.graw = p.g_raw[slot];
+        return in;
+    };
+    auto walk_slot = [&](int t, int k, const SlotIn& in) {
         const bool last = t == steps_b - 1;
-        const int64_t base = (static_cast<int64_t>(b) * T + t) * K;
-        for (int k = tid; k < K; k += kWalkThreads) {
-            const int64_t slot = base + k;
-            const int parent = p.parents[slot];
-            const bool valid = k < Kb && parent >= 0 && parent < Kb;  // malformed slots carry nothing
-            float d = 0.0f;
-            if (valid) {
-                float drank = 0.0f;
-                if (p.g_scores) drank = drank + p.g_scores[slot];
-                if (last && p.g_final) drank = drank + p.g_final[static_cast<int64_t>(b) * K + k];
-                const float inv_pen = 1.0f / length_penalty(p.lengths[slot], p.alpha);
-                d = next[k] + drank * inv_pen;
-                if (p.g_raw) d = d + p.g_raw[slot];
-                if (last && p.g_final_raw) d = d + p.g_final_raw[static_cast<int64_t>(b) * K + k];
+        const int parent = in.parent;
+        const bool valid = k < Kb && parent >= 0 && parent < Kb;  // malformed slots carry nothing
+        float d = 0.0f;
+        if (valid) {
+            float drank = 0.0f;
+            if (p.g_scores) drank = drank + in.gs;
+            if (last && p.g_final) drank = drank + p.g_final[static_cast<int64_t>(b) * K + k];
+            const float inv_pen = 1.0f / length_penalty(in.len, p.alpha);
+            d = next[k] + drank * inv_pen;
+            if (p.g_raw) d = d + in.graw;
+            if (last && p.g_final_raw) d = d + p.g_final_raw[static_cast<int64_t>(b) * K + k];
+        }
+        const bool flows = valid && d != 0.0f;
+        draw[k] = flows ? d : 0.0f;
+        par[k] = flows ? parent : -1;
+        p.draws[(static_cast<int64_t>(b) * T + t) * K + k] =
+            (flows && in.flp && in.tok >= 0 && in.tok < V) ? d : 0.0f;
+    };
+    const bool one_slot = K <= kWalkThreads;
+    SlotIn cur;
+    if (one_slot && tid < K && steps_b > 0) cur = load_slot(steps_b - 1, tid);
+    for (int t = steps_b - 1; t >= 0; --t) {
+        if (one_slot) {
+            if (tid < K) {
+                SlotIn nxt;
+                if (t > 0) nxt = load_slot(t - 1, tid);
+                walk_slot(t, tid, cur);
+                cur = nxt;
             }
-            const bool flows = valid && d != 0.0f;
-            draw[k] = flows ? d : 0.0f;
-            par[k] = flows ? parent : -1;
-            const int tok = p.tokens[slot];
-            p.draws[slot] = (flows && p.from_logprob[slot] && tok >= 0 && tok < V) ? d : 0.0f;
+        } else {
+            for (int k = tid; k < K; k += kWalkThreads) walk_slot(t, k, load_slot(t, k));
         }
         __syncthreads();
-        // each parent sums its children's raw-score gradients in slot order
+        // each parent sums its children's raw-score gradients in slot order;
+        // the sums become the next step's incoming gradients (the two
+        // buffers alternate, so one barrier separates the phases)
         for (int q = tid; q < K; q += kWalkThreads) {
             float s = 0.0f;
             for (int k = 0; k < K; ++k)
@@ -76,8 +111,9 @@ __global__ __launch_bounds__(kWalkThreads) void path_walk_kernel(BackwardParams 
             prev[q] = s;
         }
         __syncthreads();
-        for (int k = tid; k < K; k += kWalkThreads) next[k] = prev[k];
-        __syncthreads();
+        float* const swap = next;
+        next = prev;
+        prev = swap;
     }
 }
 
