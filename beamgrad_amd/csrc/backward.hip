@@ -287,18 +287,22 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardP
             // the batch: the stores may alias the logits as far as the compiler
             // knows, so a load-convert-store loop would wait out one memory
             // latency per block.
+            // Two batches alternate: the next batch's loads are in flight while
+            // the current one is converted and stored. Every load and store is
+            // unconditional, so the compiler's wait counts stay exact (a store
+            // under a branch makes it wait for every store before each use of
+            // a load): a block index past the row reads and writes the row's
+            // last block instead, the same bytes its own thread stores.
             const int n4 = V / 8;
-            for (int c0 = tid; c0 < n4; c0 += kDenseBatch * kDenseThreads) {
-                uint4 q[kDenseBatch];
+            constexpr int kStride = kDenseBatch * kDenseThreads;
+            auto block = [&](int c) __attribute__((always_inline)) { return c < n4 ? c : n4 - 1; };
+            auto load_batch = [&](uint4 (&q)[kDenseBatch], int c0) __attribute__((always_inline)) {
+#pragma unroll
+                for (int u = 0; u < kDenseBatch; ++u) q[u] = x4[block(c0 + u * kDenseThreads)];
+            };
+            auto store_batch = [&](const uint4 (&q)[kDenseBatch], int c0) __attribute__((always_inline)) {
 #pragma unroll
                 for (int u = 0; u < kDenseBatch; ++u) {
-                    const int c = c0 + u * kDenseThreads;
-                    q[u] = c < n4 ? x4[c] : make_uint4(0u, 0u, 0u, 0u);
-                }
-#pragma unroll
-                for (int u = 0; u < kDenseBatch; ++u) {
-                    const int c = c0 + u * kDenseThreads;
-                    if (c >= n4) break;
                     const uint32_t w[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
                     uint32_t o[4];
 #pragma unroll
@@ -307,8 +311,18 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardP
                         terms(w[e], lo, hi);
                         o[e] = out16(0.0f - lo * S) | (out16(0.0f - hi * S) << 16);
                     }
-                    o4[c] = make_uint4(o[0], o[1], o[2], o[3]);
+                    o4[block(c0 + u * kDenseThreads)] = make_uint4(o[0], o[1], o[2], o[3]);
                 }
+            };
+            const int pairs = (n4 + 2 * kStride - 1) / (2 * kStride);
+            uint4 qa[kDenseBatch], qb[kDenseBatch];
+            load_batch(qa, tid);
+            for (int i = 0; i < pairs; ++i) {
+                const int ca = tid + 2 * i * kStride;
+                load_batch(qb, ca + kStride);
+                store_batch(qa, ca);
+                load_batch(qa, ca + 2 * kStride);
+                store_batch(qb, ca + kStride);
             }
             __syncthreads();  // the entries' tokens land after the rest of the row
             for (int i = tid; i < ne; i += kDenseThreads) {
