@@ -171,7 +171,13 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardP
     __shared__ float s_sum;
     const int tid = static_cast<int>(threadIdx.x);
     const int K = p.K, T = p.T, V = p.V;
-    const int64_t r = blockIdx.x;  // row (b, t, q)
+    // Row (b, t, q). Workgroups go to the eight XCDs in turn (workgroup i to
+    // XCD i % 8), and the rows that read their logits are the path rows,
+    // which gather on a few parent slots q: with K = 8 they would all land on
+    // a few XCDs. Within each group of eight workgroups the rows are rotated
+    // by the group's index, which spreads every q over the XCDs.
+    const int64_t wg = blockIdx.x;
+    const int64_t r = (wg | 7) < static_cast<int64_t>(gridDim.x) ? ((wg & ~int64_t{7}) | ((wg + (wg >> 3)) & 7)) : wg;
     const int b = static_cast<int>(r / (static_cast<int64_t>(T) * K));
     const int t = static_cast<int>((r / K) % T);
     const int q = static_cast<int>(r % K);
