@@ -194,9 +194,9 @@ def _read_kernels(lib, steps: int) -> tuple[dict, float]:
     return kernels, n.value / steps
 
 
-def _traffic(config: str) -> float | None:
-    """HBM bytes per row-pass launch from the committed PMC summary."""
-    tfile = os.path.join(ROOT, "profiles", f"row_pass_{config}_traffic.txt")
+def _traffic(config: str, kernel: str = "row_pass") -> float | None:
+    """HBM bytes per launch of a kernel from the committed PMC summary."""
+    tfile = os.path.join(ROOT, "profiles", f"{kernel}_{config}_traffic.txt")
     if not os.path.exists(tfile):
         return None
     for line in open(tfile):
@@ -310,9 +310,11 @@ def c5_summary(m: dict) -> dict:
            "kernels_ms": {k: round(v["avg_ms"], 4) for k, v in m["kernels"].items()},
            "rows_read": m["rows_read"], "rows_with_gradient": m["rows_with_gradient"]}
     if "row_pass" in m["kernels"]:
-        out["forward_roofline"] = hbm_roofline(m["alg_bytes"], m["kernels"]["row_pass"]["avg_ms"], "row_pass")
+        out["forward_roofline"] = hbm_roofline(m["alg_bytes"], m["kernels"]["row_pass"]["avg_ms"], "row_pass",
+                                               _traffic("c5"))
     if "dense_gradient" in m["kernels"]:
-        out["backward_roofline"] = hbm_roofline(bwd_bytes, m["kernels"]["dense_gradient"]["avg_ms"], "dense_gradient")
+        out["backward_roofline"] = hbm_roofline(bwd_bytes, m["kernels"]["dense_gradient"]["avg_ms"], "dense_gradient",
+                                                _traffic("c5", "dense_gradient"))
     return out
 
 
