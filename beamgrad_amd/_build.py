@@ -4,7 +4,10 @@
 * ``_lib/libdbs_hip.so``: the HIP engine and its C ABIs (include/dbs_cuda.h,
   include/dbs_hip.h, and the host ABI include/dbs.h), compiled by hipcc for
   gfx950 only;
-* ``_C*.so``: the torch.ops.beamgrad operators, linked against libdbs_hip.
+* ``_C*.so``: defines the torch.ops.beamgrad operator schemas (the
+  namespace's owner, no kernels);
+* ``_C_hip*.so``: the operators' HIP kernels (CUDA dispatch key) and this
+  build's additional operators, linked against libdbs_hip.
 
 Run ``python -m beamgrad_amd._build`` (or ``__graft_entry__.build()``).
 """
@@ -44,9 +47,9 @@ def lib_path() -> str:
     return os.path.join(HERE, "_lib", "libdbs_hip.so")
 
 
-def ext_path() -> str:
+def ext_path(name: str = "_C_hip") -> str:
     suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
-    return os.path.join(HERE, "_C" + suffix)
+    return os.path.join(HERE, name + suffix)
 
 
 def _run(cmd: list[str]) -> None:
@@ -79,7 +82,9 @@ def build_lib() -> str:
     return out
 
 
-def build_ext() -> str:
+def _torch_module(name: str, source: str, hip: bool) -> str:
+    """One torch extension module compiled by g++: ``name`` from ``source``;
+    with ``hip`` it links libdbs_hip and torch's HIP libraries."""
     import torch
     from torch.utils import cpp_extension as ce
 
@@ -87,21 +92,29 @@ def build_ext() -> str:
     libdirs = ce.library_paths(device_type="cuda")
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
     py_inc = sysconfig.get_paths()["include"]
-    out = ext_path()
+    out = ext_path(name)
+    libs = ["-lc10", "-ltorch", "-ltorch_cpu"]
+    if hip:
+        libs = [f"-L{os.path.join(HERE, '_lib')}", "-ldbs_hip", *[f"-L{p}" for p in libdirs], *libs, "-lc10_hip",
+                "-ltorch_hip", "-Wl,-rpath,$ORIGIN/_lib"]
+    else:
+        libs = [*[f"-L{p}" for p in libdirs], *libs]
     cmd = [
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
         f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DUSE_ROCM=1", "-D__HIP_PLATFORM_AMD__=1",
-        "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-DTORCH_EXTENSION_NAME={name}", "-DTORCH_API_INCLUDE_EXTENSION_H",
         *[f"-I{p}" for p in incs], f"-I{py_inc}", f"-I{ROOT}/include", f"-I{ROCM}/include",
-        "csrc/torch_ops.cpp",
-        f"-L{os.path.join(HERE, '_lib')}", "-ldbs_hip",
-        *[f"-L{p}" for p in libdirs], "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
-        "-Wl,-rpath,$ORIGIN/_lib",
-        "-o", out + ".tmp",
+        source, *libs, "-o", out + ".tmp",
     ]
     _run(cmd)
     os.replace(out + ".tmp", out)
     return out
+
+
+def build_ext() -> list[str]:
+    """The schema owner ``_C`` and the HIP kernels ``_C_hip``."""
+    return [_torch_module("_C", "csrc/torch_schemas.cpp", hip=False),
+            _torch_module("_C_hip", "csrc/torch_ops.cpp", hip=True)]
 
 
 def build() -> None:
