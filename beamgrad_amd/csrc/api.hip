@@ -126,6 +126,19 @@ int finish_decode(hipStream_t stream, hipError_t e, const int32_t* fault) {
     return host != 0 ? DBS_CUDA_STATUS_LAUNCH_FAILED : DBS_CUDA_STATUS_OK;
 }
 
+// finish_decode() that always synchronises: for a caller that asked for the
+// fault word of a decode whose workspace the call allocated itself.
+int finish_decode_sync(hipStream_t stream, hipError_t e, const int32_t* fault) {
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    int32_t host = 0;
+    if (e == hipSuccess && fault) e = hipMemcpy(&host, fault, sizeof(host), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return status_of(e);
+    }
+    return host != 0 ? DBS_CUDA_STATUS_LAUNCH_FAILED : DBS_CUDA_STATUS_OK;
+}
+
 bool valid_dtype(int d) { return d == DBS_CUDA_DTYPE_F32 || d == DBS_CUDA_DTYPE_F16 || d == DBS_CUDA_DTYPE_BF16; }
 
 // Shape and option checks (reference cuda/dbs_cuda.cu:1254-1271). Candidate
@@ -232,7 +245,7 @@ int check_per_example(const DBSCudaDecodeArgs& a, int32_t* status, hipStream_t s
 int decode_common(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                   const DBSCudaSearchOptions* options, const uint8_t* banned_pe, const DBSCudaDecodeOutputs* outputs,
                   float* row_lse, void* workspace, int64_t workspace_bytes, void* stream_ptr,
-                  bool allow_overlap = true, int32_t* first_invalid = nullptr) {
+                  bool allow_overlap = true, int32_t* first_invalid = nullptr, int32_t** fault_out = nullptr) {
     if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !outputs || !outputs->final_scores)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
@@ -293,6 +306,10 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
     }
     int32_t* fault = nullptr;
     e = launch_decode(p, L, stream, ws, &fault, allow_overlap);
+    // the fault word lives in the workspace: handed out only where that is
+    // the caller's (an allocated one is released when the call returns)
+    if (fault_out) *fault_out = (e == hipSuccess && workspace) ? fault : nullptr;
+    if (fault_out && !workspace) return finish_decode_sync(stream, e, fault);
     return finish_decode(stream, e, fault);
 }
 
@@ -424,9 +441,10 @@ namespace dbs_hip {
 
 int decode_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                     const DBSCudaSearchOptions* options, const DBSCudaDecodeOutputs* outputs, float* row_lse,
-                    int32_t* first_invalid, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                    int32_t* first_invalid, void* workspace, int64_t workspace_bytes, hipStream_t stream,
+                    int32_t** fault) {
     return decode_common(inputs, data_type, from_logits, args, options, nullptr, outputs, row_lse, workspace,
-                         workspace_bytes, stream, true, first_invalid);
+                         workspace_bytes, stream, true, first_invalid, fault);
 }
 
 int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, float* draws,
@@ -572,6 +590,17 @@ DBS_CUDA_EXPORT int dbs_hip_decode_ex3(const void* inputs, int data_type, int fr
                                        float* row_lse, void* workspace, int64_t workspace_bytes, void* stream) {
     return decode_common(inputs, data_type, from_logits, args, options, banned_per_example, outputs, row_lse,
                          workspace, workspace_bytes, stream);
+}
+
+DBS_CUDA_EXPORT int dbs_hip_decode_ex4(const void* inputs, int data_type, int from_logits,
+                                       const DBSCudaDecodeArgs* args, const DBSCudaSearchOptions* options,
+                                       const uint8_t* banned_per_example, const DBSCudaDecodeOutputs* outputs,
+                                       float* row_lse, void* workspace, int64_t workspace_bytes,
+                                       int32_t** fault_word, void* stream) {
+    if (!fault_word) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    *fault_word = nullptr;
+    return decode_common(inputs, data_type, from_logits, args, options, banned_per_example, outputs, row_lse,
+                         workspace, workspace_bytes, stream, true, nullptr, fault_word);
 }
 
 DBS_CUDA_EXPORT int dbs_hip_decode_noalloc(const void* inputs, int data_type, int from_logits,

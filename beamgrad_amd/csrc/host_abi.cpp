@@ -313,9 +313,12 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
     const int64_t ws_bytes = dbs_cuda_decode_workspace_size(&a);
     need(ws_bytes > 0, "invalid decode arguments");
     void* ws = h->arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
+    int32_t* fault = nullptr;
     engine_check(dbs_hip::decode_for_host(x, data_type, from_logits ? 1 : 0, &a, &opts, &o, row_lse, first_invalid,
-                                          ws, ws_bytes, st),
+                                          ws, ws_bytes, st, &fault),
                  "HIP decode");
+    int32_t gave_up = 0;
+    if (fault) download(&gave_up, fault, 1, st);
 
     std::vector<int32_t> bad;
     if (first_invalid) {
@@ -333,6 +336,13 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
     download(out->from_logprob, o.from_logprob, BTK, st);
     if (ex) download(ex->row_lse, row_lse, BTK, st);
     hip_check(hipStreamSynchronize(st), "HIP decode");
+    // the overlapped select pass gave up waiting for rows of the row pass
+    // (bounded at 2 s; only when something starves or serialises the
+    // kernels): the traces of those examples are padding
+    if (gave_up != 0)
+        throw std::runtime_error(
+            "HIP decode: the select pass gave up waiting for the row pass (the GPU was starved or its kernels were "
+            "serialised); the trace is incomplete");
     // validate_inputs: the first example whose search read a NaN/+inf row,
     // reported at that row (reference src/decoder.cpp:143-171)
     for (int b = 0; b < static_cast<int>(bad.size()); ++b) {

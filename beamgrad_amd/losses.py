@@ -1,6 +1,18 @@
 # SPDX-License-Identifier: MIT
 """Sequence-level objectives on a :class:`BeamSearchResult`, differentiable
-through its scores (reference python/beamgrad/losses.py)."""
+through its scores (the interface of reference python/beamgrad/losses.py:
+139-169: name, arguments, reductions and error texts).
+
+``minimum_risk`` is the expected cost of the beams under a softmax of their
+scores. Its gradient has a closed form, so it is one autograd node instead
+of a chain of elementwise operators: with ``p = softmax(s / t)`` over an
+example's live beams (finite scores) and ``r = sum_k p_k c_k``,
+
+    d r / d s_k = p_k (c_k - r) / t        (live beams; 0 for dead ones)
+
+An example without a live beam has risk 0 and no gradient, and the costs of
+dead beams are never read (NaN there is harmless).
+"""
 
 from __future__ import annotations
 
@@ -10,32 +22,59 @@ from ._search import BeamSearchResult
 
 __all__ = ["minimum_risk"]
 
+_REDUCTIONS = ("mean", "sum", "none")
 
-def _reduce(loss: torch.Tensor, reduction: str) -> torch.Tensor:
-    if reduction == "mean":
-        return loss.mean()
-    if reduction == "sum":
-        return loss.sum()
-    if reduction == "none":
-        return loss
-    raise ValueError(f"reduction must be 'mean', 'sum' or 'none', got {reduction!r}")
+
+class _ExpectedCost(torch.autograd.Function):
+    """Per-example risk [B] of scores [B, K] under costs [B, K]."""
+
+    generate_vmap_rule = True  # elementwise and last-dim reductions only
+
+    @staticmethod
+    def forward(scores: torch.Tensor, costs: torch.Tensor, temperature: float):
+        live = torch.isfinite(scores)
+        z = torch.where(live, scores / temperature, float("-inf"))
+        top = z.amax(-1, keepdim=True)
+        # rows without a live beam: every weight is 0 (exp(-inf - 0))
+        w = torch.exp(z - torch.where(torch.isfinite(top), top, 0.0))
+        total = w.sum(-1, keepdim=True)
+        p = w / torch.where(total > 0, total, 1.0)
+        c = torch.where(live, costs.to(device=p.device, dtype=p.dtype), 0.0)
+        risk = (p * c).sum(-1)
+        return risk, p, c
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        risk, p, c = output
+        ctx.save_for_backward(p, c, risk)
+        ctx.temperature = inputs[2]
+        ctx.mark_non_differentiable(p, c)
+
+    @staticmethod
+    def backward(ctx, grad_risk: torch.Tensor, _grad_p, _grad_c):
+        p, c, risk = ctx.saved_tensors
+        g = (grad_risk / ctx.temperature)[:, None] * p * (c - risk[:, None])
+        return g, None, None
 
 
 def minimum_risk(result: BeamSearchResult, costs: torch.Tensor, temperature: float = 1.0,
                  reduction: str = "mean") -> torch.Tensor:
-    """Expected cost of the beams under ``softmax(scores / temperature)``; dead
-    beams (-inf scores) get no probability and their costs are ignored
-    (reference python/beamgrad/losses.py:139-169)."""
+    """Expected cost of the beams under ``softmax(scores / temperature)``.
+
+    ``costs[b, k]`` is the cost of beam ``k`` (no gradient needed); dead beams
+    (``-inf`` scores) get no probability and their costs are ignored. The
+    gradient reaches the scores, and through them the inputs of the search,
+    along the paths of the beams found."""
     if not temperature > 0:
         raise ValueError(f"temperature must be positive, got {temperature}")
-    scores = result.scores if result.scores.dim() == 2 else result.scores[None]
+    scores = result.scores
+    if scores.dim() == 1:
+        scores = scores[None]
     if tuple(costs.shape) != tuple(scores.shape):
         raise ValueError(f"costs must have the scores' shape {tuple(scores.shape)}, got {tuple(costs.shape)}")
-    live = torch.isfinite(scores)
-    any_live = live.any(-1, keepdim=True)
-    logits = torch.where(live, scores / temperature, float("-inf"))
-    logits = torch.where(any_live, logits, torch.zeros_like(logits))
-    probs = torch.softmax(logits, dim=-1)
-    costs = torch.where(live, costs.to(probs), 0.0)
-    loss = (probs * costs).sum(-1) * any_live[:, 0]
-    return _reduce(loss, reduction)
+    if reduction not in _REDUCTIONS:
+        raise ValueError(f"reduction must be 'mean', 'sum' or 'none', got {reduction!r}")
+    risk = _ExpectedCost.apply(scores, costs, float(temperature))[0]
+    if reduction == "none":
+        return risk
+    return risk.sum() if reduction == "sum" else risk.mean()

@@ -30,6 +30,33 @@ DBS_CUDA_EXPORT int dbs_hip_decode_ex3(
     int64_t workspace_bytes,
     void* stream);
 
+/* dbs_hip_decode_ex3 that also says where the decode records a select-pass
+ * wait that gave up, so that an asynchronous caller can tell an incomplete
+ * trace from a good one without validate flags. *fault_word is set to a
+ * device int32 inside `workspace` that is non-zero, once `stream` has passed
+ * the decode, if a wait of the overlapped decode gave up (those examples'
+ * traces are padding; invalid_input[b] == 2 where flags were given), or to
+ * NULL when the decode ran its passes one after the other (nothing can give
+ * up) or failed to launch. The word is valid until the workspace is reused.
+ * Without a caller workspace (workspace == NULL) the call synchronises,
+ * returns DBS_CUDA_STATUS_LAUNCH_FAILED for a wait that gave up and sets
+ * *fault_word to NULL. No counterpart in the reference, whose CUDA engine
+ * has no overlapped passes (reference include/dbs_cuda.h:299-315 is the
+ * decode it extends). */
+DBS_CUDA_EXPORT int dbs_hip_decode_ex4(
+    const void* inputs,
+    int data_type,
+    int from_logits,
+    const DBSCudaDecodeArgs* args,
+    const DBSCudaSearchOptions* options,
+    const uint8_t* banned_per_example,
+    const DBSCudaDecodeOutputs* outputs,
+    float* row_lse,
+    void* workspace,
+    int64_t workspace_bytes,
+    int32_t** fault_word,
+    void* stream);
+
 /* dbs_hip_decode_ex3 without a workspace argument and without any device
  * allocation, for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the

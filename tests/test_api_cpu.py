@@ -185,3 +185,57 @@ def test_batching_rules_are_registered():
     for op in ("decode", "decode_ex", "decode_backward", "decode_backward_as", "final_scores_backward",
                "final_scores_path_gradient", "length_penalty", "backtrack"):
         assert C._dispatch_has_kernel_for_dispatch_key(f"beamgrad::{op}", "FuncTorchBatched"), op
+
+
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+@pytest.mark.parametrize("temperature", [1.0, 0.25, 3.0])
+def test_minimum_risk_closed_form(reduction, temperature):
+    """minimum_risk and its gradient against the closed form in float64
+    (reference python/beamgrad/losses.py:139-169 defines the objective):
+    risk_b = sum_k p_k c_k with p = softmax(s_b / t) over live beams, and
+    d risk_b / d s_k = p_k (c_k - risk_b) / t; dead beams (-inf) get no
+    probability and their costs (even NaN) are never read; an example with
+    no live beam has risk 0 and no gradient."""
+    from collections import namedtuple
+
+    rng = np.random.default_rng(17)
+    B, K = 6, 5
+    s = rng.normal(0.0, 2.0, (B, K))
+    s[1, [0, 3]] = -np.inf
+    s[4, :] = -np.inf
+    c = rng.random((B, K))
+    c[1, 3] = np.nan
+    c[4, :] = np.nan
+    want_risk = np.zeros(B)
+    want_grad = np.zeros((B, K))
+    for b in range(B):
+        live = np.isfinite(s[b])
+        if not live.any():
+            continue
+        z = s[b, live] / temperature
+        p = np.exp(z - z.max())
+        p /= p.sum()
+        want_risk[b] = (p * c[b, live]).sum()
+        want_grad[b, live] = p * (c[b, live] - want_risk[b]) / temperature
+    scale = {"mean": 1.0 / B, "sum": 1.0, "none": 1.0}[reduction]
+    R = namedtuple("R", "scores")
+    st = torch.tensor(s, requires_grad=True)
+    loss = bg.losses.minimum_risk(R(st), torch.tensor(c), temperature, reduction)
+    want_loss = {"mean": want_risk.mean(), "sum": want_risk.sum(), "none": want_risk}[reduction]
+    np.testing.assert_allclose(loss.detach().numpy(), want_loss, rtol=1e-12, atol=1e-15)
+    loss.sum().backward()
+    np.testing.assert_allclose(st.grad.numpy(), want_grad * scale, rtol=1e-10, atol=1e-15)
+
+
+def test_minimum_risk_errors():
+    from collections import namedtuple
+
+    R = namedtuple("R", "scores")
+    s = torch.zeros(2, 3)
+    with pytest.raises(ValueError, match="temperature must be positive, got 0"):
+        bg.losses.minimum_risk(R(s), torch.zeros(2, 3), 0)
+    with pytest.raises(ValueError, match=r"costs must have the scores' shape \(2, 3\), got \(3, 2\)"):
+        bg.losses.minimum_risk(R(s), torch.zeros(3, 2), reduction="bad")
+    with pytest.raises(ValueError, match="reduction must be 'mean', 'sum' or 'none', got 'bad'"):
+        bg.losses.minimum_risk(R(s), torch.zeros(2, 3), reduction="bad")
+    assert bg.losses.minimum_risk(R(torch.zeros(3)), torch.zeros(1, 3), reduction="none").shape == (1,)

@@ -159,3 +159,81 @@ def test_two_threads_two_streams(hip, oracle, overlap_on):
         for rep in range(4):
             assert first_difference(results[i][rep], wants[i]) is None, (i, rep)
     assert _timeouts(overlap_on) == 0
+
+
+def _torch_case(seed):
+    """A multi-step 16-bit from-logits case (decoded overlapped by default)
+    as a torch tensor, with its options."""
+    import beamgrad_amd as bg
+
+    case = _big_case(seed)
+    while case["T"] < 2:
+        case = _big_case(case["seed"] + 1)
+    # no constraints: the options below carry EOS, min_length and alpha only
+    case["kw"] = kw = dict(case["kw"], banned=None, banned_per_example=None, no_repeat_ngram_size=0,
+                           repetition_penalty=1.0)
+    x = torch.from_numpy(case["xin"].view(np.int16)).cuda()
+    x = x.view(torch.bfloat16 if case["dtype"] == "bf16" else torch.float16)
+    eos = [kw["eos_token"], *kw["extra_eos"]] if kw["eos_token"] >= 0 and kw["extra_eos"] else kw["eos_token"]
+
+    def opts(validate):
+        return bg.BeamOptions(beam_size=case["K"], eos_token=eos, min_length=kw["min_length"],
+                              length_penalty_alpha=kw["alpha"], validate_inputs=validate)
+
+    return case, x, opts
+
+
+@pytest.mark.parametrize("validate", [True, False])
+def test_given_up_wait_raises_from_the_torch_ops(oracle, monkeypatch, validate):
+    """decode / final_scores raise a RuntimeError of their own (not the NaN
+    ValueError) whether or not the inputs are validated: with validate the
+    example's flag says 2, without it the decode's fault word is read back.
+    The same calls without the knob match the oracle."""
+    import beamgrad_amd as bg
+
+    case, x, opts = _torch_case(7430)
+    kw = case["kw"]
+    _forced_give_up(monkeypatch)
+    with pytest.raises(RuntimeError, match="gave up waiting for the row pass"):
+        bg.decode(x, opts(validate), kw["steps"], from_logits=True)
+    with pytest.raises(RuntimeError, match="gave up waiting for the row pass"):
+        bg.final_scores(x.detach().clone().requires_grad_(True), opts(validate), kw["steps"], from_logits=True)
+    monkeypatch.delenv("DBS_HIP_TEST_WAIT_GIVE_UP")
+    out = bg.decode(x, opts(validate), kw["steps"], from_logits=True)
+    want = oracle.decode(case["xin"], dtype=case["dtype"], **kw)
+    got = {k: getattr(out, k).cpu().numpy() for k in ("final_scores", "final_raw_scores", "scores", "raw_scores")}
+    for k in ("final_lengths", "tokens", "parents", "lengths"):
+        got[k] = getattr(out, k).cpu().numpy().astype(np.int32)
+    assert first_difference(got, want, tuple(got)) is None
+    scores = bg.final_scores(x, opts(validate), kw["steps"], from_logits=True)
+    assert np.array_equal(scores.detach().cpu().numpy().view(np.uint32), want["final_scores"].view(np.uint32))
+
+
+@pytest.mark.parametrize("validate", [0, 1])
+def test_given_up_wait_fails_the_host_abi_decode(oracle, monkeypatch, validate):
+    """dbs_decode_batch_into_ex on the GPU returns DBS_ERROR_RUNTIME with its
+    own error text for a given-up wait, and decodes as the oracle without
+    the knob."""
+    from beamgrad_amd import _build
+    from tests.host_abi import HostLib
+
+    case, _x, _opts = _torch_case(7440)
+    kw = case["kw"]
+    lib = HostLib(_build.lib_path())
+    h = lib.create(beam_size=case["K"], eos_token=kw["eos_token"], length_penalty_alpha=kw["alpha"],
+                   min_length=kw["min_length"], validate_inputs=validate)
+    try:
+        if kw["extra_eos"]:
+            assert lib.set_extra_eos(h, kw["extra_eos"]) == 0, lib.error()
+        _forced_give_up(monkeypatch)
+        st, _out = lib.decode(h, case["xin"], case["K"], dtype=case["dtype"], from_logits=True, steps=kw["steps"])
+        assert st == -2, (st, lib.error())  # DBS_ERROR_RUNTIME
+        assert "gave up waiting for the row pass" in lib.error()
+        monkeypatch.delenv("DBS_HIP_TEST_WAIT_GIVE_UP")
+        st, out = lib.decode(h, case["xin"], case["K"], dtype=case["dtype"], from_logits=True, steps=kw["steps"])
+        assert st == 0, lib.error()
+    finally:
+        lib.destroy(h)
+    want = oracle.decode(case["xin"], dtype=case["dtype"], **kw)
+    assert first_difference(out, want, ("final_scores", "final_raw_scores", "final_lengths", "tokens", "parents",
+                                        "lengths", "scores", "raw_scores", "from_logprob", "row_lse")) is None
