@@ -39,7 +39,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-LIB_SOURCES = ["csrc/api.hip", "csrc/host_abi.cpp", "csrc/decode.hip", "csrc/row_pass.hip", "csrc/row_resident.hip",
+LIB_SOURCES = ["csrc/api.hip", "csrc/host_abi.cpp", "csrc/host_results.cpp", "csrc/decode.hip", "csrc/row_pass.hip", "csrc/row_resident.hip",
                "csrc/row_pipe.hip", "csrc/row_logprob.hip", "csrc/row_stream.hip", "csrc/row_relay.hip", "csrc/select.hip", "csrc/backward.hip"]
 
 

@@ -440,11 +440,11 @@ int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* 
 namespace dbs_hip {
 
 int decode_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
-                    const DBSCudaSearchOptions* options, const DBSCudaDecodeOutputs* outputs, float* row_lse,
-                    int32_t* first_invalid, void* workspace, int64_t workspace_bytes, hipStream_t stream,
-                    int32_t** fault) {
-    return decode_common(inputs, data_type, from_logits, args, options, nullptr, outputs, row_lse, workspace,
-                         workspace_bytes, stream, true, first_invalid, fault);
+                    const DBSCudaSearchOptions* options, const uint8_t* banned_per_example,
+                    const DBSCudaDecodeOutputs* outputs, float* row_lse, int32_t* first_invalid, void* workspace,
+                    int64_t workspace_bytes, hipStream_t stream, int32_t** fault) {
+    return decode_common(inputs, data_type, from_logits, args, options, banned_per_example, outputs, row_lse,
+                         workspace, workspace_bytes, stream, true, first_invalid, fault);
 }
 
 int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, float* draws,

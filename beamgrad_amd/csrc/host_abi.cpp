@@ -2,7 +2,8 @@
 //
 // The libdbs host C ABI (include/dbs.h) served by the HIP engine: decoder
 // handles and the batch entry points of the reference's host library
-// (reference src/c_api.cpp:312-400, 700-983), with host arrays in and out.
+// (reference src/c_api.cpp:312-400, 700-983), with host arrays in and out,
+// and the two drivers the other entry points (host_results.cpp) share.
 //
 // A call checks its arguments as the reference does, with the same status
 // and error text, stages the host arrays into device buffers owned by the
@@ -11,92 +12,59 @@
 // backward accumulates into the caller's host buffer exactly where the
 // reference's does: the log-prob entries on the beams' paths (from the
 // per-slot path gradients), or, from logits, the whole rows on those paths
-// (from the device's log-softmax gradient rows).
-#include <hip/hip_runtime.h>
+// (from the device's log-softmax gradient rows, computed a bounded chunk of
+// examples at a time).
+#include "host_abi.hpp"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
-#include <cstring>
 #include <exception>
-#include <limits>
-#include <mutex>
-#include <new>
-#include <stdexcept>
-#include <string>
-#include <vector>
 
-#include "dbs.h"
 #include "dbs_cuda.h"
 #include "dbs_hip.h"
 #include "host_entry.hpp"
 
+namespace dbs_host {
+
+std::atomic<int64_t> g_device_bytes{0};
+std::atomic<int64_t> g_device_allocations{0};
+
 namespace {
-
 thread_local std::string t_error;  // the calling thread's latest error
-
-// Device buffers of one handle, by purpose; grown on demand, freed with the
-// handle.
-enum Slot : int {
-    kInputs, kBanned, kSteps, kFinalScores, kFinalRaw, kFinalLengths, kTokens, kParents, kLengths, kScores,
-    kRawScores, kFromLogprob, kRowLse, kFirstInvalid, kWorkspace, kGradFinal, kGradFinalRaw, kGradScores,
-    kGradRaw, kDraws, kDense, kSlotCount
-};
-
-struct Arena {
-    void* ptr[kSlotCount] = {};
-    size_t size[kSlotCount] = {};
-
-    void* get(Slot s, size_t bytes) {
-        if (bytes == 0) bytes = 1;
-        if (size[s] < bytes) {
-            if (ptr[s]) (void)hipFree(ptr[s]);
-            ptr[s] = nullptr;
-            size[s] = 0;
-            if (hipMalloc(&ptr[s], bytes) != hipSuccess) {
-                (void)hipGetLastError();
-                ptr[s] = nullptr;
-                throw std::bad_alloc();
-            }
-            size[s] = bytes;
-        }
-        return ptr[s];
-    }
-    void release() {
-        for (int i = 0; i < kSlotCount; ++i) {
-            if (ptr[i]) (void)hipFree(ptr[i]);
-            ptr[i] = nullptr;
-            size[i] = 0;
-        }
-    }
-};
-
 }  // namespace
 
-struct DBSDecoderHandle {
-    // options after their defaults (reference src/c_api.cpp:160-189)
-    int beam_size = 8;
-    int eos_token = -1;
-    float alpha = 0.0f;
-    int min_length = 0;
-    int validate = 0;
-    int pool_multiplier = 0;
-    std::vector<int32_t> extra_eos;
-
-    std::mutex error_mutex;
-    std::string error;
-
-    std::mutex run_mutex;  // one GPU call at a time on a handle
-    Arena arena;
-    hipStream_t stream = nullptr;
-    int device = -1;
-
-    ~DBSDecoderHandle() {
-        arena.release();
-        if (stream) (void)hipStreamDestroy(stream);
+void* Arena::get(Slot s, size_t bytes) {
+    if (bytes == 0) bytes = 1;
+    if (size[s] < bytes) {
+        if (ptr[s]) {
+            (void)hipFree(ptr[s]);
+            g_device_bytes -= static_cast<int64_t>(size[s]);
+        }
+        ptr[s] = nullptr;
+        size[s] = 0;
+        if (hipMalloc(&ptr[s], bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            ptr[s] = nullptr;
+            throw std::bad_alloc();
+        }
+        size[s] = bytes;
+        g_device_bytes += static_cast<int64_t>(bytes);
+        ++g_device_allocations;
     }
-};
+    return ptr[s];
+}
 
-namespace {
+void Arena::release() {
+    for (int i = 0; i < kSlotCount; ++i) {
+        if (ptr[i]) {
+            (void)hipFree(ptr[i]);
+            g_device_bytes -= static_cast<int64_t>(size[i]);
+        }
+        ptr[i] = nullptr;
+        size[i] = 0;
+    }
+}
 
 void need(bool ok, const char* message) {
     if (!ok) throw std::invalid_argument(message);
@@ -107,48 +75,25 @@ size_t mul(size_t a, size_t b, const char* what) {
     return a * b;
 }
 
-// An input error of one example, prefixed as the reference's batch functions
-// do (reference src/c_api.cpp:264-267).
-[[noreturn]] void example_error(int b, const std::string& what) {
+void example_error(int b, const std::string& what) {
     throw std::invalid_argument("example " + std::to_string(b) + ": " + what);
 }
 
-void record(DBSDecoderHandle* h, const std::string& message) {
+void record(DBSDecoderHandle* h, const std::string& message, int category) {
     t_error = message;
     if (h) {
-        std::lock_guard<std::mutex> lock(h->error_mutex);
-        h->error = message;
+        {
+            std::lock_guard<std::mutex> lock(h->error_mutex);
+            h->error = message;
+        }
+        if (category != 0) {
+            std::lock_guard<std::mutex> lock(h->stats_mutex);
+            h->stats.last_error_category = category;
+        }
     }
 }
 
-// Runs body and turns its exceptions into the ABI's statuses; a success
-// clears the recorded errors.
-template <class Body>
-int run(DBSDecoderHandle* h, Body&& body) {
-    try {
-        body();
-        record(h, std::string());
-        return DBS_OK;
-    } catch (const std::invalid_argument& e) {
-        record(h, e.what());
-        return DBS_ERROR_INVALID_ARGUMENT;
-    } catch (const std::overflow_error& e) {
-        record(h, e.what());
-        return DBS_ERROR_INVALID_ARGUMENT;
-    } catch (const std::length_error& e) {
-        record(h, e.what());
-        return DBS_ERROR_INVALID_ARGUMENT;
-    } catch (const std::bad_alloc&) {
-        record(h, "out of memory");
-        return DBS_ERROR_RUNTIME;
-    } catch (const std::exception& e) {
-        record(h, e.what());
-        return DBS_ERROR_RUNTIME;
-    } catch (...) {
-        record(h, "unknown exception");
-        return DBS_ERROR_UNKNOWN;
-    }
-}
+const char* last_thread_error() { return t_error.c_str(); }
 
 void hip_check(hipError_t e, const char* what) {
     if (e == hipSuccess) return;
@@ -163,8 +108,6 @@ void engine_check(int status, const char* what) {
     throw std::runtime_error(std::string(what) + ": " + dbs_cuda_status_string(status));
 }
 
-// The handle's stream on the calling thread's device (set up on first use;
-// a change of device drops the buffers of the previous one).
 hipStream_t stream_of(DBSDecoderHandle* h) {
     int device = 0;
     hip_check(hipGetDevice(&device), "no usable GPU");
@@ -180,24 +123,6 @@ hipStream_t stream_of(DBSDecoderHandle* h) {
     return h->stream;
 }
 
-template <class T>
-T* upload(DBSDecoderHandle* h, Slot s, const T* host, size_t count, hipStream_t st) {
-    if (!host) return nullptr;
-    T* d = static_cast<T*>(h->arena.get(s, sizeof(T) * count));
-    hip_check(hipMemcpyAsync(d, host, sizeof(T) * count, hipMemcpyHostToDevice, st), "copy to the device");
-    return d;
-}
-
-template <class T>
-T* device_out(DBSDecoderHandle* h, Slot s, const T* host, size_t count) {
-    return host ? static_cast<T*>(h->arena.get(s, sizeof(T) * count)) : nullptr;
-}
-
-template <class T>
-void download(T* host, const T* dev, size_t count, hipStream_t st) {
-    if (host && dev) hip_check(hipMemcpyAsync(host, dev, sizeof(T) * count, hipMemcpyDeviceToHost, st), "copy back");
-}
-
 size_t dtype_bytes(int data_type) { return data_type == DBS_DTYPE_F32 ? 4 : 2; }
 
 void check_dtype(int data_type) {
@@ -205,7 +130,6 @@ void check_dtype(int data_type) {
          "unsupported DBS data type");
 }
 
-// Steps of each example (reference src/c_api.cpp:269-279).
 std::vector<int32_t> steps_of(const int32_t* steps_per_example, int B, int T) {
     std::vector<int32_t> out(static_cast<size_t>(B), T);
     if (!steps_per_example) return out;
@@ -217,17 +141,189 @@ std::vector<int32_t> steps_of(const int32_t* steps_per_example, int B, int T) {
     return out;
 }
 
-// The engine's own limits (device ABI): K <= DBS_CUDA_MAX_BEAM, candidate
-// indices K * V within int32, at most DBS_CUDA_MAX_EXTRA_EOS extra EOS tokens.
-void check_engine_limits(const DBSDecoderHandle* h, int V) {
-    if (h->beam_size > DBS_CUDA_MAX_BEAM ||
-        static_cast<int64_t>(h->beam_size) * V > std::numeric_limits<int32_t>::max())
-        throw std::invalid_argument("beam_size " + std::to_string(h->beam_size) + " with vocab_size " +
-                                    std::to_string(V) + " is beyond the HIP engine (beam_size <= " +
-                                    std::to_string(DBS_CUDA_MAX_BEAM) + ", beam_size * vocab_size < 2^31)");
+void check_engine_limits(const DBSDecoderHandle* h, int K, int V) {
+    if (K > DBS_CUDA_MAX_BEAM || static_cast<int64_t>(K) * V > std::numeric_limits<int32_t>::max())
+        throw std::invalid_argument("beam_size " + std::to_string(K) + " with vocab_size " + std::to_string(V) +
+                                    " is beyond the HIP engine (beam_size <= " + std::to_string(DBS_CUDA_MAX_BEAM) +
+                                    ", beam_size * vocab_size < 2^31)");
     if (h->extra_eos.size() > static_cast<size_t>(DBS_CUDA_MAX_EXTRA_EOS))
         throw std::invalid_argument("more than " + std::to_string(DBS_CUDA_MAX_EXTRA_EOS) +
                                     " extra EOS tokens are beyond the HIP engine");
+}
+
+void run_decode(DBSDecoderHandle* h, const DecodeJob& j) {
+    const int B = j.B, T = j.T, K = j.K, V = j.V;
+    check_engine_limits(h, K, V);
+    const size_t BK = static_cast<size_t>(B) * K;
+    const size_t BTK = mul(BK, static_cast<size_t>(T), "batch size overflow");
+    const size_t elements = mul(BTK, static_cast<size_t>(V), "batch size overflow");
+
+    std::lock_guard<std::mutex> lock(h->run_mutex);
+    const hipStream_t st = stream_of(h);
+    const void* x = upload(h, kInputs, static_cast<const unsigned char*>(j.inputs), elements * dtype_bytes(j.data_type),
+                           st);
+    DBSCudaDecodeArgs a{};
+    a.batch_size = B;
+    a.steps = T;
+    a.beam_size = K;
+    a.vocab_size = V;
+    a.eos_token = h->eos_token;
+    a.min_length = j.min_length;
+    a.length_penalty_alpha = h->alpha;
+    a.no_repeat_ngram_size = j.ngram;
+    a.repetition_penalty = j.repetition_penalty;
+    a.steps_per_example = upload(h, kSteps, j.steps, static_cast<size_t>(B), st);
+    a.beam_sizes_per_example = upload(h, kBeams, j.beams, static_cast<size_t>(B), st);
+    a.eos_tokens_per_example = upload(h, kEos, j.eos, static_cast<size_t>(B), st);
+    a.min_lengths_per_example = upload(h, kMinLengths, j.min_lengths, static_cast<size_t>(B), st);
+    a.banned_tokens = upload(h, kBanned, j.banned, static_cast<size_t>(V), st);
+    const uint8_t* banned_pe = upload(h, kBannedPe, j.banned_pe, mul(static_cast<size_t>(B), V, "banned size"), st);
+    DBSCudaSearchOptions opts{};
+    opts.extra_eos_count = static_cast<int>(h->extra_eos.size());
+    for (size_t i = 0; i < h->extra_eos.size(); ++i) opts.extra_eos_tokens[i] = h->extra_eos[i];
+
+    DBSCudaDecodeOutputs o{};
+    o.final_scores = device_out(h, kFinalScores, j.final_scores, BK);
+    o.final_raw_scores = device_out(h, kFinalRaw, j.final_raw, BK);
+    o.final_lengths = device_out(h, kFinalLengths, j.final_lengths, BK);
+    o.tokens = device_out(h, kTokens, j.tokens, BTK);
+    o.parents = device_out(h, kParents, j.parents, BTK);
+    o.lengths = device_out(h, kLengths, j.lengths, BTK);
+    o.scores = device_out(h, kScores, j.scores, BTK);
+    o.raw_scores = device_out(h, kRawScores, j.raw_scores, BTK);
+    o.from_logprob = device_out(h, kFromLogprob, j.from_logprob, BTK);
+    float* row_lse = device_out(h, kRowLse, j.row_lse, BTK);
+    int32_t* first_invalid =
+        h->validate ? static_cast<int32_t*>(h->arena.get(kFirstInvalid, sizeof(int32_t) * static_cast<size_t>(B)))
+                    : nullptr;
+    const int64_t ws_bytes = dbs_cuda_decode_workspace_size(&a);
+    need(ws_bytes > 0, "invalid decode arguments");
+    void* ws = h->arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
+    int32_t* fault = nullptr;
+    engine_check(dbs_hip::decode_for_host(x, j.data_type, j.from_logits ? 1 : 0, &a, &opts, banned_pe, &o, row_lse,
+                                          first_invalid, ws, ws_bytes, st, &fault),
+                 "HIP decode");
+    int32_t gave_up = 0;
+    if (fault) download(&gave_up, fault, 1, st);
+    std::vector<int32_t> bad;
+    if (first_invalid) {
+        bad.resize(static_cast<size_t>(B));
+        download(bad.data(), first_invalid, bad.size(), st);
+    }
+    download(j.final_scores, o.final_scores, BK, st);
+    download(j.final_raw, o.final_raw_scores, BK, st);
+    download(j.final_lengths, o.final_lengths, BK, st);
+    download(j.tokens, o.tokens, BTK, st);
+    download(j.parents, o.parents, BTK, st);
+    download(j.lengths, o.lengths, BTK, st);
+    download(j.scores, o.scores, BTK, st);
+    download(j.raw_scores, o.raw_scores, BTK, st);
+    download(j.from_logprob, o.from_logprob, BTK, st);
+    download(j.row_lse, row_lse, BTK, st);
+    hip_check(hipStreamSynchronize(st), "HIP decode");
+    // the overlapped select pass gave up waiting for rows of the row pass
+    // (bounded at 2 s; only when something starves or serialises the
+    // kernels): the traces of those examples are padding
+    if (gave_up != 0)
+        throw std::runtime_error(
+            "HIP decode: the select pass gave up waiting for the row pass (the GPU was starved or its kernels were "
+            "serialised); the trace is incomplete");
+    // validate_inputs: the first example whose search read a NaN/+inf row,
+    // reported at that row (reference src/decoder.cpp:143-171)
+    for (int b = 0; b < static_cast<int>(bad.size()); ++b) {
+        if (bad[static_cast<size_t>(b)] < 0) continue;
+        const int t = bad[static_cast<size_t>(b)] / K, k = bad[static_cast<size_t>(b)] % K;
+        const std::string what = std::string(j.from_logits ? "logits contain NaN or +inf"
+                                                            : "log_probs contains NaN or +inf") +
+                                 " (step " + std::to_string(t) + ", beam " + std::to_string(k) + ")";
+        if (j.batch_errors) example_error(b, what);
+        throw std::invalid_argument(what);
+    }
+}
+
+void check_trace(int B, int T, int K, int V, const std::vector<int32_t>& steps_b, const int32_t* parents,
+                 const int32_t* tokens, const int32_t* lengths) {
+    for (int b = 0; b < B; ++b) {
+        const size_t base = static_cast<size_t>(b) * T * K;
+        const size_t n = static_cast<size_t>(steps_b[static_cast<size_t>(b)]) * K;
+        for (size_t i = base; i < base + n; ++i) {
+            if (parents[i] < -1 || parents[i] >= K || tokens[i] < -1 || tokens[i] >= V || lengths[i] < 0)
+                example_error(b, "decode trace is out of range (parents, tokens or lengths)");
+        }
+    }
+}
+
+namespace {
+
+DBSCudaDecodeArgs trace_args(int B, int T, int K, int V, float alpha) {
+    DBSCudaDecodeArgs a{};
+    a.batch_size = B;
+    a.steps = T;
+    a.beam_size = K;
+    a.vocab_size = V;
+    a.eos_token = -1;
+    a.length_penalty_alpha = alpha;
+    a.repetition_penalty = 1.0f;
+    return a;
+}
+
+}  // namespace
+
+std::vector<float> path_draws(DBSDecoderHandle* h, int B, int T, int K, int V, float alpha,
+                              const int32_t* steps_per_example, const int32_t* parents, const int32_t* tokens,
+                              const int32_t* lengths, const uint8_t* from_logprob, const Grads& g) {
+    check_engine_limits(h, K, V);
+    const size_t BK = static_cast<size_t>(B) * K, BTK = BK * static_cast<size_t>(T);
+    std::lock_guard<std::mutex> lock(h->run_mutex);
+    const hipStream_t st = stream_of(h);
+    DBSCudaDecodeArgs a = trace_args(B, T, K, V, alpha);
+    a.steps_per_example = upload(h, kSteps, steps_per_example, static_cast<size_t>(B), st);
+    DBSCudaBackwardInputs in{};
+    in.parents = upload(h, kParents, parents, BTK, st);
+    in.tokens = upload(h, kTokens, tokens, BTK, st);
+    in.lengths = upload(h, kLengths, lengths, BTK, st);
+    in.from_logprob = upload(h, kFromLogprob, from_logprob, BTK, st);
+    in.grad_final_scores = upload(h, kGradFinal, g.final_scores, BK, st);
+    in.grad_final_raw_scores = upload(h, kGradFinalRaw, g.final_raw, BK, st);
+    in.grad_scores = upload(h, kGradScores, g.scores, BTK, st);
+    in.grad_raw_scores = upload(h, kGradRaw, g.raw, BTK, st);
+    float* draws_d = static_cast<float*>(h->arena.get(kDraws, sizeof(float) * BTK));
+    engine_check(dbs_hip::path_draws_for_host(&a, &in, draws_d, st), "HIP path gradient");
+    std::vector<float> draws(BTK);
+    download(draws.data(), draws_d, BTK, st);
+    hip_check(hipStreamSynchronize(st), "HIP path gradient");
+    return draws;
+}
+
+void stats_decode(DBSDecoderHandle* h, int64_t elapsed_ns, int64_t selected, int64_t pool, int64_t logprobs,
+                  int64_t allocation_bytes, bool model_step) {
+    std::lock_guard<std::mutex> lock(h->stats_mutex);
+    h->stats.abi_version = DBS_ABI_VERSION;
+    h->stats.last_kernel = kKernelHip;
+    h->stats.used_batch_threads = 1;
+    h->stats.used_model_step_callback = model_step ? 1 : 0;
+    h->stats.last_decode_ns = elapsed_ns;
+    h->stats.last_selected_count = selected;
+    h->stats.last_pool_count = pool;
+    h->stats.last_logprob_count = logprobs;
+    h->stats.last_allocation_bytes = allocation_bytes;
+    h->stats.last_error_category = 0;
+}
+
+void stats_backward(DBSDecoderHandle* h, int64_t elapsed_ns, bool sparse, int64_t sparse_count) {
+    std::lock_guard<std::mutex> lock(h->stats_mutex);
+    h->stats.abi_version = DBS_ABI_VERSION;
+    h->stats.used_sparse_backward = sparse ? 1 : 0;
+    h->stats.used_dense_backward = sparse ? 0 : 1;
+    h->stats.last_backward_ns = elapsed_ns;
+    h->stats.last_sparse_grad_count = sparse_count;
+    h->stats.last_error_category = 0;
+}
+
+namespace {
+
+int64_t ns_since(std::chrono::steady_clock::time_point start) {
+    return std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - start).count();
 }
 
 // dbs_decode_batch_into(_ex) (reference src/c_api.cpp:703-800); ex may be null.
@@ -246,10 +342,11 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
              "reserved fields must be NULL");
         need(!pool || h->pool_multiplier > 0, "pool outputs need a relaxed pool: set relaxed_pool_multiplier >= 1");
     }
+    const auto start = std::chrono::steady_clock::now();
     const int K = h->beam_size;
     const size_t trace = mul(static_cast<size_t>(T), static_cast<size_t>(K), "batch stride overflow");
     const size_t per_example = mul(trace, static_cast<size_t>(V), "batch stride overflow");
-    const size_t elements = mul(per_example, static_cast<size_t>(B), "batch size overflow");
+    (void)mul(per_example, static_cast<size_t>(B), "batch size overflow");
     (void)mul(per_example, dtype_bytes(data_type), "batch stride overflow");
     const std::vector<int32_t> steps_b = steps_of(steps_per_example, B, T);
 
@@ -271,108 +368,50 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
     need(!(cons && cons->forced_tokens), "forced_tokens are not served by libdbs_hip (the HIP engine)");
     need(!(cons && cons->token_filter), "token_filter callbacks are not served by libdbs_hip (the HIP engine)");
     need(!pool, "relaxed-pool outputs are not served by libdbs_hip (the HIP engine)");
-    check_engine_limits(h, V);
 
-    std::lock_guard<std::mutex> lock(h->run_mutex);
-    const hipStream_t st = stream_of(h);
-    const size_t BK = static_cast<size_t>(B) * K, BTK = static_cast<size_t>(B) * trace;
-    const void* x = upload(h, kInputs, static_cast<const unsigned char*>(inputs), elements * dtype_bytes(data_type), st);
-    const uint8_t* banned = cons ? upload(h, kBanned, cons->banned_tokens, static_cast<size_t>(V), st) : nullptr;
-    const int32_t* steps_d = upload(h, kSteps, steps_per_example, static_cast<size_t>(B), st);
-
-    DBSCudaDecodeOutputs o{};
-    o.final_scores = device_out(h, kFinalScores, out->final_scores, BK);
-    o.final_raw_scores = device_out(h, kFinalRaw, out->final_raw_scores, BK);
-    o.final_lengths = device_out(h, kFinalLengths, out->final_lengths, BK);
-    o.tokens = device_out(h, kTokens, out->tokens, BTK);
-    o.parents = device_out(h, kParents, out->parents, BTK);
-    o.lengths = device_out(h, kLengths, out->lengths, BTK);
-    o.scores = device_out(h, kScores, out->scores, BTK);
-    o.raw_scores = device_out(h, kRawScores, out->raw_scores, BTK);
-    o.from_logprob = device_out(h, kFromLogprob, out->from_logprob, BTK);
-    float* row_lse = ex ? device_out(h, kRowLse, ex->row_lse, BTK) : nullptr;
-    int32_t* first_invalid =
-        h->validate ? static_cast<int32_t*>(h->arena.get(kFirstInvalid, sizeof(int32_t) * static_cast<size_t>(B)))
-                    : nullptr;
-
-    DBSCudaDecodeArgs a{};
-    a.batch_size = B;
-    a.steps = T;
-    a.beam_size = K;
-    a.vocab_size = V;
-    a.eos_token = h->eos_token;
-    a.min_length = min_length;
-    a.length_penalty_alpha = h->alpha;
-    a.no_repeat_ngram_size = cons && cons->no_repeat_ngram_size > 0 ? cons->no_repeat_ngram_size : 0;
-    a.repetition_penalty = rep;
-    a.steps_per_example = steps_d;
-    a.banned_tokens = banned;
-    DBSCudaSearchOptions opts{};
-    opts.extra_eos_count = static_cast<int>(h->extra_eos.size());
-    for (size_t i = 0; i < h->extra_eos.size(); ++i) opts.extra_eos_tokens[i] = h->extra_eos[i];
-    const int64_t ws_bytes = dbs_cuda_decode_workspace_size(&a);
-    need(ws_bytes > 0, "invalid decode arguments");
-    void* ws = h->arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
-    int32_t* fault = nullptr;
-    engine_check(dbs_hip::decode_for_host(x, data_type, from_logits ? 1 : 0, &a, &opts, &o, row_lse, first_invalid,
-                                          ws, ws_bytes, st, &fault),
-                 "HIP decode");
-    int32_t gave_up = 0;
-    if (fault) download(&gave_up, fault, 1, st);
-
-    std::vector<int32_t> bad;
-    if (first_invalid) {
-        bad.resize(static_cast<size_t>(B));
-        download(bad.data(), first_invalid, bad.size(), st);
-    }
-    download(out->final_scores, o.final_scores, BK, st);
-    download(out->final_raw_scores, o.final_raw_scores, BK, st);
-    download(out->final_lengths, o.final_lengths, BK, st);
-    download(out->tokens, o.tokens, BTK, st);
-    download(out->parents, o.parents, BTK, st);
-    download(out->lengths, o.lengths, BTK, st);
-    download(out->scores, o.scores, BTK, st);
-    download(out->raw_scores, o.raw_scores, BTK, st);
-    download(out->from_logprob, o.from_logprob, BTK, st);
-    if (ex) download(ex->row_lse, row_lse, BTK, st);
-    hip_check(hipStreamSynchronize(st), "HIP decode");
-    // the overlapped select pass gave up waiting for rows of the row pass
-    // (bounded at 2 s; only when something starves or serialises the
-    // kernels): the traces of those examples are padding
-    if (gave_up != 0)
-        throw std::runtime_error(
-            "HIP decode: the select pass gave up waiting for the row pass (the GPU was starved or its kernels were "
-            "serialised); the trace is incomplete");
-    // validate_inputs: the first example whose search read a NaN/+inf row,
-    // reported at that row (reference src/decoder.cpp:143-171)
-    for (int b = 0; b < static_cast<int>(bad.size()); ++b) {
-        if (bad[static_cast<size_t>(b)] < 0) continue;
-        const int t = bad[static_cast<size_t>(b)] / K, k = bad[static_cast<size_t>(b)] % K;
-        example_error(b, std::string(from_logits ? "logits contain NaN or +inf" : "log_probs contains NaN or +inf") +
-                             " (step " + std::to_string(t) + ", beam " + std::to_string(k) + ")");
+    DecodeJob j;
+    j.inputs = inputs;
+    j.data_type = data_type;
+    j.from_logits = from_logits;
+    j.B = B;
+    j.T = T;
+    j.K = K;
+    j.V = V;
+    j.steps = steps_per_example;
+    j.banned = cons ? cons->banned_tokens : nullptr;
+    j.min_length = min_length;
+    j.ngram = cons && cons->no_repeat_ngram_size > 0 ? cons->no_repeat_ngram_size : 0;
+    j.repetition_penalty = rep;
+    j.final_scores = out->final_scores;
+    j.final_raw = out->final_raw_scores;
+    j.final_lengths = out->final_lengths;
+    j.tokens = out->tokens;
+    j.parents = out->parents;
+    j.lengths = out->lengths;
+    j.scores = out->scores;
+    j.raw_scores = out->raw_scores;
+    j.from_logprob = out->from_logprob;
+    j.row_lse = ex ? ex->row_lse : nullptr;
+    run_decode(h, j);
+    const int64_t selected = static_cast<int64_t>(B) * static_cast<int64_t>(trace);
+    {
+        std::lock_guard<std::mutex> lock(h->stats_mutex);
+        h->stats.abi_version = DBS_ABI_VERSION;
+        h->stats.last_kernel = kKernelHip;
+        h->stats.used_batch_threads = 1;
+        h->stats.used_model_step_callback = 0;
+        h->stats.last_decode_ns = ns_since(start);
+        h->stats.last_selected_count = selected;
+        h->stats.last_pool_count = 0;
+        h->stats.last_logprob_count = selected * V;
+        h->stats.last_allocation_bytes = 0;
+        h->stats.last_error_category = 0;
     }
 }
 
-// The checks of a trace handed to a backward (reference src/decoder.cpp:
-// 947-963): indexes in range over each example's own steps.
-void check_trace(int B, int T, int K, int V, const std::vector<int32_t>& steps_b, const int32_t* parents,
-                 const int32_t* tokens, const int32_t* lengths) {
-    for (int b = 0; b < B; ++b) {
-        const size_t base = static_cast<size_t>(b) * T * K;
-        const size_t n = static_cast<size_t>(steps_b[static_cast<size_t>(b)]) * K;
-        for (size_t i = base; i < base + n; ++i) {
-            if (parents[i] < -1 || parents[i] >= K || tokens[i] < -1 || tokens[i] >= V || lengths[i] < 0)
-                example_error(b, "decode trace is out of range (parents, tokens or lengths)");
-        }
-    }
-}
-
-struct Grads {
-    const float* final_scores = nullptr;
-    const float* final_raw = nullptr;
-    const float* scores = nullptr;
-    const float* raw = nullptr;
-};
+// Device buffers a chunk of examples of the from-logits backward may take:
+// the logits and a float32 gradient of its rows.
+constexpr size_t kBackwardChunkBytes = size_t{1} << 30;
 
 // The backward of a batch into the host buffer grad [B, T, K, V] (+=): the
 // per-slot path gradients from the device, then the entries they name, or
@@ -381,40 +420,16 @@ struct Grads {
 void backward_batch(DBSDecoderHandle* h, int B, int T, int V, const int32_t* steps_per_example,
                     const int32_t* parents, const int32_t* tokens, const int32_t* lengths, const uint8_t* flp,
                     const Grads& g, const void* logits, int logits_type, const float* row_lse, float* grad) {
+    const auto start = std::chrono::steady_clock::now();
     const int K = h->beam_size;
     const size_t trace = mul(static_cast<size_t>(T), static_cast<size_t>(K), "batch stride overflow");
     const size_t row_block = mul(trace, static_cast<size_t>(V), "batch stride overflow");
     (void)mul(row_block, static_cast<size_t>(B), "batch size overflow");
     const std::vector<int32_t> steps_b = steps_of(steps_per_example, B, T);
     check_trace(B, T, K, V, steps_b, parents, tokens, lengths);
-    check_engine_limits(h, V);
-
-    std::lock_guard<std::mutex> lock(h->run_mutex);
-    const hipStream_t st = stream_of(h);
-    const size_t BK = static_cast<size_t>(B) * K, BTK = static_cast<size_t>(B) * trace;
-    DBSCudaDecodeArgs a{};
-    a.batch_size = B;
-    a.steps = T;
-    a.beam_size = K;
-    a.vocab_size = V;
-    a.eos_token = -1;
-    a.length_penalty_alpha = h->alpha;
-    a.repetition_penalty = 1.0f;
-    a.steps_per_example = upload(h, kSteps, steps_per_example, static_cast<size_t>(B), st);
-    DBSCudaBackwardInputs in{};
-    in.parents = upload(h, kParents, parents, BTK, st);
-    in.tokens = upload(h, kTokens, tokens, BTK, st);
-    in.lengths = upload(h, kLengths, lengths, BTK, st);
-    in.from_logprob = upload(h, kFromLogprob, flp, BTK, st);
-    in.grad_final_scores = upload(h, kGradFinal, g.final_scores, BK, st);
-    in.grad_final_raw_scores = upload(h, kGradFinalRaw, g.final_raw, BK, st);
-    in.grad_scores = upload(h, kGradScores, g.scores, BTK, st);
-    in.grad_raw_scores = upload(h, kGradRaw, g.raw, BTK, st);
-    float* draws_d = static_cast<float*>(h->arena.get(kDraws, sizeof(float) * BTK));
-    engine_check(dbs_hip::path_draws_for_host(&a, &in, draws_d, st), "HIP path gradient");
-    std::vector<float> draws(BTK);
-    download(draws.data(), draws_d, BTK, st);
-    hip_check(hipStreamSynchronize(st), "HIP path gradient");
+    const std::vector<float> draws =
+        path_draws(h, B, T, K, V, h->alpha, steps_per_example, parents, tokens, lengths, flp, g);
+    const size_t BTK = static_cast<size_t>(B) * trace;
 
     // (b, t, parent) row and token of every slot with an entry: distinct
     // slots of one step select distinct (parent, token) pairs, so each entry
@@ -432,40 +447,73 @@ void backward_batch(DBSDecoderHandle* h, int B, int T, int V, const int32_t* ste
             int token = 0;
             if (entry_of(i, row, token)) grad[row * static_cast<size_t>(V) + static_cast<size_t>(token)] += draws[i];
         }
-        return;
+    } else {
+        // From logits: the device writes each gradient row (g - softmax(row) *
+        // sum(g), entries summed in token order; zero rows elsewhere), a
+        // chunk of examples at a time, and the rows with an entry are added
+        // here in full (reference src/decoder.hpp:212-242).
+        const size_t example_bytes = mul(row_block, dtype_bytes(logits_type) + sizeof(float), "batch stride overflow");
+        const int chunk = static_cast<int>(std::max<size_t>(1, std::min<size_t>(B, kBackwardChunkBytes / example_bytes)));
+        std::lock_guard<std::mutex> lock(h->run_mutex);
+        const hipStream_t st = stream_of(h);
+        for (int b0 = 0; b0 < B; b0 += chunk) {
+            const int nb = std::min(chunk, B - b0);
+            const size_t off = static_cast<size_t>(b0) * trace;  // first [b, t, k] slot of the chunk
+            std::vector<size_t> rows;
+            for (size_t i = off; i < off + static_cast<size_t>(nb) * trace; ++i) {
+                size_t row = 0;
+                int token = 0;
+                if (entry_of(i, row, token)) rows.push_back(row);
+            }
+            if (rows.empty()) continue;
+            std::sort(rows.begin(), rows.end());
+            rows.erase(std::unique(rows.begin(), rows.end()), rows.end());
+            const size_t nslots = static_cast<size_t>(nb) * trace;
+            DBSCudaDecodeArgs a = trace_args(nb, T, K, V, h->alpha);
+            a.steps_per_example = upload(h, kSteps, steps_per_example ? steps_per_example + b0 : nullptr,
+                                         static_cast<size_t>(nb), st);
+            DBSCudaBackwardInputs in{};
+            in.parents = upload(h, kParents, parents + off, nslots, st);
+            in.tokens = upload(h, kTokens, tokens + off, nslots, st);
+            in.lengths = upload(h, kLengths, lengths + off, nslots, st);
+            in.from_logprob = upload(h, kFromLogprob, flp + off, nslots, st);
+            const size_t fin = static_cast<size_t>(b0) * K, nfin = static_cast<size_t>(nb) * K;
+            in.grad_final_scores = upload(h, kGradFinal, g.final_scores ? g.final_scores + fin : nullptr, nfin, st);
+            in.grad_final_raw_scores = upload(h, kGradFinalRaw, g.final_raw ? g.final_raw + fin : nullptr, nfin, st);
+            in.grad_scores = upload(h, kGradScores, g.scores ? g.scores + off : nullptr, nslots, st);
+            in.grad_raw_scores = upload(h, kGradRaw, g.raw ? g.raw + off : nullptr, nslots, st);
+            in.logits = upload(h, kInputs, static_cast<const unsigned char*>(logits) + off * V * dtype_bytes(logits_type),
+                               nslots * V * dtype_bytes(logits_type), st);
+            in.logits_type = logits_type;
+            in.row_lse = upload(h, kRowLse, row_lse + off, nslots, st);
+            float* dense = static_cast<float*>(h->arena.get(kDense, sizeof(float) * nslots * static_cast<size_t>(V)));
+            const int64_t ws_bytes = dbs_cuda_backward_workspace_size(&a);
+            need(ws_bytes > 0, "invalid backward arguments");
+            void* ws = h->arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
+            engine_check(dbs_hip_backward_dense(&a, &in, dense, DBS_HIP_GRAD_F32, ws, ws_bytes, st), "HIP backward");
+            std::vector<float> buf(rows.size() * static_cast<size_t>(V));
+            for (size_t r = 0; r < rows.size(); ++r)
+                download(buf.data() + r * V, dense + (rows[r] - off) * V, static_cast<size_t>(V), st);
+            hip_check(hipStreamSynchronize(st), "HIP backward");
+            for (size_t r = 0; r < rows.size(); ++r) {
+                float* dst = grad + rows[r] * static_cast<size_t>(V);
+                const float* src = buf.data() + r * static_cast<size_t>(V);
+                for (int v = 0; v < V; ++v) dst[v] += src[v];
+            }
+        }
     }
-    // From logits: the device writes each gradient row (g - softmax(row) *
-    // sum(g), entries summed in token order; zero rows elsewhere), and the
-    // rows with an entry are added here in full (reference
-    // src/decoder.hpp:212-242).
-    in.logits = upload(h, kInputs, static_cast<const unsigned char*>(logits), BTK * V * dtype_bytes(logits_type), st);
-    in.logits_type = logits_type;
-    in.row_lse = upload(h, kRowLse, row_lse, BTK, st);
-    float* dense = static_cast<float*>(h->arena.get(kDense, sizeof(float) * BTK * static_cast<size_t>(V)));
-    const int64_t ws_bytes = dbs_cuda_backward_workspace_size(&a);
-    need(ws_bytes > 0, "invalid backward arguments");
-    void* ws = h->arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
-    engine_check(dbs_hip_backward_dense(&a, &in, dense, DBS_HIP_GRAD_F32, ws, ws_bytes, st), "HIP backward");
-    std::vector<size_t> rows;
-    for (size_t i = 0; i < BTK; ++i) {
-        size_t row = 0;
-        int token = 0;
-        if (entry_of(i, row, token)) rows.push_back(row);
-    }
-    std::sort(rows.begin(), rows.end());
-    rows.erase(std::unique(rows.begin(), rows.end()), rows.end());
-    std::vector<float> buf(rows.size() * static_cast<size_t>(V));
-    for (size_t j = 0; j < rows.size(); ++j)
-        download(buf.data() + j * V, dense + rows[j] * V, static_cast<size_t>(V), st);
-    hip_check(hipStreamSynchronize(st), "HIP backward");
-    for (size_t j = 0; j < rows.size(); ++j) {
-        float* dst = grad + rows[j] * static_cast<size_t>(V);
-        const float* src = buf.data() + j * static_cast<size_t>(V);
-        for (int v = 0; v < V; ++v) dst[v] += src[v];
-    }
+    std::lock_guard<std::mutex> lock(h->stats_mutex);
+    h->stats.used_sparse_backward = 0;
+    h->stats.used_dense_backward = 1;
+    h->stats.last_backward_ns = ns_since(start);
+    h->stats.last_sparse_grad_count = 0;
+    h->stats.last_error_category = 0;
 }
 
 }  // namespace
+}  // namespace dbs_host
+
+using namespace dbs_host;
 
 extern "C" {
 
@@ -473,7 +521,7 @@ DBS_EXPORT int dbs_abi_version(void) { return DBS_ABI_VERSION; }
 
 DBS_EXPORT const char* dbs_version_string(void) { return "2.3.0"; }
 
-DBS_EXPORT const char* dbs_last_global_error(void) { return t_error.c_str(); }
+DBS_EXPORT const char* dbs_last_global_error(void) { return last_thread_error(); }
 
 DBS_EXPORT const char* dbs_selected_kernel_name(void) { return "hip-gfx950"; }
 
@@ -505,6 +553,13 @@ DBS_EXPORT int dbs_create_ex(DBSOptionsC o, DBSDecoderHandle** out_handle) {
         h->min_length = o.min_length;
         h->validate = o.validate_inputs != 0 ? 1 : 0;
         h->pool_multiplier = o.relaxed_pool_multiplier;
+        if (o.selected_temperature > 0.0f) h->selected_temperature = o.selected_temperature;
+        if (o.soft_topk_temperature > 0.0f) h->soft_topk_temperature = o.soft_topk_temperature;
+        if (o.soft_topk_tolerance > 0.0f) h->soft_topk_tolerance = o.soft_topk_tolerance;
+        if (o.soft_topk_max_iters > 0) h->soft_topk_max_iters = o.soft_topk_max_iters;
+        if (o.max_dense_gradient_elements > 0) h->max_dense_gradient_elements = o.max_dense_gradient_elements;
+        h->stats.abi_version = DBS_ABI_VERSION;
+        h->stats.last_kernel = kKernelHip;
         *out_handle = h;
     });
 }

@@ -13,14 +13,15 @@
 
 namespace dbs_hip {
 
-// dbs_cuda_decode_ex2, plus first_invalid (device int32 [B] or null): the
-// first row holding NaN or +inf that example b's search read, t * K + k in
-// reading order, or -1; and *fault, as dbs_hip_decode_ex4's fault word (the
-// workspace is the caller's). Returns a DBS_CUDA_STATUS_*.
+// dbs_hip_decode_ex3 (per-example banned masks [B, V] or null), plus
+// first_invalid (device int32 [B] or null): the first row holding NaN or
+// +inf that example b's search read, t * K + k in reading order, or -1; and
+// *fault, as dbs_hip_decode_ex4's fault word (the workspace is the
+// caller's). Returns a DBS_CUDA_STATUS_*.
 int decode_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
-                    const DBSCudaSearchOptions* options, const DBSCudaDecodeOutputs* outputs, float* row_lse,
-                    int32_t* first_invalid, void* workspace, int64_t workspace_bytes, hipStream_t stream,
-                    int32_t** fault);
+                    const DBSCudaSearchOptions* options, const uint8_t* banned_per_example,
+                    const DBSCudaDecodeOutputs* outputs, float* row_lse, int32_t* first_invalid, void* workspace,
+                    int64_t workspace_bytes, hipStream_t stream, int32_t** fault);
 
 // The per-slot path gradients draws [B, T, K] of the surrogate backward for
 // every gradient input of `in` (final scores, final raw scores, scores, raw

@@ -20,9 +20,12 @@
  *   - A decoder handle may be shared between threads; calls on one handle run
  *     one at a time on the GPU.
  *
- * Only what the batch entry points need is declared here; the reference's
- * result handles, sparse backward, statistics, model-step callbacks, token
- * filters, forced tokens and relaxed pool are not served by this library.
+ * All 81 functions of the reference's ABI are exported. What the GPU engine
+ * does not serve is refused with DBS_ERROR_INVALID_ARGUMENT and a message
+ * naming it: the relaxed pool (relaxed_pool_multiplier > 0 and the pool
+ * outputs and gradients), forced tokens (a forced_tokens entry >= 0) and
+ * token-filter callbacks. Result handles therefore have no pool
+ * (dbs_result_pool_size 0, pool accessors NULL).
  */
 #pragma once
 
@@ -55,7 +58,7 @@ extern "C" {
 typedef struct DBSOptionsC {
     int beam_size;                       /* K [8] */
     int eos_token;                       /* -1: no EOS handling */
-    float selected_temperature;          /* [1.0] (selected-beam weights: not served) */
+    float selected_temperature;          /* softmax temperature of the selected-beam weights [1.0] */
     float soft_topk_temperature;         /* [0.25] (relaxed pool: not served) */
     int relaxed_pool_multiplier;         /* [0] (relaxed pool: not served) */
     int vocab_block;                     /* ignored */
@@ -64,12 +67,53 @@ typedef struct DBSOptionsC {
     int soft_topk_max_iters;             /* [48] (relaxed pool: not served) */
     int min_length;                      /* EOS masked below this length [0] */
     int validate_inputs;                 /* non-zero: NaN/+inf in a row the search reads is an error */
-    int64_t max_dense_gradient_elements; /* [1e8] (dense single-example backward: not served) */
+    int64_t max_dense_gradient_elements; /* cap on T*K*V for dbs_backward_dense() [1e8] */
     int reserved0;
     int reserved1;
 } DBSOptionsC;
 
 typedef struct DBSDecoderHandle DBSDecoderHandle;
+typedef struct DBSResultHandle DBSResultHandle;
+typedef struct DBSBackwardHandle DBSBackwardHandle;
+typedef struct DBSBatchResultHandle DBSBatchResultHandle;
+typedef struct DBSWorkspaceHandle DBSWorkspaceHandle;
+
+/* Model-step callback of dbs_decode_model_steps (reference include/dbs.h:
+ * 87-101): fills out_log_probs [K, V] for `step` from the tokens the beams
+ * emitted at step - 1 and their length-penalised scores (-1 and 0 at step
+ * 0); 0 on success. */
+typedef int (*DBSModelStepFn)(
+    void* user_data,
+    int batch_index,
+    int step,
+    const int32_t* prev_tokens,
+    const float* prev_scores,
+    int beam_size,
+    int vocab_size,
+    float* out_log_probs);
+
+/* The beams entering a model step (reference include/dbs.h:103-121): slot k
+ * is the k-th best hypothesis after step - 1; parents[k] the slot it
+ * extends. Pointers are valid during the callback only. */
+typedef struct DBSModelStepInfoC {
+    int batch_index;
+    int step;
+    int beam_size;
+    int vocab_size;
+    const int32_t* parents;       /* [K] (-1 at step 0 and for dead slots) */
+    const int32_t* tokens;        /* [K] token emitted at step - 1 (-1 at step 0) */
+    const int32_t* lengths;       /* [K] */
+    const float* scores;          /* [K] length-penalised scores */
+    const float* raw_scores;      /* [K] cumulative log-probabilities */
+    const uint8_t* finished;      /* [K] non-zero once the beam emitted EOS (its row is not read) */
+    const int32_t* prefixes;      /* [K * step] the tokens of each beam's path */
+    const void* reserved[4];
+} DBSModelStepInfoC;
+
+/* Fills out_log_probs [K, V] (pre-filled with -inf) for the beams `info`
+ * describes; any non-zero return aborts the decode with DBS_ERROR_RUNTIME
+ * (reference include/dbs.h:123-127). */
+typedef int (*DBSModelStepExFn)(void* user_data, const DBSModelStepInfoC* info, float* out_log_probs);
 
 /* Token filter callback of the reference (reference include/dbs.h:129-137).
  * Declared for the layout of DBSAdvancedConstraintsC; a non-NULL filter is
@@ -111,6 +155,30 @@ typedef struct DBSDecodeOutputsC {
     float* raw_scores;                   /* [B, T, K] cumulative log-probabilities */
     uint8_t* from_logprob;               /* [B, T, K] 0 for EOS carry-forward and padding slots */
 } DBSDecodeOutputsC;
+
+/* Per-handle statistics (reference include/dbs.h:165-184). last_kernel is 5
+ * here (the GPU engine; the reference's 0-4 name its CPU paths); the
+ * allocator totals count the device buffers this library's handles hold. */
+typedef struct DBSStatsC {
+    int abi_version;
+    int last_kernel;
+    int used_sparse_backward;
+    int used_dense_backward;
+    int used_batch_threads;
+    int used_model_step_callback;
+    int last_error_category;           /* 0 none, 1 invalid argument, 2 runtime, 3 allocation, 4 overflow */
+    int64_t last_decode_ns;
+    int64_t last_backward_ns;
+    int64_t last_allocation_bytes;
+    int64_t last_selected_count;
+    int64_t last_pool_count;
+    int64_t last_logprob_count;
+    int64_t last_sparse_grad_count;
+    int64_t total_allocator_calls;
+    int64_t total_allocator_bytes;
+    int64_t reserved_stats0;
+    int64_t reserved_stats1;
+} DBSStatsC;
 
 /* Element types (reference include/dbs.h:186-190). */
 typedef enum DBSDataTypeC {
@@ -237,6 +305,227 @@ DBS_EXPORT int dbs_backward_batch_into_ex(
 /* Name of the compute path ("hip-gfx950"; the reference names its CPU
  * kernel, reference include/dbs.h:527). */
 DBS_EXPORT const char* dbs_selected_kernel_name(void);
+
+/* ---- Workspaces (reference include/dbs.h:196-199): the host row buffer of
+ * the model-step decodes. ---- */
+DBS_EXPORT int dbs_workspace_create(DBSWorkspaceHandle** out_workspace);
+DBS_EXPORT void dbs_workspace_destroy(DBSWorkspaceHandle* workspace);
+DBS_EXPORT int dbs_workspace_reserve(DBSWorkspaceHandle* workspace, int64_t float_count, int64_t int_count);
+DBS_EXPORT int64_t dbs_workspace_allocated_bytes(DBSWorkspaceHandle* workspace);
+
+/* ---- Decodes of log-probabilities into result handles (reference
+ * include/dbs.h:215-299, 412-437). One example: log_probs [T, K, V]; a
+ * batch: [B, T, K, V]; dbs_decode_batch_variable: [B, max_steps,
+ * max_beam_size, V] with per-example steps, beam sizes, EOS tokens, minimum
+ * lengths and banned masks [B, V] (forced_tokens_per_example [B, max_steps]
+ * must hold no entry >= 0). Each result holds the trace, the selected-beam
+ * softmax weights of every step and the final scores. num_threads is
+ * accepted and ignored (the GPU decodes every example at once). ---- */
+DBS_EXPORT int dbs_decode(
+    DBSDecoderHandle* handle,
+    const float* log_probs,
+    int steps,
+    int vocab_size,
+    DBSResultHandle** out_result);
+
+DBS_EXPORT int dbs_decode_typed(
+    DBSDecoderHandle* handle,
+    const void* log_probs,
+    int data_type,
+    int steps,
+    int vocab_size,
+    DBSResultHandle** out_result);
+
+DBS_EXPORT int dbs_decode_batch_typed(
+    DBSDecoderHandle* handle,
+    const void* log_probs,
+    int data_type,
+    int batch_size,
+    int steps,
+    int vocab_size,
+    int num_threads,
+    DBSBatchResultHandle** out_result);
+
+DBS_EXPORT int dbs_decode_constrained(
+    DBSDecoderHandle* handle,
+    const float* log_probs,
+    int steps,
+    int vocab_size,
+    const uint8_t* banned_tokens,
+    const int32_t* forced_tokens,
+    int min_length,
+    DBSResultHandle** out_result);
+
+DBS_EXPORT int dbs_decode_constrained_ex(
+    DBSDecoderHandle* handle,
+    const float* log_probs,
+    int steps,
+    int vocab_size,
+    const DBSAdvancedConstraintsC* constraints,
+    DBSResultHandle** out_result);
+
+DBS_EXPORT int dbs_decode_batch(
+    DBSDecoderHandle* handle,
+    const float* log_probs,
+    int batch_size,
+    int steps,
+    int vocab_size,
+    int num_threads,
+    DBSBatchResultHandle** out_result);
+
+DBS_EXPORT int dbs_decode_batch_variable(
+    DBSDecoderHandle* handle,
+    const float* log_probs,
+    int batch_size,
+    int max_steps,
+    int max_beam_size,
+    int vocab_size,
+    const int32_t* steps_per_example,
+    const int32_t* beam_sizes_per_example,
+    const int32_t* eos_tokens_per_example,
+    const int32_t* min_lengths_per_example,
+    const uint8_t* banned_tokens_per_example,
+    const int32_t* forced_tokens_per_example,
+    int num_threads,
+    DBSBatchResultHandle** out_result);
+
+/* ---- Model-in-the-loop decodes (reference include/dbs.h:254-298): the
+ * callback gives each step's [K, V] rows; each step's selection runs on the
+ * GPU (one device step per callback). ---- */
+DBS_EXPORT int dbs_decode_model_steps(
+    DBSDecoderHandle* handle,
+    DBSModelStepFn step_fn,
+    void* user_data,
+    int batch_index,
+    int steps,
+    int vocab_size,
+    DBSResultHandle** out_result);
+
+DBS_EXPORT int dbs_decode_model_steps_with_workspace(
+    DBSDecoderHandle* handle,
+    DBSWorkspaceHandle* workspace,
+    DBSModelStepFn step_fn,
+    void* user_data,
+    int batch_index,
+    int steps,
+    int vocab_size,
+    DBSResultHandle** out_result);
+
+DBS_EXPORT int dbs_decode_model_steps_ex(
+    DBSDecoderHandle* handle,
+    DBSModelStepExFn step_fn,
+    void* user_data,
+    int batch_index,
+    int steps,
+    int vocab_size,
+    const DBSAdvancedConstraintsC* constraints,
+    DBSResultHandle** out_result);
+
+/* ---- Backward of a result (reference include/dbs.h:439-473): the gradient
+ * w.r.t. the log-probabilities [T, K, V] of the selected-beam weight
+ * gradients [T, K] and final-score gradients [K] (either may be NULL), dense
+ * (capped by max_dense_gradient_elements) or as sorted sparse entries
+ * (dbs_backward and dbs_backward_default), and the gradient w.r.t. the
+ * initial beam scores [K]. grad_relaxed_weights must be NULL (no pool). ---- */
+DBS_EXPORT int dbs_backward(
+    DBSDecoderHandle* handle,
+    const DBSResultHandle* result,
+    const float* grad_selected_weights,
+    const float* grad_relaxed_weights,
+    const float* grad_final_scores,
+    DBSBackwardHandle** out_backward);
+
+DBS_EXPORT int dbs_backward_dense(
+    DBSDecoderHandle* handle,
+    const DBSResultHandle* result,
+    const float* grad_selected_weights,
+    const float* grad_relaxed_weights,
+    const float* grad_final_scores,
+    DBSBackwardHandle** out_backward);
+
+DBS_EXPORT int dbs_backward_sparse(
+    DBSDecoderHandle* handle,
+    const DBSResultHandle* result,
+    const float* grad_selected_weights,
+    const float* grad_relaxed_weights,
+    const float* grad_final_scores,
+    DBSBackwardHandle** out_backward);
+
+DBS_EXPORT int dbs_backward_default(
+    DBSDecoderHandle* handle,
+    const DBSResultHandle* result,
+    const float* grad_selected_weights,
+    const float* grad_relaxed_weights,
+    const float* grad_final_scores,
+    DBSBackwardHandle** out_backward);
+
+DBS_EXPORT void dbs_free_result(DBSResultHandle* result);
+DBS_EXPORT void dbs_free_batch_result(DBSBatchResultHandle* result);
+DBS_EXPORT void dbs_free_backward(DBSBackwardHandle* result);
+
+/* ---- Accessors (reference include/dbs.h:475-521). Pointers are borrowed
+ * from the handle; NULL for a NULL handle or an empty array. ---- */
+DBS_EXPORT int dbs_batch_result_size(const DBSBatchResultHandle* result);
+DBS_EXPORT const DBSResultHandle* dbs_batch_result_at(const DBSBatchResultHandle* result, int batch_index);
+
+DBS_EXPORT int dbs_result_steps(const DBSResultHandle* result);
+DBS_EXPORT int dbs_result_beam_size(const DBSResultHandle* result);
+DBS_EXPORT int dbs_result_vocab_size(const DBSResultHandle* result);
+DBS_EXPORT int dbs_result_pool_size(const DBSResultHandle* result);
+
+DBS_EXPORT const int32_t* dbs_result_tokens(const DBSResultHandle* result);
+DBS_EXPORT const int32_t* dbs_result_parents(const DBSResultHandle* result);
+DBS_EXPORT const int32_t* dbs_result_lengths(const DBSResultHandle* result);
+DBS_EXPORT const float* dbs_result_scores(const DBSResultHandle* result);
+DBS_EXPORT const float* dbs_result_raw_scores(const DBSResultHandle* result);
+DBS_EXPORT const float* dbs_result_weights(const DBSResultHandle* result);
+DBS_EXPORT const float* dbs_result_final_scores(const DBSResultHandle* result);
+DBS_EXPORT const float* dbs_result_final_raw_scores(const DBSResultHandle* result);
+
+DBS_EXPORT const float* dbs_result_relaxed_weights(const DBSResultHandle* result);
+DBS_EXPORT const int32_t* dbs_result_pool_tokens(const DBSResultHandle* result);
+DBS_EXPORT const int32_t* dbs_result_pool_parents(const DBSResultHandle* result);
+DBS_EXPORT const int32_t* dbs_result_pool_lengths(const DBSResultHandle* result);
+DBS_EXPORT const float* dbs_result_pool_scores(const DBSResultHandle* result);
+DBS_EXPORT const float* dbs_result_pool_raw_scores(const DBSResultHandle* result);
+
+DBS_EXPORT const float* dbs_backward_grad_log_probs(const DBSBackwardHandle* result);
+DBS_EXPORT const float* dbs_backward_grad_initial_scores(const DBSBackwardHandle* result);
+DBS_EXPORT const int64_t* dbs_backward_sparse_logprob_indices(const DBSBackwardHandle* result);
+DBS_EXPORT const float* dbs_backward_sparse_logprob_values(const DBSBackwardHandle* result);
+DBS_EXPORT int64_t dbs_backward_sparse_logprob_count(const DBSBackwardHandle* result);
+DBS_EXPORT int dbs_backward_is_sparse(const DBSBackwardHandle* result);
+
+DBS_EXPORT int64_t dbs_result_selected_count(const DBSResultHandle* result);
+DBS_EXPORT int64_t dbs_result_pool_count(const DBSResultHandle* result);
+DBS_EXPORT int64_t dbs_result_logprob_count(const DBSResultHandle* result);
+DBS_EXPORT int64_t dbs_backward_grad_log_probs_count(const DBSResultHandle* result);
+DBS_EXPORT int64_t dbs_backward_grad_initial_scores_count(const DBSResultHandle* result);
+
+DBS_EXPORT int64_t dbs_result_eos_count(const DBSResultHandle* result, int eos_token);
+/* 0 if every step's beams follow the candidate order, -3 for scores out of
+ * order, -4 for a tie broken out of order, -1 for NULL. */
+DBS_EXPORT int dbs_result_validate_deterministic_order(const DBSResultHandle* result);
+DBS_EXPORT int dbs_result_summary_json(const DBSResultHandle* result, int eos_token, char* out_json,
+                                       int64_t out_json_capacity);
+
+/* ---- Host queries, statistics and determinism (reference include/dbs.h:
+ * 523-545). dbs_has_* report the host CPU's extensions. ---- */
+DBS_EXPORT int dbs_has_avx512(void);
+DBS_EXPORT int dbs_has_avx2(void);
+DBS_EXPORT int dbs_has_sse42(void);
+DBS_EXPORT int dbs_has_neon(void);
+DBS_EXPORT int dbs_get_stats(DBSDecoderHandle* handle, DBSStatsC* out_stats);
+DBS_EXPORT int dbs_get_stats_json(DBSDecoderHandle* handle, char* out_json, int64_t out_json_capacity);
+/* Always 1: no randomness, and a strict total order over candidates. */
+DBS_EXPORT int dbs_is_deterministic(void);
+/* A per-handle seed kept for ABI compatibility; nothing reads it. */
+DBS_EXPORT int dbs_set_deterministic_seed(DBSDecoderHandle* handle, uint64_t seed);
+DBS_EXPORT uint64_t dbs_get_deterministic_seed(DBSDecoderHandle* handle);
+DBS_EXPORT void dbs_allocator_counters_reset(void);
+DBS_EXPORT int64_t dbs_allocator_call_count(void);
+DBS_EXPORT int64_t dbs_allocator_byte_count(void);
+DBS_EXPORT void dbs_reset_stats(DBSDecoderHandle* handle);
 
 #ifdef __cplusplus
 }

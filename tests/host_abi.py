@@ -215,3 +215,137 @@ class HostLib:
             inp.row_lse = _p(arr("lse", row_lse, np.float32), C.c_float)
         status = self.lib.dbs_backward_batch_into_ex(h, C.byref(inp), 0, _p(grad, C.c_float))
         return status, grad
+
+
+# ---------------------------------------------------------------------------
+# Result handles, backward handles and model-step decodes
+# ---------------------------------------------------------------------------
+
+class StatsC(C.Structure):
+    _fields_ = [("abi_version", C.c_int), ("last_kernel", C.c_int), ("used_sparse_backward", C.c_int),
+                ("used_dense_backward", C.c_int), ("used_batch_threads", C.c_int),
+                ("used_model_step_callback", C.c_int), ("last_error_category", C.c_int),
+                ("last_decode_ns", C.c_int64), ("last_backward_ns", C.c_int64), ("last_allocation_bytes", C.c_int64),
+                ("last_selected_count", C.c_int64), ("last_pool_count", C.c_int64),
+                ("last_logprob_count", C.c_int64), ("last_sparse_grad_count", C.c_int64),
+                ("total_allocator_calls", C.c_int64), ("total_allocator_bytes", C.c_int64),
+                ("reserved_stats0", C.c_int64), ("reserved_stats1", C.c_int64)]
+
+
+class StepInfoC(C.Structure):
+    _fields_ = [("batch_index", C.c_int), ("step", C.c_int), ("beam_size", C.c_int), ("vocab_size", C.c_int),
+                ("parents", _i32p), ("tokens", _i32p), ("lengths", _i32p), ("scores", _f32p),
+                ("raw_scores", _f32p), ("finished", _u8p), ("prefixes", _i32p), ("reserved", C.c_void_p * 4)]
+
+
+STEP_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, _i32p, _f32p, C.c_int, C.c_int, _f32p)
+STEP_EX_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(StepInfoC), _f32p)
+
+_RESULT_I32 = ("tokens", "parents", "lengths")
+_RESULT_F32 = ("scores", "raw_scores", "weights")
+
+
+def _declare_results(L):
+    vp, i = C.c_void_p, C.c_int
+    sig = {
+        "dbs_decode": (i, [vp, _f32p, i, i, C.POINTER(vp)]),
+        "dbs_decode_typed": (i, [vp, vp, i, i, i, C.POINTER(vp)]),
+        "dbs_decode_batch_typed": (i, [vp, vp, i, i, i, i, i, C.POINTER(vp)]),
+        "dbs_decode_constrained": (i, [vp, _f32p, i, i, _u8p, _i32p, i, C.POINTER(vp)]),
+        "dbs_decode_constrained_ex": (i, [vp, _f32p, i, i, C.POINTER(ConstraintsC), C.POINTER(vp)]),
+        "dbs_decode_batch": (i, [vp, _f32p, i, i, i, i, C.POINTER(vp)]),
+        "dbs_decode_batch_variable": (i, [vp, _f32p, i, i, i, i, _i32p, _i32p, _i32p, _i32p, _u8p, _i32p, i,
+                                          C.POINTER(vp)]),
+        "dbs_decode_model_steps": (i, [vp, STEP_FN, vp, i, i, i, C.POINTER(vp)]),
+        "dbs_decode_model_steps_with_workspace": (i, [vp, vp, STEP_FN, vp, i, i, i, C.POINTER(vp)]),
+        "dbs_decode_model_steps_ex": (i, [vp, STEP_EX_FN, vp, i, i, i, C.POINTER(ConstraintsC), C.POINTER(vp)]),
+        "dbs_backward": (i, [vp, vp, _f32p, _f32p, _f32p, C.POINTER(vp)]),
+        "dbs_backward_dense": (i, [vp, vp, _f32p, _f32p, _f32p, C.POINTER(vp)]),
+        "dbs_backward_sparse": (i, [vp, vp, _f32p, _f32p, _f32p, C.POINTER(vp)]),
+        "dbs_backward_default": (i, [vp, vp, _f32p, _f32p, _f32p, C.POINTER(vp)]),
+        "dbs_free_result": (None, [vp]),
+        "dbs_free_batch_result": (None, [vp]),
+        "dbs_free_backward": (None, [vp]),
+        "dbs_batch_result_size": (i, [vp]),
+        "dbs_batch_result_at": (vp, [vp, i]),
+        "dbs_result_steps": (i, [vp]),
+        "dbs_result_beam_size": (i, [vp]),
+        "dbs_result_vocab_size": (i, [vp]),
+        "dbs_result_pool_size": (i, [vp]),
+        "dbs_result_final_scores": (_f32p, [vp]),
+        "dbs_result_final_raw_scores": (_f32p, [vp]),
+        "dbs_result_relaxed_weights": (_f32p, [vp]),
+        "dbs_result_pool_tokens": (_i32p, [vp]),
+        "dbs_backward_grad_log_probs": (_f32p, [vp]),
+        "dbs_backward_grad_initial_scores": (_f32p, [vp]),
+        "dbs_backward_sparse_logprob_indices": (C.POINTER(C.c_int64), [vp]),
+        "dbs_backward_sparse_logprob_values": (_f32p, [vp]),
+        "dbs_backward_sparse_logprob_count": (C.c_int64, [vp]),
+        "dbs_backward_is_sparse": (i, [vp]),
+        "dbs_result_selected_count": (C.c_int64, [vp]),
+        "dbs_result_pool_count": (C.c_int64, [vp]),
+        "dbs_result_logprob_count": (C.c_int64, [vp]),
+        "dbs_backward_grad_log_probs_count": (C.c_int64, [vp]),
+        "dbs_backward_grad_initial_scores_count": (C.c_int64, [vp]),
+        "dbs_result_eos_count": (C.c_int64, [vp, i]),
+        "dbs_result_validate_deterministic_order": (i, [vp]),
+        "dbs_result_summary_json": (i, [vp, i, C.c_char_p, C.c_int64]),
+        "dbs_get_stats": (i, [vp, C.POINTER(StatsC)]),
+        "dbs_get_stats_json": (i, [vp, C.c_char_p, C.c_int64]),
+        "dbs_reset_stats": (None, [vp]),
+        "dbs_is_deterministic": (i, []),
+        "dbs_set_deterministic_seed": (i, [vp, C.c_uint64]),
+        "dbs_get_deterministic_seed": (C.c_uint64, [vp]),
+        "dbs_workspace_create": (i, [C.POINTER(vp)]),
+        "dbs_workspace_destroy": (None, [vp]),
+        "dbs_workspace_reserve": (i, [vp, C.c_int64, C.c_int64]),
+        "dbs_workspace_allocated_bytes": (C.c_int64, [vp]),
+    }
+    for name in _RESULT_I32:
+        sig[f"dbs_result_{name}"] = (_i32p, [vp])
+    for name in _RESULT_F32:
+        sig[f"dbs_result_{name}"] = (_f32p, [vp])
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _copy(ptr, n, dt):
+    if not ptr or n == 0:
+        return None
+    return np.ctypeslib.as_array(ptr, shape=(n,)).astype(dt, copy=True)
+
+
+def read_result(L, r) -> dict:
+    """Every accessor of a result handle, copied out."""
+    T, K, V = L.dbs_result_steps(r), L.dbs_result_beam_size(r), L.dbs_result_vocab_size(r)
+    out = {"steps": T, "beam_size": K, "vocab_size": V, "pool_size": L.dbs_result_pool_size(r)}
+    for name in _RESULT_I32:
+        out[name] = _copy(getattr(L, f"dbs_result_{name}")(r), T * K, np.int32)
+    for name in _RESULT_F32:
+        out[name] = _copy(getattr(L, f"dbs_result_{name}")(r), T * K, np.float32)
+    out["final_scores"] = _copy(L.dbs_result_final_scores(r), K, np.float32)
+    out["final_raw_scores"] = _copy(L.dbs_result_final_raw_scores(r), K, np.float32)
+    out["relaxed_weights_null"] = not L.dbs_result_relaxed_weights(r)
+    out["pool_tokens_null"] = not L.dbs_result_pool_tokens(r)
+    out["counts"] = (L.dbs_result_selected_count(r), L.dbs_result_pool_count(r), L.dbs_result_logprob_count(r),
+                     L.dbs_backward_grad_log_probs_count(r), L.dbs_backward_grad_initial_scores_count(r))
+    out["order"] = L.dbs_result_validate_deterministic_order(r)
+    return out
+
+
+def read_backward(L, b, n_dense: int, K: int) -> dict:
+    """Every accessor of a backward handle, copied out."""
+    count = L.dbs_backward_sparse_logprob_count(b)
+    return {"is_sparse": L.dbs_backward_is_sparse(b),
+            "dense": _copy(L.dbs_backward_grad_log_probs(b), n_dense, np.float32),
+            "initial": _copy(L.dbs_backward_grad_initial_scores(b), K, np.float32),
+            "count": count,
+            "indices": _copy(L.dbs_backward_sparse_logprob_indices(b), count, np.int64),
+            "values": _copy(L.dbs_backward_sparse_logprob_values(b), count, np.float32)}
+
+
+def enable_results(host: "HostLib") -> "HostLib":
+    _declare_results(host.lib)
+    return host

@@ -334,3 +334,60 @@ def test_features_the_engine_does_not_serve_are_refused(ours):
         assert st == -1 and "beyond the HIP engine" in ours.error()
     finally:
         ours.destroy(h)
+
+
+REF_SYMBOLS = "/root/reference/abi/libdbs.symbols"
+
+
+@pytest.mark.skipif(not os.path.exists(REF_SYMBOLS), reason="reference not mounted")
+def test_exported_host_symbols_are_the_references():
+    """The host functions libdbs_hip.so exports are exactly the reference's
+    81 (its abi/libdbs.symbols, the list its scripts/check_abi.sh checks);
+    the device ABI (dbs_cuda_*) and its additions (dbs_hip_*) come on top."""
+    out = subprocess.run(["nm", "-D", "--defined-only", _build.lib_path()], capture_output=True, text=True,
+                         check=True).stdout
+    host = {n for n in re.findall(r" T (dbs_\w+)", out) if not n.startswith(("dbs_cuda_", "dbs_hip_"))}
+    want = set(open(REF_SYMBOLS).read().split())
+    assert len(want) == 81
+    assert host == want
+    assert set(declared()) == want
+
+
+STATS_PROBE = r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "dbs.h"
+#define S(s) printf(#s " %zu\n", sizeof(s));
+#define F(s, f) printf(#s "." #f " %zu\n", offsetof(s, f));
+int main(void) {
+  S(DBSStatsC) F(DBSStatsC, last_error_category) F(DBSStatsC, last_decode_ns) F(DBSStatsC, total_allocator_bytes)
+  F(DBSStatsC, reserved_stats1)
+  S(DBSModelStepInfoC) F(DBSModelStepInfoC, parents) F(DBSModelStepInfoC, finished) F(DBSModelStepInfoC, prefixes)
+  F(DBSModelStepInfoC, reserved)
+  return 0;
+}
+"""
+
+
+def test_result_structs_layout(tmp_path):
+    """DBSStatsC and DBSModelStepInfoC: our header against the ctypes
+    mirror, and against the reference header where it is mounted."""
+    import ctypes as C
+
+    from tests.host_abi import StatsC, StepInfoC
+
+    def probe(include_dir):
+        src = tmp_path / "probe_stats.c"
+        src.write_text(STATS_PROBE)
+        exe = tmp_path / f"probe_stats_{abs(hash(include_dir))}"
+        subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{include_dir}", str(src), "-o", str(exe)],
+                       check=True)
+        return subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+
+    ours = probe(INCLUDE)
+    lines = dict(line.rsplit(" ", 1) for line in ours.strip().splitlines())
+    assert int(lines["DBSStatsC"]) == C.sizeof(StatsC)
+    assert int(lines["DBSModelStepInfoC"]) == C.sizeof(StepInfoC)
+    assert int(lines["DBSModelStepInfoC.prefixes"]) == StepInfoC.prefixes.offset
+    if os.path.exists(REF_INCLUDE):
+        assert ours == probe(REF_INCLUDE)
