@@ -40,7 +40,7 @@ HIP_FLAGS = [
 ]
 
 LIB_SOURCES = ["csrc/api.hip", "csrc/host_abi.cpp", "csrc/host_results.cpp", "csrc/decode.hip", "csrc/row_pass.hip", "csrc/row_resident.hip",
-               "csrc/row_pipe.hip", "csrc/row_logprob.hip", "csrc/row_stream.hip", "csrc/row_relay.hip", "csrc/select.hip", "csrc/backward.hip"]
+               "csrc/row_pipe.hip", "csrc/row_logprob.hip", "csrc/row_relay.hip", "csrc/select.hip", "csrc/backward.hip"]
 
 
 def lib_path() -> str:

@@ -723,7 +723,7 @@ DBS_CUDA_EXPORT int dbs_hip_set_decode_overlap(int on) {
 }
 
 DBS_CUDA_EXPORT int dbs_hip_set_row_pass(int kind) {
-    if (kind < -1 || kind > 5) return -2;
+    if (kind < -1 || kind > 5 || kind == 4) return -2;
     return dbs_hip::g_row_pass_kind.exchange(kind);
 }
 

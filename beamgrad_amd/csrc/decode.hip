@@ -107,10 +107,6 @@ DecodeLayout decode_layout(int B, int T, int K, int V, bool constrained, bool st
         off = align(off + sizeof(int32_t) * static_cast<size_t>(B) * K * (L.prefix_cap > 0 ? L.prefix_cap : 1));
     L.off_sync = off;
     if (!step_mode) off = align(off + sync_bytes(B, T));
-    // rows a persistent row pass leaves to the fixup kernel: the count (16
-    // bytes), then one index per row
-    L.off_fixup = off;
-    off = align(off + 16 + sizeof(int64_t) * static_cast<size_t>(rows));
     L.total = off;
     (void)V;
     return L;
@@ -207,8 +203,6 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
                          int32_t** fault, bool allow_overlap) {
     DecodeParams p = p0;
     *fault = nullptr;
-    p.fixup_count = reinterpret_cast<unsigned long long*>(ws + L.off_fixup);
-    p.fixup_rows = reinterpret_cast<int64_t*>(ws + L.off_fixup + 16);
     int device = 0;
     hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess) return e;

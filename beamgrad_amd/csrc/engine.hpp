@@ -121,10 +121,6 @@ struct DecodeParams {
     int32_t* fault;
     unsigned long long wait_ticks;
     int wait_extra;
-    // rows a persistent row pass leaves to the two-pass fixup kernel (rows
-    // indices, count; in the workspace, the count cleared before the pass)
-    int64_t* fixup_rows;
-    unsigned long long* fixup_count;
     // optional [B]: the first row holding NaN or +inf that example b's search
     // read, as t * K + k in reading order, or -1 (the host ABI's error text)
     int32_t* first_invalid;
@@ -147,7 +143,7 @@ struct DecodeLayout {
     int use_tau;
     int prefix_cap;
     SelectLayout sel;
-    size_t off_rowinfo, off_short, off_prefix, off_blocked, off_sync, off_fixup, total;
+    size_t off_rowinfo, off_short, off_prefix, off_blocked, off_sync, total;
 };
 
 DecodeLayout decode_layout(int B, int T, int K, int V, bool constrained, bool step_mode, int prefix_stride);
@@ -171,10 +167,6 @@ bool row_pass_persistent(const DecodeParams& p);
 bool row_resident_eligible(const DecodeParams& p);
 hipError_t launch_row_resident(const DecodeParams& p, int64_t rows, hipStream_t stream);
 bool row_pipe_eligible(const DecodeParams& p);
-// Row pass that streams bfloat16 logits rows through an LDS ring into
-// registers (65536 < V <= 153600, V % 8 == 0, 16-byte aligned).
-bool row_stream_eligible(const DecodeParams& p);
-hipError_t launch_row_stream(const DecodeParams& p, int64_t rows, hipStream_t stream);
 // bfloat16 logits, both segments of a 512-thread workgroup relaying (row_relay.hip)
 bool row_relay_eligible(const DecodeParams& p);
 // The relay row pass is the default for the rows it fills (it always folds

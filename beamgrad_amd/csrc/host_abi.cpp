@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <exception>
 
 #include "dbs_cuda.h"
@@ -410,8 +411,17 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
 }
 
 // Device buffers a chunk of examples of the from-logits backward may take:
-// the logits and a float32 gradient of its rows.
-constexpr size_t kBackwardChunkBytes = size_t{1} << 30;
+// the logits and a float32 gradient of its rows. Test knob
+// DBS_HIP_TEST_BACKWARD_CHUNK_BYTES sets a smaller bound (one example per
+// chunk at least).
+size_t backward_chunk_bytes() {
+    const char* env = std::getenv("DBS_HIP_TEST_BACKWARD_CHUNK_BYTES");
+    if (env && env[0]) {
+        const long long v = std::atoll(env);
+        if (v > 0) return static_cast<size_t>(v);
+    }
+    return size_t{1} << 30;
+}
 
 // The backward of a batch into the host buffer grad [B, T, K, V] (+=): the
 // per-slot path gradients from the device, then the entries they name, or
@@ -453,7 +463,8 @@ void backward_batch(DBSDecoderHandle* h, int B, int T, int V, const int32_t* ste
         // chunk of examples at a time, and the rows with an entry are added
         // here in full (reference src/decoder.hpp:212-242).
         const size_t example_bytes = mul(row_block, dtype_bytes(logits_type) + sizeof(float), "batch stride overflow");
-        const int chunk = static_cast<int>(std::max<size_t>(1, std::min<size_t>(B, kBackwardChunkBytes / example_bytes)));
+        const int chunk =
+            static_cast<int>(std::max<size_t>(1, std::min<size_t>(B, backward_chunk_bytes() / example_bytes)));
         std::lock_guard<std::mutex> lock(h->run_mutex);
         const hipStream_t st = stream_of(h);
         for (int b0 = 0; b0 < B; b0 += chunk) {

@@ -146,24 +146,6 @@ __global__ __launch_bounds__(kRowThreads) void row_pass_kernel(DecodeParams p) {
     row_pass_one<DT, LOGITS, VEC>(p, r, b, new_len, s_key, s_x, s_count);
 }
 
-// The rows a persistent row pass left to this kernel (p.fixup_rows, count in
-// *p.fixup_count), one wavefront each, grid-strided.
-template <int DT, bool LOGITS, bool VEC>
-__global__ __launch_bounds__(kRowThreads) void row_fixup_kernel(DecodeParams p) {
-    __shared__ uint64_t s_key[kSurvivorCap];
-    __shared__ float s_x[kSurvivorCap];
-    __shared__ int s_count;
-    const int64_t n = static_cast<int64_t>(*p.fixup_count);
-    for (int64_t i = blockIdx.x; i < n; i += gridDim.x) {
-        const int64_t r = p.fixup_rows[i];
-        int b, new_len;
-        if (!row_is_read(p, r, b, new_len)) continue;
-        row_pass_one<DT, LOGITS, VEC>(p, r, b, new_len, s_key, s_x, s_count);
-        __syncthreads();
-    }
-}
-
-
 }  // namespace
 
 std::atomic<int> g_row_pass_kind{-1};
@@ -173,7 +155,6 @@ bool row_pass_persistent(const DecodeParams& p) {
     if ((kind == -1 || kind == 3) && row_logprob_eligible(p)) return false;
     if ((kind == 5 || (kind == -1 && row_relay_preferred(p))) && row_relay_eligible(p)) return true;
     if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return true;
-    if ((kind == -1 || kind == 4) && row_stream_eligible(p)) return true;
     return (kind == -1 || kind == 2) && row_pipe_eligible(p);
 }
 
@@ -188,18 +169,6 @@ hipError_t launch_row_pass(const DecodeParams& p, hipStream_t stream) {
     if ((kind == 5 || (kind == -1 && row_relay_preferred(p))) && row_relay_eligible(p))
         return launch_row_relay(p, rows, stream);
     if ((kind == -1 || kind == 1) && row_resident_eligible(p)) return launch_row_resident(p, rows, stream);
-    if ((kind == -1 || kind == 4) && row_stream_eligible(p)) {
-        // the streaming pass, then the rows it left (NaN/+inf, no term table)
-        hipError_t e = launch_clear(p.fixup_count, sizeof(unsigned long long), stream);
-        if (e == hipSuccess) e = launch_row_stream(p, rows, stream);
-        if (e != hipSuccess) return e;
-        const int64_t grid = rows < 1024 ? rows : 1024;
-        if (vec) hipLaunchKernelGGL((row_fixup_kernel<2, true, true>), dim3(static_cast<unsigned>(grid)),
-                                    dim3(kRowThreads), 0, stream, p);
-        else hipLaunchKernelGGL((row_fixup_kernel<2, true, false>), dim3(static_cast<unsigned>(grid)),
-                                dim3(kRowThreads), 0, stream, p);
-        return hipGetLastError();
-    }
     if ((kind == -1 || kind == 2) && row_pipe_eligible(p)) return launch_row_pipe(p, rows, stream);
     const dim3 grid(static_cast<unsigned>(rows));
 #define DBS_ROW_PASS(DT, LG)                                                                                 \

@@ -11,7 +11,10 @@ count). Beside it: the row pass's HBM roofline fraction (kernel time from the
 engine's HIP events on its own stream), the reference CPU library on the same
 batch (num_threads = 0, median of 5 runs), and under ``c5`` the second half
 of the metric: the C5 forward + minimum-risk loss + backward step latency with
-the forward's and the backward's (dense gradient's) roofline.
+the forward's and the backward's (dense gradient's) roofline, and the
+reference CPU library's decode + backward of the same batch fed the same
+final-score gradient. Every roofline also states the box's measured device
+copy bandwidth (``copy_gbs``) and the fraction of it reached.
 
     python bench.py [--steps K] [--warmup W] [--config c1..c5] [--no-cpu-baseline] [--no-c5]
 """
@@ -150,7 +153,8 @@ def cpu_baseline(name: str, wl: dict, rows_per_example: float, runs: int = 5) ->
             run = lambda: impl.decode(host, banned_per_example=banned, **kw)  # noqa: E731
         what = "per-example dbs_decode_batch_into_ex calls (one banned mask each)"
     elif wl["costs"] is not None:
-        g_final = np.full((cfg["B"], cfg["K"]), 1.0 / cfg["B"], np.float32)
+        # the loss's gradient w.r.t. the final scores, as the GPU computed it
+        g_final = np.ascontiguousarray(wl["g_final"].cpu().numpy(), np.float32)
 
         def run():
             tr = impl.decode(host, **kw)
@@ -241,6 +245,11 @@ def measure(name: str, steps: int, warmup: int, copy_probe: bool = False) -> dic
         out = step()
     torch.cuda.synchronize()
     n_rows = rows_read(out, opts.eos_tokens)
+    if name == "c5":
+        # grad_final of this batch (the CPU baseline's backward gets the same)
+        result = bg.search(x.detach(), opts, from_logits=True)
+        s = result.scores.detach().clone().requires_grad_(True)
+        wl["g_final"] = torch.autograd.grad(bg.losses.minimum_risk(result._replace(scores=s), wl["costs"]), s)[0]
 
     if copy_probe:
         src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
@@ -293,10 +302,40 @@ def rows_with_gradient(trace, V: int, alpha: float) -> int:
     return int(torch.unique(keys).numel())
 
 
+_COPY_GBS: float | None = None
+
+
+def copy_bandwidth(gib: int = 2, reps: int = 10) -> float:
+    """The box's measured device copy bandwidth (GB/s, bytes read + bytes
+    written): a device-to-device copy of ``gib`` GiB on the current stream,
+    2 warm-ups, the median of ``reps`` HIP-event timings. Measured once per
+    process."""
+    global _COPY_GBS
+    if _COPY_GBS is None:
+        n = gib << 28  # float32 elements
+        src = torch.empty(n, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        times = []
+        for i in range(2 + reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            dst.copy_(src)
+            b.record()
+            b.synchronize()
+            if i >= 2:
+                times.append(a.elapsed_time(b))
+        _COPY_GBS = 2 * 4 * n / (float(np.median(times)) / 1e3) / 1e9
+        del src, dst
+        torch.cuda.empty_cache()
+    return _COPY_GBS
+
+
 def hbm_roofline(bytes_per_launch: float, avg_ms: float, kernel: str, traffic=None) -> dict:
     achieved = bytes_per_launch / (avg_ms / 1e3) / 1e9
+    copy_gbs = copy_bandwidth()
     return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-            "traffic": traffic, "kernel": kernel, "algorithmic_bytes": bytes_per_launch}
+            "traffic": traffic, "kernel": kernel, "algorithmic_bytes": bytes_per_launch, "copy_gbs": copy_gbs,
+            "frac_of_copy": achieved / copy_gbs}
 
 
 def c5_summary(m: dict) -> dict:
@@ -376,7 +415,10 @@ def main() -> int:
     if args.config == "c2" and not args.no_c5:
         del m
         torch.cuda.empty_cache()
-        result["c5"] = c5_summary(measure("c5", max(3, args.steps // 2), 2))
+        m5 = measure("c5", max(3, args.steps // 2), 2)
+        result["c5"] = c5_summary(m5)
+        if not args.no_cpu_baseline:
+            result["c5"]["cpu_baseline"] = cpu_baseline("c5", m5["wl"], m5["rows_read"] / m5["cfg"]["B"])
     print(json.dumps(result), flush=True)
     return 0
 

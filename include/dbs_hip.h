@@ -175,13 +175,12 @@ DBS_CUDA_EXPORT int dbs_hip_profile_read(int kernel, double* total_ms, int64_t* 
  * default: for log-prob rows the one-read log-prob kernel where it applies;
  * else, for bfloat16 logits rows of 116481 to 155648 entries, the relay
  * kernel; else the resident 16-bit kernel where it applies, else the
- * streaming 16-bit kernel, else the pipelined 16-bit kernel, else the
- * two-pass kernel), 0 two-pass, 1 resident 16-bit (V % 8 == 0, 16-byte
- * aligned rows), 2 pipelined 16-bit (any V), 3 one-read log-prob rows (any
- * dtype, rows up to 163824 bytes), 4 streaming 16-bit (V % 8 == 0, 16-byte
- * aligned rows), 5 relay for bfloat16 logits (V % 8 == 0, 16-byte aligned
- * rows, V <= 155648). A kernel that does not apply to a decode falls back to
- * the two-pass one. Returns the previous choice, or -2 for an invalid
+ * pipelined 16-bit kernel, else the two-pass kernel), 0 two-pass, 1 resident
+ * 16-bit (V % 8 == 0, 16-byte aligned rows), 2 pipelined 16-bit (any V), 3
+ * one-read log-prob rows (any dtype, rows up to 163824 bytes), 5 relay for
+ * bfloat16 logits (V % 8 == 0, 16-byte aligned rows, V <= 155648); 4 is not
+ * a kernel (-2). A kernel that does not apply to a decode falls back to the
+ * two-pass one. Returns the previous choice, or -2 for an invalid
  * argument. */
 DBS_CUDA_EXPORT int dbs_hip_set_row_pass(int kind);
 

@@ -143,6 +143,7 @@ def test_host_entry_points(lib):
     assert lib.dbs_cuda_length_penalty(None, -1, 1.0, None, None) == 2
     assert lib.dbs_hip_profile_enable(3) == 2
     assert lib.dbs_hip_set_row_pass(6) == -2
+    assert lib.dbs_hip_set_row_pass(4) == -2  # no longer a kernel
     assert lib.dbs_hip_set_row_pass(-1) == -1  # automatic is the default
     assert lib.dbs_hip_set_row_pass(-1) == -1
     assert lib.dbs_hip_set_decode_overlap(2) == -2

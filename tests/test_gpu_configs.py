@@ -2,7 +2,8 @@
 """The five BASELINE configurations at their full sizes on the GPU, checked
 against the reference's own CPU library (oracle/_ref, where it is built; the
 oracle otherwise) on identical seeded inputs: every trace field and the final
-scores bit for bit, the backtracked sequences exactly, and for config 5 the
+scores bit for bit, the logsumexp of every row (row_lse: the rows the search
+read, 0 elsewhere), the backtracked sequences exactly, and for config 5 the
 gradient of the minimum-risk loss w.r.t. the bf16 logits (bf16 bits equal to
 the reference's float32 gradient rounded to bf16).
 
@@ -43,6 +44,16 @@ def _cpu_decode(name, wl, host):
     orc = Oracle()
     bpe = None if wl["banned"] is None else wl["banned"].cpu().numpy()
     return orc.decode(host, banned_per_example=bpe, **kw), orc
+
+
+def _gpu_row_lse(name, wl):
+    """row_lse [B, T, K] of the config's decode on the GPU (the operator the
+    Python API calls, which returns it as its tenth output)."""
+    cfg = CONFIGS[name]
+    out = torch.ops.beamgrad.decode_ex(wl["x"].detach(), cfg["from_logits"], wl["steps"], cfg["eos"],
+                                       cfg["min_length"], cfg["alpha"], wl["banned"], cfg.get("ngram", 0),
+                                       cfg.get("rep", 1.0), True, [])
+    return out[9].cpu().numpy()
 
 
 def _gpu_trace(out):
@@ -92,10 +103,11 @@ def test_config_decode_matches_reference(name):
     out = bg.decode(wl["x"], opts, wl["steps"], from_logits=cfg["from_logits"], banned_mask=wl["banned"])
     seq = bg.backtrack(out).cpu().numpy()
     got = _gpu_trace(out)
+    got["row_lse"] = _gpu_row_lse(name, wl)
     host = _host(wl["x"])
     print(f"[config {name}] CPU reference", flush=True)
     want, _ = _cpu_decode(name, wl, host)
-    diff = first_difference(got, want, KEYS)
+    diff = first_difference(got, want, KEYS + ("row_lse",))
     assert diff is None, f"config {name}: {diff}"
     steps = None if wl["steps"] is None else wl["steps"].cpu().numpy()
     assert np.array_equal(seq, Oracle().backtrack(want["tokens"], want["parents"], steps))
@@ -117,11 +129,12 @@ def test_config5_forward_backward_matches_reference():
     g_final = torch.autograd.grad(bg.losses.minimum_risk(result._replace(scores=s), wl["costs"]), s)[0]
     got = _gpu_trace(result.trace)
     got["final_scores"] = result.scores.detach().cpu().numpy()
+    got["row_lse"] = _gpu_row_lse(name, wl)
     grad_got = x.grad.view(torch.int16).cpu().numpy()
     host = _host(x)
     print("[config c5] CPU reference decode", flush=True)
     want, impl = _cpu_decode(name, wl, host)
-    diff = first_difference(got, want, KEYS)
+    diff = first_difference(got, want, KEYS + ("row_lse",))
     assert diff is None, f"config c5: {diff}"
     print("[config c5] CPU reference backward", flush=True)
     grad_want = impl.backward(want, cfg["V"], grad_final=g_final.cpu().numpy(), logits=host, logits_dtype="bf16",

@@ -184,3 +184,20 @@ def test_handle_reused_across_shapes(libs):
     finally:
         for lib, h in zip(libs, hs):
             lib.destroy(h)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_logits_backward_in_small_chunks(libs, monkeypatch, seed):
+    """The from-logits backward works a bounded chunk of examples at a time
+    (at most 1 GiB of logits and gradient rows on the device); with the
+    bound forced down to one example per chunk the bits are still the
+    reference library's."""
+    case = make_case(9950 + seed, dtypes=["bf16", "f32"], logits=True, allow_invalid=False)
+    while case["B"] < 2:
+        case = make_case(case["seed"] + 100, dtypes=["bf16", "f32"], logits=True, allow_invalid=False)
+    kw = dict(case["kw"])
+    kw["banned_per_example"] = None
+    out = _check_decode(libs, case["xin"], case["K"], case["dtype"], kw, cons_kw=_constraints_of(kw))
+    monkeypatch.setenv("DBS_HIP_TEST_BACKWARD_CHUNK_BYTES", "1")
+    _check_backward(libs, out, case["V"], case["K"], kw, xin=case["xin"], dtype=case["dtype"], steps=kw["steps"],
+                    seed=seed)

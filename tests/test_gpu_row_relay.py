@@ -1,10 +1,9 @@
 # SPDX-License-Identifier: MIT
-"""GPU parity of the persistent bfloat16 logits row passes against the CPU
-oracle, bit for bit on every decode output (tokens, parents, lengths, scores,
-final scores, row logsumexp, NaN/+inf flags): the streaming pass (kind 4,
-rows of 65537 to 153600 entries, V % 8 == 0; rows its table cannot take go to
-a fixup kernel) and the two-segment relay (kind 5, rows up to 155648
-entries; rows its fixed-base table cannot take fold from memory).
+"""GPU parity of the two-segment relay row pass for bfloat16 logits (row-pass
+kind 5, forced, at vocabularies from 65544 up to 155648 entries; rows its
+fixed-base table cannot take fold from memory) against the CPU oracle, bit
+for bit on every decode output (tokens, parents, lengths, scores, final
+scores, row logsumexp, NaN/+inf flags).
 
 The cases cover: random shapes and options (EOS, extra EOS, min_length,
 banned tokens, n-gram blocking, repetition penalty, per-example steps); a
@@ -24,11 +23,10 @@ pytestmark = pytest.mark.gpu
 _VOCABS = [65544, 70000, 100008, 128256, 131072, 131080, 151936, 153600]
 
 
-@pytest.fixture(params=[4, 5], ids=["stream", "relay"])
-def stream(hip, request):
-    """The persistent bfloat16 logits row passes, chosen explicitly: the
-    streaming pass (kind 4) and the two-segment relay (kind 5)."""
-    prev = hip.lib.dbs_hip_set_row_pass(request.param)
+@pytest.fixture
+def stream(hip):
+    """The relay row pass (kind 5), chosen explicitly."""
+    prev = hip.lib.dbs_hip_set_row_pass(5)
     yield hip
     hip.lib.dbs_hip_set_row_pass(prev)
 
