@@ -118,34 +118,31 @@ namespace {
 
 // The second stream of the overlapped decode and its two events, one set per
 // (device, caller stream): callers on different streams never share one, so
-// their decodes do not serialise. Default priority; created on first use and
-// kept until the process ends. At most kMaxAux per process; past that the
-// decode runs its passes one after the other on the caller's stream.
+// their decodes do not serialise. Default priority; created on first use.
+// The table holds kMaxAux sets; once it is full, the set a new caller stream
+// gets is the least recently used one of its device, rebound to it (the
+// callers that shared it then serialise their select passes on its stream,
+// still in order), or, with none on its device, the least recently used one
+// of any device, its stream and events made anew on this device.
 struct Aux {
     int device = -1;
     hipStream_t caller = nullptr;
     hipStream_t stream = nullptr;
     hipEvent_t start = nullptr, done = nullptr;
     int cus = 0;
-    std::mutex mutex;  // one decode's enqueue sequence at a time on this pair
+    uint64_t last_use = 0;
+    std::mutex mutex;  // one decode's enqueue sequence at a time on this set
 };
 constexpr int kMaxAux = 64;
 Aux g_aux[kMaxAux];
 int g_aux_used = 0;
+uint64_t g_aux_clock = 0;
 std::mutex g_aux_mutex;  // guards the table, not the launches
 
-// The caller's Aux (created on first use), or null when the table is full.
-hipError_t aux_for(int device, hipStream_t caller, Aux*& out) {
-    out = nullptr;
-    std::lock_guard<std::mutex> lock(g_aux_mutex);
-    for (int i = 0; i < g_aux_used; ++i) {
-        if (g_aux[i].device == device && g_aux[i].caller == caller) {
-            out = &g_aux[i];
-            return hipSuccess;
-        }
-    }
-    if (g_aux_used == kMaxAux) return hipSuccess;
-    Aux& a = g_aux[g_aux_used];
+// Stream, events and CU count of a set on `device` (current).
+hipError_t aux_create(Aux& a, int device) {
+    a.stream = nullptr;
+    a.start = a.done = nullptr;
     hipError_t e = hipDeviceGetAttribute(&a.cus, hipDeviceAttributeMultiprocessorCount, device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&a.start, hipEventDisableTiming);
@@ -154,13 +151,61 @@ hipError_t aux_for(int device, hipStream_t caller, Aux*& out) {
         if (a.stream) (void)hipStreamDestroy(a.stream);
         if (a.start) (void)hipEventDestroy(a.start);
         a.stream = nullptr;
-        a.start = nullptr;
+        a.start = a.done = nullptr;
+        a.device = -1;
         return e;
     }
     a.device = device;
-    a.caller = caller;
-    ++g_aux_used;
-    out = &a;
+    return hipSuccess;
+}
+
+// The caller's set (created, or taken over from the least recently used
+// one, on first use).
+hipError_t aux_for(int device, hipStream_t caller, Aux*& out) {
+    out = nullptr;
+    std::lock_guard<std::mutex> lock(g_aux_mutex);
+    const uint64_t now = ++g_aux_clock;
+    for (int i = 0; i < g_aux_used; ++i) {
+        if (g_aux[i].device == device && g_aux[i].caller == caller) {
+            g_aux[i].last_use = now;
+            out = &g_aux[i];
+            return hipSuccess;
+        }
+    }
+    if (g_aux_used < kMaxAux) {
+        Aux& a = g_aux[g_aux_used];
+        const hipError_t e = aux_create(a, device);
+        if (e != hipSuccess) return e;
+        a.caller = caller;
+        a.last_use = now;
+        ++g_aux_used;
+        out = &a;
+        return hipSuccess;
+    }
+    Aux* same = nullptr;
+    Aux* any = nullptr;
+    for (int i = 0; i < kMaxAux; ++i) {
+        Aux& a = g_aux[i];
+        if (a.device == device && (!same || a.last_use < same->last_use)) same = &a;
+        if (!any || a.last_use < any->last_use) any = &a;
+    }
+    if (same) {
+        same->caller = caller;
+        same->last_use = now;
+        out = same;
+        return hipSuccess;
+    }
+    // no set on this device: the oldest one moves here (its stream finishes
+    // the work already queued on it before it is destroyed)
+    std::lock_guard<std::mutex> busy(any->mutex);
+    if (any->stream) (void)hipStreamDestroy(any->stream);
+    if (any->start) (void)hipEventDestroy(any->start);
+    if (any->done) (void)hipEventDestroy(any->done);
+    const hipError_t e = aux_create(*any, device);
+    if (e != hipSuccess) return e;
+    any->caller = caller;
+    any->last_use = now;
+    out = any;
     return hipSuccess;
 }
 

@@ -237,3 +237,20 @@ def test_given_up_wait_fails_the_host_abi_decode(oracle, monkeypatch, validate):
     want = oracle.decode(case["xin"], dtype=case["dtype"], **kw)
     assert first_difference(out, want, ("final_scores", "final_raw_scores", "final_lengths", "tokens", "parents",
                                         "lengths", "scores", "raw_scores", "from_logprob", "row_lse")) is None
+
+
+def test_more_caller_streams_than_overlap_sets(hip, oracle, overlap_on):
+    """A decode on each of 70 caller streams (the library keeps 64 sets of
+    an auxiliary stream and two events; the least recently used set of the
+    device is rebound to a new caller), then again on the first ones: every
+    decode bit-exact, no wait given up."""
+    case = _big_case(7600)
+    want = oracle.decode(case["xin"], dtype=case["dtype"], **case["kw"])
+    streams = [torch.cuda.Stream() for _ in range(70)]
+    for rep in range(2):
+        for i, s in enumerate(streams if rep == 0 else streams[:8]):
+            with torch.cuda.stream(s):
+                got = hip.decode(case["xin"], case["dtype"], **case["kw"])
+            assert first_difference(got, want) is None, (rep, i)
+    torch.cuda.synchronize()
+    assert _timeouts(overlap_on) == 0
