@@ -811,8 +811,31 @@ DBS_CUDA_EXPORT int dbs_hip_backtrack_i64(const int64_t* tokens, const int64_t* 
         beam_size > DBS_CUDA_MAX_BEAM)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    return finish(stream,
-                  launch_backtrack(tokens, parents, steps_per_example, batch_size, steps, beam_size, sequences, stream));
+    return finish(stream, launch_backtrack(tokens, parents, steps_per_example, nullptr, batch_size, steps, beam_size,
+                                           sequences, stream));
+}
+
+DBS_CUDA_EXPORT int dbs_hip_search_sequences(const int64_t* tokens, const int64_t* parents,
+                                             const int64_t* steps_per_example, const int64_t* final_lengths,
+                                             int batch_size, int steps, int beam_size, int64_t* sequences,
+                                             void* stream_ptr) {
+    if (!tokens || !parents || !final_lengths || !sequences || batch_size <= 0 || steps <= 0 || beam_size <= 0 ||
+        beam_size > DBS_CUDA_MAX_BEAM)
+        return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    return finish(stream, launch_backtrack(tokens, parents, steps_per_example, final_lengths, batch_size, steps,
+                                           beam_size, sequences, stream));
+}
+
+DBS_CUDA_EXPORT int dbs_hip_minimum_risk(const float* scores, const float* costs, int batch_size, int beam_size,
+                                         float temperature, float scale, float* risk, float* grad_factor,
+                                         void* stream_ptr) {
+    if (!scores || !costs || !risk || !grad_factor || batch_size <= 0 || beam_size <= 0 ||
+        !(temperature > 0.0f) || !(temperature < kInf) || !(scale == scale))
+        return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    return finish(stream, launch_risk(scores, costs, batch_size, beam_size, temperature, scale, risk, grad_factor,
+                                      stream));
 }
 
 }  // extern "C"

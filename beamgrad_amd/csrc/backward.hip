@@ -4,9 +4,9 @@
 // decode's score outputs (each output differentiated along its own path with
 // the selection held fixed) and the backtrack of the final beams.
 //
-//  * path_walk: one workgroup per example walks the trace from its last step
-//    and produces, per selected slot, the gradient of the log-prob entry it
-//    used ("draws"). Per step every slot's draw is formed in the reference's
+//  * path_walk: one workgroup per example (one wavefront for K <= 64) walks
+//    the trace from its last step and produces, per selected slot, the
+//    gradient of the log-prob entry it used ("draws"). Per step every slot's draw is formed in the reference's
 //    operation order and each parent sums its children in slot order
 //    (reference src/decoder.cpp:565-624, 668-683).
 //  * dense_gradient: one workgroup per [V] row writes the row's gradient once.
@@ -115,6 +115,154 @@ __global__ __launch_bounds__(kWalkThreads) void path_walk_kernel(BackwardParams 
         next = prev;
         prev = swap;
     }
+}
+
+// path_walk_kernel for K <= 64: one wavefront per example walks, lane k
+// holding slot k and its incoming gradient in registers, and each parent
+// sums its children's raw-score gradients by reading the slots' lanes in slot
+// order (v_readlane): the same additions in the same order as the workgroup
+// walk, with no barrier and no LDS round trip per step. The next step's slot
+// is loaded while a step is walked.
+__global__ __launch_bounds__(64) void path_walk_wave_kernel(BackwardParams p) {
+    const int b = static_cast<int>(blockIdx.x);
+    const int k = static_cast<int>(threadIdx.x);
+    const int K = p.K, T = p.T, V = p.V;
+    const int steps_b = p.steps ? p.steps[b] : T;
+    const int Kb = p.beams ? p.beams[b] : K;  // slots past the example's beams carry nothing
+    const int64_t base = static_cast<int64_t>(b) * T * K;
+    // steps the example did not decode carry no gradient
+    for (int64_t i = static_cast<int64_t>(steps_b) * K + k; i < static_cast<int64_t>(T) * K; i += 64)
+        p.draws[base + i] = 0.0f;
+    struct SlotIn {
+        int parent = -1, len = 0, tok = -1;
+        float gs = 0.0f, graw = 0.0f;
+        bool flp = false;
+    };
+    auto load_slot = [&](int t) -> SlotIn {
+        SlotIn in;
+        const int64_t i = base + static_cast<int64_t>(t) * K + k;
+        in.parent = p.parents[i];
+        in.len = p.lengths[i];
+        in.tok = p.tokens[i];
+        in.flp = p.from_logprob[i] != 0;
+        if (p.g_scores) in.gs = p.g_scores[i];
+        if (p.g_raw) in.graw = p.g_raw[i];
+        return in;
+    };
+    float next = 0.0f;  // the slot's incoming gradient from the later steps
+    SlotIn cur;
+    if (k < K && steps_b > 0) cur = load_slot(steps_b - 1);
+    for (int t = steps_b - 1; t >= 0; --t) {
+        SlotIn nxt;
+        if (k < K && t > 0) nxt = load_slot(t - 1);
+        const bool last = t == steps_b - 1;
+        const bool valid = k < K && k < Kb && cur.parent >= 0 && cur.parent < Kb;  // malformed slots carry nothing
+        float d = 0.0f;
+        if (valid) {
+            float drank = 0.0f;
+            if (p.g_scores) drank = drank + cur.gs;
+            if (last && p.g_final) drank = drank + p.g_final[static_cast<int64_t>(b) * K + k];
+            const float inv_pen = 1.0f / length_penalty(cur.len, p.alpha);
+            d = next + drank * inv_pen;
+            if (p.g_raw) d = d + cur.graw;
+            if (last && p.g_final_raw) d = d + p.g_final_raw[static_cast<int64_t>(b) * K + k];
+        }
+        const bool flows = valid && d != 0.0f;
+        const float draw = flows ? d : 0.0f;
+        const int par = flows ? cur.parent : -1;
+        if (k < K)
+            p.draws[base + static_cast<int64_t>(t) * K + k] =
+                (flows && cur.flp && cur.tok >= 0 && cur.tok < V) ? d : 0.0f;
+        // each parent sums its children's draws in slot order
+        float sum = 0.0f;
+        for (int j = 0; j < K; ++j) {
+            const int pj = __builtin_amdgcn_readlane(par, j);
+            const float dj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, draw), j));
+            if (pj == k) sum = sum + dj;
+        }
+        next = sum;
+        cur = nxt;
+    }
+}
+
+// path_walk_wave_kernel with the example's trace in LDS (T * K up to
+// kWalkStageSlots): the workgroup's four wavefronts first stage every slot's
+// parent, inverse length penalty, incoming score gradients and whether its
+// draw is emitted (from a log-prob entry with a token in range), all loads
+// in flight at once; wavefront 0 then walks reading only LDS and writes the
+// draws to LDS; after a barrier the four wavefronts store them. The serial
+// loop holds no global memory round trip and no division.
+constexpr int kWalkStageThreads = 256;
+constexpr int kWalkStageSlots = 2560;  // at most 25 bytes a slot: 64000 bytes of LDS
+
+size_t walk_stage_bytes(const BackwardParams& p) {
+    const size_t per = 3 * sizeof(float) + (p.g_scores ? sizeof(float) : 0) + (p.g_raw ? sizeof(float) : 0) + 1;
+    return per * static_cast<size_t>(p.T) * static_cast<size_t>(p.K);
+}
+
+__global__ __launch_bounds__(kWalkStageThreads) void path_walk_staged_kernel(BackwardParams p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int b = static_cast<int>(blockIdx.x);
+    const int tid = static_cast<int>(threadIdx.x);
+    const int K = p.K, T = p.T, V = p.V;
+    const int steps_b = p.steps ? p.steps[b] : T;
+    const int Kb = p.beams ? p.beams[b] : K;  // slots past the example's beams carry nothing
+    const int64_t base = static_cast<int64_t>(b) * T * K;
+    // steps the example did not decode carry no gradient
+    for (int64_t i = static_cast<int64_t>(steps_b) * K + tid; i < static_cast<int64_t>(T) * K;
+         i += kWalkStageThreads)
+        p.draws[base + i] = 0.0f;
+    const int n = steps_b * K;
+    int32_t* s_par = reinterpret_cast<int32_t*>(smem);
+    float* s_ipen = reinterpret_cast<float*>(s_par + n);
+    float* s_draw = s_ipen + n;
+    float* s_gs = s_draw + n;
+    float* s_graw = s_gs + (p.g_scores ? n : 0);
+    uint8_t* s_emit = reinterpret_cast<uint8_t*>(s_graw + (p.g_raw ? n : 0));
+    for (int i = tid; i < n; i += kWalkStageThreads) {
+        const int64_t g = base + i;
+        s_par[i] = p.parents[g];
+        s_ipen[i] = 1.0f / length_penalty(p.lengths[g], p.alpha);
+        const int tok = p.tokens[g];
+        s_emit[i] = p.from_logprob[g] != 0 && tok >= 0 && tok < V;
+        if (p.g_scores) s_gs[i] = p.g_scores[g];
+        if (p.g_raw) s_graw[i] = p.g_raw[g];
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int k = tid;
+        float next = 0.0f;  // the slot's incoming gradient from the later steps
+        for (int t = steps_b - 1; t >= 0; --t) {
+            const int i = t * K + k;
+            const int parent = k < K ? s_par[i] : -1;
+            const bool last = t == steps_b - 1;
+            const bool valid = k < K && k < Kb && parent >= 0 && parent < Kb;  // malformed slots carry nothing
+            float d = 0.0f;
+            if (valid) {
+                float drank = 0.0f;
+                if (p.g_scores) drank = drank + s_gs[i];
+                if (last && p.g_final) drank = drank + p.g_final[static_cast<int64_t>(b) * K + k];
+                d = next + drank * s_ipen[i];
+                if (p.g_raw) d = d + s_graw[i];
+                if (last && p.g_final_raw) d = d + p.g_final_raw[static_cast<int64_t>(b) * K + k];
+            }
+            const bool flows = valid && d != 0.0f;
+            const float draw = flows ? d : 0.0f;
+            const int par = flows ? parent : -1;
+            if (k < K) s_draw[i] = (flows && s_emit[i]) ? d : 0.0f;
+            // each parent sums its children's draws in slot order
+            float sum = 0.0f;
+            for (int j = 0; j < K; ++j) {
+                const int pj = __builtin_amdgcn_readlane(par, j);
+                const float dj =
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, draw), j));
+                if (pj == k) sum = sum + dj;
+            }
+            next = sum;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < n; i += kWalkStageThreads) p.draws[base + i] = s_draw[i];
 }
 
 template <int DT>
@@ -387,9 +535,11 @@ hipError_t launch_dense_ot(const BackwardParams& p, hipStream_t stream) {
 // hands the trace to the caller). STAGED: the example's tokens and parents
 // are first copied into LDS by the whole workgroup (coalesced), so each
 // beam's walk back through the steps reads the LDS instead of waiting on one
-// dependent global load per step.
+// dependent global load per step. With `lengths` ([B, K] final lengths),
+// positions at and past each final beam's length are -1 as well.
 template <typename I, bool STAGED>
-__global__ void backtrack_kernel(const I* tokens, const I* parents, const I* steps, int T, int K, int64_t* seq) {
+__global__ void backtrack_kernel(const I* tokens, const I* parents, const I* steps, const I* lengths, int T, int K,
+                                 int64_t* seq) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int b = static_cast<int>(blockIdx.x);
     const int64_t steps_b = steps ? static_cast<int64_t>(steps[b]) : T;
@@ -407,6 +557,7 @@ __global__ void backtrack_kernel(const I* tokens, const I* parents, const I* ste
     for (int k = static_cast<int>(threadIdx.x); k < K; k += static_cast<int>(blockDim.x)) {
         int beam = k;
         int64_t* dst = seq + (static_cast<int64_t>(b) * K + k) * T;
+        const int64_t keep = lengths ? static_cast<int64_t>(lengths[static_cast<int64_t>(b) * K + k]) : T;
         for (int t = T - 1; t >= 0; --t) {
             if (t >= steps_b || beam < 0) {
                 dst[t] = -1;
@@ -414,10 +565,10 @@ __global__ void backtrack_kernel(const I* tokens, const I* parents, const I* ste
             }
             const int64_t slot = static_cast<int64_t>(t) * K + beam;
             if constexpr (STAGED) {
-                dst[t] = s_tok[slot];
+                dst[t] = t < keep ? s_tok[slot] : -1;
                 beam = s_par[slot];
             } else {
-                dst[t] = static_cast<int64_t>(tokens[base + slot]);
+                dst[t] = t < keep ? static_cast<int64_t>(tokens[base + slot]) : -1;
                 const int64_t next = static_cast<int64_t>(parents[base + slot]);
                 beam = next >= 0 && next < K ? static_cast<int>(next) : -1;  // a malformed parent ends the path
             }
@@ -434,7 +585,14 @@ size_t backward_workspace_bytes(int B, int T, int K) {
 
 hipError_t launch_path_walk(const BackwardParams& p, hipStream_t stream) {
     KernelTimer timer(kKindPathWalk, stream);
-    hipLaunchKernelGGL(path_walk_kernel, dim3(p.B), dim3(kWalkThreads), 0, stream, p);
+    if (p.K <= 64 && static_cast<int64_t>(p.T) * p.K <= kWalkStageSlots) {
+        hipLaunchKernelGGL(path_walk_staged_kernel, dim3(p.B), dim3(kWalkStageThreads), walk_stage_bytes(p), stream,
+                           p);
+    } else if (p.K <= 64) {
+        hipLaunchKernelGGL(path_walk_wave_kernel, dim3(p.B), dim3(64), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL(path_walk_kernel, dim3(p.B), dim3(kWalkThreads), 0, stream, p);
+    }
     return hipGetLastError();
 }
 
@@ -447,29 +605,89 @@ hipError_t launch_dense_gradient(const BackwardParams& p, hipStream_t stream) {
 }
 
 template <typename I>
-hipError_t launch_backtrack_t(const I* tokens, const I* parents, const I* steps, int B, int T, int K, int64_t* seq,
-                              hipStream_t stream) {
+hipError_t launch_backtrack_t(const I* tokens, const I* parents, const I* steps, const I* lengths, int B, int T, int K,
+                              int64_t* seq, hipStream_t stream) {
     const int threads = K < 256 ? ((K + 63) / 64) * 64 : 256;
     KernelTimer timer(kKindBacktrack, stream);
     const size_t staged = (sizeof(int64_t) + sizeof(int32_t)) * static_cast<size_t>(T) * static_cast<size_t>(K);
     if (staged <= 48 * 1024) {
         hipLaunchKernelGGL((backtrack_kernel<I, true>), dim3(B), dim3(threads), staged, stream, tokens, parents, steps,
-                           T, K, seq);
+                           lengths, T, K, seq);
     } else {
-        hipLaunchKernelGGL((backtrack_kernel<I, false>), dim3(B), dim3(threads), 0, stream, tokens, parents, steps, T,
-                           K, seq);
+        hipLaunchKernelGGL((backtrack_kernel<I, false>), dim3(B), dim3(threads), 0, stream, tokens, parents, steps,
+                           lengths, T, K, seq);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_backtrack(const int32_t* tokens, const int32_t* parents, const int32_t* steps, int B, int T, int K,
                             int64_t* seq, hipStream_t stream) {
-    return launch_backtrack_t(tokens, parents, steps, B, T, K, seq, stream);
+    return launch_backtrack_t<int32_t>(tokens, parents, steps, nullptr, B, T, K, seq, stream);
 }
 
-hipError_t launch_backtrack(const int64_t* tokens, const int64_t* parents, const int64_t* steps, int B, int T, int K,
-                            int64_t* seq, hipStream_t stream) {
-    return launch_backtrack_t(tokens, parents, steps, B, T, K, seq, stream);
+hipError_t launch_backtrack(const int64_t* tokens, const int64_t* parents, const int64_t* steps,
+                            const int64_t* lengths, int B, int T, int K, int64_t* seq, hipStream_t stream) {
+    return launch_backtrack_t<int64_t>(tokens, parents, steps, lengths, B, T, K, seq, stream);
+}
+
+namespace {
+
+constexpr int kRiskThreads = 256;
+
+// The expected cost of one example's beams under softmax(score / t) over its
+// live beams (finite scores), and each beam's gradient factor
+// scale * p_k (c_k - risk) / t (0 for dead beams). One workgroup per example,
+// beams strided over its threads; max and sums by wave reduction, then over
+// the wavefronts in LDS.
+__global__ __launch_bounds__(kRiskThreads) void risk_kernel(const float* scores, const float* costs, int K,
+                                                           float temperature, float scale, float* risk,
+                                                           float* factor) {
+    __shared__ float s_red[kRiskThreads / 64];
+    const int b = static_cast<int>(blockIdx.x);
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+    const float* s = scores + static_cast<int64_t>(b) * K;
+    const float* c = costs + static_cast<int64_t>(b) * K;
+    auto block_reduce = [&](float v, bool is_max) {
+        for (int off = 32; off > 0; off >>= 1) {
+            const float o = __shfl_xor(v, off);
+            v = is_max ? fmaxf(v, o) : v + o;
+        }
+        if (lane == 0) s_red[wave] = v;
+        __syncthreads();
+        float r = s_red[0];
+        for (int w = 1; w < kRiskThreads / 64; ++w) r = is_max ? fmaxf(r, s_red[w]) : r + s_red[w];
+        __syncthreads();
+        return r;
+    };
+    float m = -kInf;
+    for (int k = tid; k < K; k += kRiskThreads)
+        if (__builtin_fabsf(s[k]) < kInf) m = fmaxf(m, s[k] / temperature);
+    m = block_reduce(m, true);
+    const float shift = m > -kInf ? m : 0.0f;
+    float w_sum = 0.0f;
+    for (int k = tid; k < K; k += kRiskThreads)
+        if (__builtin_fabsf(s[k]) < kInf) w_sum += expf(s[k] / temperature - shift);
+    w_sum = block_reduce(w_sum, false);
+    const float inv = w_sum > 0.0f ? 1.0f / w_sum : 0.0f;
+    float r = 0.0f;
+    for (int k = tid; k < K; k += kRiskThreads)
+        if (__builtin_fabsf(s[k]) < kInf) r += expf(s[k] / temperature - shift) * inv * c[k];
+    r = block_reduce(r, false);
+    for (int k = tid; k < K; k += kRiskThreads) {
+        const bool live = __builtin_fabsf(s[k]) < kInf;
+        const float p = live ? expf(s[k] / temperature - shift) * inv : 0.0f;
+        factor[static_cast<int64_t>(b) * K + k] = live ? scale * p * (c[k] - r) / temperature : 0.0f;
+    }
+    if (tid == 0) risk[b] = r;
+}
+
+}  // namespace
+
+hipError_t launch_risk(const float* scores, const float* costs, int B, int K, float temperature, float scale,
+                       float* risk, float* factor, hipStream_t stream) {
+    hipLaunchKernelGGL(risk_kernel, dim3(B), dim3(kRiskThreads), 0, stream, scores, costs, K, temperature, scale,
+                       risk, factor);
+    return hipGetLastError();
 }
 
 }  // namespace dbs_hip

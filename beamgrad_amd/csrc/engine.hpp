@@ -236,7 +236,12 @@ hipError_t launch_path_walk(const BackwardParams& p, hipStream_t stream);
 hipError_t launch_dense_gradient(const BackwardParams& p, hipStream_t stream);
 hipError_t launch_backtrack(const int32_t* tokens, const int32_t* parents, const int32_t* steps, int B, int T, int K,
                             int64_t* seq, hipStream_t stream);
-hipError_t launch_backtrack(const int64_t* tokens, const int64_t* parents, const int64_t* steps, int B, int T, int K,
+hipError_t launch_backtrack(const int64_t* tokens, const int64_t* parents, const int64_t* steps,
+                            const int64_t* lengths, int B, int T, int K,
                             int64_t* seq, hipStream_t stream);
+// The minimum-risk loss of scores [B, K] under costs [B, K]: risk [B] and
+// the gradient factor [B, K] (scale * d risk_b / d score_bk).
+hipError_t launch_risk(const float* scores, const float* costs, int B, int K, float temperature, float scale,
+                       float* risk, float* factor, hipStream_t stream);
 
 }  // namespace dbs_hip

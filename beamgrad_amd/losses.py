@@ -26,35 +26,48 @@ _REDUCTIONS = ("mean", "sum", "none")
 
 
 class _ExpectedCost(torch.autograd.Function):
-    """Per-example risk [B] of scores [B, K] under costs [B, K]."""
+    """The loss (per-example risk [B], or its mean or sum) of scores [B, K]
+    under costs [B, K], and the factor [B, K] that turns the loss's incoming
+    gradient into the scores' gradient (the reduction's scale included). On
+    the GPU both come from one HIP launch (``beamgrad::minimum_risk``), the
+    reduction from one more; CPU tensors take the same formula in torch
+    operations. The backward is one multiplication."""
 
     generate_vmap_rule = True  # elementwise and last-dim reductions only
 
     @staticmethod
-    def forward(scores: torch.Tensor, costs: torch.Tensor, temperature: float):
-        live = torch.isfinite(scores)
-        z = torch.where(live, scores / temperature, float("-inf"))
-        top = z.amax(-1, keepdim=True)
-        # rows without a live beam: every weight is 0 (exp(-inf - 0))
-        w = torch.exp(z - torch.where(torch.isfinite(top), top, 0.0))
-        total = w.sum(-1, keepdim=True)
-        p = w / torch.where(total > 0, total, 1.0)
-        c = torch.where(live, costs.to(device=p.device, dtype=p.dtype), 0.0)
-        risk = (p * c).sum(-1)
-        return risk, p, c
+    def forward(scores: torch.Tensor, costs: torch.Tensor, temperature: float, reduction: str):
+        scale = 1.0 / scores.shape[0] if reduction == "mean" else 1.0
+        if scores.is_cuda:
+            risk, factor = torch.ops.beamgrad.minimum_risk(scores.float(), costs, temperature, scale)
+        else:
+            live = torch.isfinite(scores)
+            z = torch.where(live, scores / temperature, float("-inf"))
+            top = z.amax(-1, keepdim=True)
+            # rows without a live beam: every weight is 0 (exp(-inf - 0))
+            w = torch.exp(z - torch.where(torch.isfinite(top), top, 0.0))
+            total = w.sum(-1, keepdim=True)
+            p = w / torch.where(total > 0, total, 1.0)
+            c = torch.where(live, costs.to(device=p.device, dtype=p.dtype), 0.0)
+            risk = (p * c).sum(-1)
+            factor = (scale / temperature) * p * (c - risk[:, None])
+        loss = risk if reduction == "none" else (risk.sum() if reduction == "sum" else risk.mean())
+        return loss, factor
 
     @staticmethod
     def setup_context(ctx, inputs, output):
-        risk, p, c = output
-        ctx.save_for_backward(p, c, risk)
-        ctx.temperature = inputs[2]
-        ctx.mark_non_differentiable(p, c)
+        _loss, factor = output
+        ctx.save_for_backward(factor)
+        ctx.mark_non_differentiable(factor)
+        ctx.set_materialize_grads(False)
 
     @staticmethod
-    def backward(ctx, grad_risk: torch.Tensor, _grad_p, _grad_c):
-        p, c, risk = ctx.saved_tensors
-        g = (grad_risk / ctx.temperature)[:, None] * p * (c - risk[:, None])
-        return g, None, None
+    def backward(ctx, grad_loss, _grad_factor):
+        (factor,) = ctx.saved_tensors
+        if grad_loss is None:
+            return None, None, None, None
+        g = grad_loss[:, None] if grad_loss.dim() == 1 else grad_loss
+        return g * factor, None, None, None
 
 
 def minimum_risk(result: BeamSearchResult, costs: torch.Tensor, temperature: float = 1.0,
@@ -74,7 +87,4 @@ def minimum_risk(result: BeamSearchResult, costs: torch.Tensor, temperature: flo
         raise ValueError(f"costs must have the scores' shape {tuple(scores.shape)}, got {tuple(costs.shape)}")
     if reduction not in _REDUCTIONS:
         raise ValueError(f"reduction must be 'mean', 'sum' or 'none', got {reduction!r}")
-    risk = _ExpectedCost.apply(scores, costs, float(temperature))[0]
-    if reduction == "none":
-        return risk
-    return risk.sum() if reduction == "sum" else risk.mean()
+    return _ExpectedCost.apply(scores, costs, float(temperature), reduction)[0]

@@ -133,6 +133,39 @@ DBS_CUDA_EXPORT int dbs_hip_backtrack_i64(
     int64_t* sequences,
     void* stream);
 
+/* The sequences a search returns (reference python/beamgrad/_search.py:
+ * 258-311): dbs_hip_backtrack_i64's [B, K, T] tokens with, besides, -1 at
+ * and past each final beam's length (final_lengths int64 [B, K]). One launch. */
+DBS_CUDA_EXPORT int dbs_hip_search_sequences(
+    const int64_t* tokens,
+    const int64_t* parents,
+    const int64_t* steps_per_example,
+    const int64_t* final_lengths,
+    int batch_size,
+    int steps,
+    int beam_size,
+    int64_t* sequences,
+    void* stream);
+
+/* The minimum-risk loss of the final beams in one launch (the objective of
+ * reference python/beamgrad/losses.py:139-169): for each example b,
+ * risk[b] = sum_k p_k c_k with p = softmax(scores[b] / temperature) over its
+ * live beams (finite scores; dead beams get no probability and their costs
+ * are not read), and grad_factor[b, k] = scale * p_k (c_k - risk[b]) /
+ * temperature, the gradient of scale * risk[b] w.r.t. scores[b, k] (0 for
+ * dead beams). An example without a live beam has risk 0. scores and costs
+ * are float32 [B, K] on the device; temperature finite and positive. */
+DBS_CUDA_EXPORT int dbs_hip_minimum_risk(
+    const float* scores,
+    const float* costs,
+    int batch_size,
+    int beam_size,
+    float temperature,
+    float scale,
+    float* risk,
+    float* grad_factor,
+    void* stream);
+
 /* A decode trace's outputs in the dtypes torch returns them in, in one
  * launch: final_lengths [B, K], tokens, parents and lengths [B, T, K] as
  * int64, from_logprob [B, T, K] as 0/1 bytes (torch bool), and the

@@ -177,3 +177,62 @@ def test_step_api_equals_decode(oracle, seed, constrained):
     assert torch.equal(scores, want.scores)
     assert torch.equal(final, want.final_scores) and torch.equal(raw, want.final_raw_scores)
     assert torch.equal(lengths, want.final_lengths.int())
+
+
+@pytest.mark.parametrize("K", [1, 8, 300])
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+def test_minimum_risk_kernel_closed_form(K, reduction):
+    """The GPU loss (one HIP launch, beamgrad::minimum_risk) against the
+    closed form in float64: risk_b = sum_k p_k c_k over the live beams with
+    p = softmax(s / t), gradient p_k (c_k - risk_b) / t (times 1 / B for the
+    mean); dead beams (-inf) get no probability and their costs (NaN here)
+    are not read; an example without a live beam has risk 0. K = 300 takes
+    more beams than the kernel has threads."""
+    from collections import namedtuple
+
+    rng = np.random.default_rng(K)
+    B, t = 5, 0.7
+    s = rng.normal(0, 3, (B, K))
+    dead = rng.random((B, K)) < 0.2
+    dead[3, :] = True
+    s[dead] = -np.inf
+    c = rng.random((B, K))
+    c[dead] = np.nan
+    want_risk = np.zeros(B)
+    want_grad = np.zeros((B, K))
+    for b in range(B):
+        live = ~dead[b]
+        if not live.any():
+            continue
+        z = s[b, live] / t
+        p = np.exp(z - z.max())
+        p /= p.sum()
+        want_risk[b] = (p * c[b, live]).sum()
+        want_grad[b, live] = p * (c[b, live] - want_risk[b]) / t
+    scale = 1.0 / B if reduction == "mean" else 1.0
+    R = namedtuple("R", "scores")
+    st = torch.tensor(s, dtype=torch.float32, device="cuda", requires_grad=True)
+    loss = bg.losses.minimum_risk(R(st), torch.tensor(c, dtype=torch.float32, device="cuda"), t, reduction)
+    want_loss = {"mean": want_risk.mean(), "sum": want_risk.sum(), "none": want_risk}[reduction]
+    np.testing.assert_allclose(loss.detach().double().cpu().numpy(), want_loss, rtol=2e-6, atol=1e-7)
+    loss.sum().backward()
+    np.testing.assert_allclose(st.grad.double().cpu().numpy(), want_grad * scale, rtol=2e-5, atol=1e-7)
+    assert torch.isfinite(st.grad).all()
+
+
+def test_decode_trace_engine_outputs():
+    """decode_trace's widened trace and its engine trace (outputs 11-14, what
+    the backward reads) against decode_ex's own outputs, bit for bit."""
+    rng = np.random.default_rng(2)
+    x = torch.from_numpy(rng.normal(0, 2, (3, 6, 4, 257)).astype(np.float32)).cuda()
+    args = (x, True, None, 5, 1, 0.6, None, 0, 1.0, True, [])
+    ex = torch.ops.beamgrad.decode_ex(*args)
+    tr = torch.ops.beamgrad.decode_trace(*args)
+    for i in (0, 1, 6, 7, 9):
+        assert torch.equal(ex[i].view(torch.int32), tr[i].view(torch.int32)), i
+    for i, j in ((2, 2), (3, 3), (4, 4), (5, 5)):
+        assert torch.equal(ex[i].long(), tr[j]), i
+    assert torch.equal(ex[8].bool(), tr[8])
+    assert torch.equal(tr[10], torch.full((3,), 6, dtype=torch.long, device="cuda"))
+    for i, j in ((4, 11), (3, 12), (5, 13), (8, 14)):
+        assert tr[j].dtype == ex[i].dtype and torch.equal(ex[i], tr[j]), j
