@@ -186,22 +186,30 @@ __global__ __launch_bounds__(64) void path_walk_wave_kernel(BackwardParams p) {
 }
 
 // path_walk_wave_kernel with the example's trace in LDS (T * K up to
-// kWalkStageSlots): the workgroup's four wavefronts first stage every slot's
-// parent, inverse length penalty, incoming score gradients and whether its
-// draw is emitted (from a log-prob entry with a token in range), all loads
-// in flight at once; wavefront 0 then walks reading only LDS and writes the
-// draws to LDS; after a barrier the four wavefronts store them. The serial
-// loop holds no global memory round trip and no division.
+// kWalkStageSlots). The workgroup's four wavefronts first stage, per slot,
+// everything of the walk that does not depend on the later steps, with all
+// loads in flight at once: the parent (-1 for a malformed slot), the product
+// of the slot's score gradient (the final one added at the last step) and
+// its inverse length penalty, the raw-score gradient and whether the draw is
+// emitted (from a log-prob entry with a token in range). Wavefront 0 then
+// walks reading only LDS, the next step's slot read while a step is walked,
+// and writes the draws to LDS; after a barrier the four wavefronts store
+// them. The serial loop holds no global memory round trip and no division;
+// every value is rounded as in the one-wavefront walk.
 constexpr int kWalkStageThreads = 256;
-constexpr int kWalkStageSlots = 2560;  // at most 25 bytes a slot: 64000 bytes of LDS
+constexpr int kWalkStageSlots = 3072;  // at most 17 bytes a slot in LDS
 
 size_t walk_stage_bytes(const BackwardParams& p) {
-    const size_t per = 3 * sizeof(float) + (p.g_scores ? sizeof(float) : 0) + (p.g_raw ? sizeof(float) : 0) + 1;
+    const size_t per = 3 * sizeof(float) + (p.g_raw ? sizeof(float) : 0) + 1;
     return per * static_cast<size_t>(p.T) * static_cast<size_t>(p.K);
 }
 
+// KMAX (a power of two >= K): the children loop is unrolled over KMAX lanes;
+// lanes from K on hold parent -1, so they match no slot.
+template <int KMAX>
 __global__ __launch_bounds__(kWalkStageThreads) void path_walk_staged_kernel(BackwardParams p) {
     extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float s_gfr[64];
     const int b = static_cast<int>(blockIdx.x);
     const int tid = static_cast<int>(threadIdx.x);
     const int K = p.K, T = p.T, V = p.V;
@@ -214,51 +222,70 @@ __global__ __launch_bounds__(kWalkStageThreads) void path_walk_staged_kernel(Bac
         p.draws[base + i] = 0.0f;
     const int n = steps_b * K;
     int32_t* s_par = reinterpret_cast<int32_t*>(smem);
-    float* s_ipen = reinterpret_cast<float*>(s_par + n);
-    float* s_draw = s_ipen + n;
-    float* s_gs = s_draw + n;
-    float* s_graw = s_gs + (p.g_scores ? n : 0);
+    float* s_a = reinterpret_cast<float*>(s_par + n);
+    float* s_draw = s_a + n;
+    float* s_graw = s_draw + n;
     uint8_t* s_emit = reinterpret_cast<uint8_t*>(s_graw + (p.g_raw ? n : 0));
     for (int i = tid; i < n; i += kWalkStageThreads) {
         const int64_t g = base + i;
-        s_par[i] = p.parents[g];
-        s_ipen[i] = 1.0f / length_penalty(p.lengths[g], p.alpha);
+        const int k = i % K;
+        const int parent = p.parents[g];
+        s_par[i] = k < Kb && parent >= 0 && parent < Kb ? parent : -1;  // malformed slots carry nothing
+        float drank = 0.0f;
+        if (p.g_scores) drank = drank + p.g_scores[g];
+        if (i >= n - K && p.g_final) drank = drank + p.g_final[static_cast<int64_t>(b) * K + k];
+        const float inv_pen = 1.0f / length_penalty(p.lengths[g], p.alpha);
+        s_a[i] = drank * inv_pen;
         const int tok = p.tokens[g];
         s_emit[i] = p.from_logprob[g] != 0 && tok >= 0 && tok < V;
-        if (p.g_scores) s_gs[i] = p.g_scores[g];
         if (p.g_raw) s_graw[i] = p.g_raw[g];
     }
+    if (tid < K) s_gfr[tid] = p.g_final_raw ? p.g_final_raw[static_cast<int64_t>(b) * K + tid] : 0.0f;
     __syncthreads();
     if (tid < 64) {
         const int k = tid;
+        const int kc = k < K ? k : K - 1;  // lanes past K read slot K - 1 and drop it
+        struct Slot {
+            int par;
+            float a, graw;
+            bool emit;
+        };
+        auto read_slot = [&](int t) -> Slot {
+            const int i = t * K + kc;
+            Slot s;
+            s.par = k < K ? s_par[i] : -1;
+            s.a = s_a[i];
+            s.graw = p.g_raw ? s_graw[i] : 0.0f;
+            s.emit = s_emit[i] != 0;
+            return s;
+        };
         float next = 0.0f;  // the slot's incoming gradient from the later steps
+        Slot cur = steps_b > 0 ? read_slot(steps_b - 1) : Slot{-1, 0.0f, 0.0f, false};
         for (int t = steps_b - 1; t >= 0; --t) {
-            const int i = t * K + k;
-            const int parent = k < K ? s_par[i] : -1;
-            const bool last = t == steps_b - 1;
-            const bool valid = k < K && k < Kb && parent >= 0 && parent < Kb;  // malformed slots carry nothing
+            const Slot nxt = t > 0 ? read_slot(t - 1) : cur;
             float d = 0.0f;
-            if (valid) {
-                float drank = 0.0f;
-                if (p.g_scores) drank = drank + s_gs[i];
-                if (last && p.g_final) drank = drank + p.g_final[static_cast<int64_t>(b) * K + k];
-                d = next + drank * s_ipen[i];
-                if (p.g_raw) d = d + s_graw[i];
-                if (last && p.g_final_raw) d = d + p.g_final_raw[static_cast<int64_t>(b) * K + k];
+            if (cur.par >= 0) {
+                d = next + cur.a;
+                if (p.g_raw) d = d + cur.graw;
+                if (t == steps_b - 1 && p.g_final_raw) d = d + s_gfr[k];
             }
-            const bool flows = valid && d != 0.0f;
+            const bool flows = cur.par >= 0 && d != 0.0f;
             const float draw = flows ? d : 0.0f;
-            const int par = flows ? parent : -1;
-            if (k < K) s_draw[i] = (flows && s_emit[i]) ? d : 0.0f;
-            // each parent sums its children's draws in slot order
+            const int par = flows ? cur.par : -1;
+            if (k < K) s_draw[t * K + k] = (flows && cur.emit) ? d : 0.0f;
+            // each parent sums its children's draws in slot order (a child's
+            // draw is never +-0, and a sum of them never -0, so adding +0
+            // for the other lanes changes nothing)
             float sum = 0.0f;
-            for (int j = 0; j < K; ++j) {
+#pragma unroll
+            for (int j = 0; j < KMAX; ++j) {
                 const int pj = __builtin_amdgcn_readlane(par, j);
                 const float dj =
                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, draw), j));
-                if (pj == k) sum = sum + dj;
+                sum = sum + (pj == k ? dj : 0.0f);
             }
             next = sum;
+            cur = nxt;
         }
     }
     __syncthreads();
@@ -586,8 +613,12 @@ size_t backward_workspace_bytes(int B, int T, int K) {
 hipError_t launch_path_walk(const BackwardParams& p, hipStream_t stream) {
     KernelTimer timer(kKindPathWalk, stream);
     if (p.K <= 64 && static_cast<int64_t>(p.T) * p.K <= kWalkStageSlots) {
-        hipLaunchKernelGGL(path_walk_staged_kernel, dim3(p.B), dim3(kWalkStageThreads), walk_stage_bytes(p), stream,
-                           p);
+        const dim3 g(p.B), blk(kWalkStageThreads);
+        const size_t lds = walk_stage_bytes(p);
+        if (p.K <= 8) hipLaunchKernelGGL(path_walk_staged_kernel<8>, g, blk, lds, stream, p);
+        else if (p.K <= 16) hipLaunchKernelGGL(path_walk_staged_kernel<16>, g, blk, lds, stream, p);
+        else if (p.K <= 32) hipLaunchKernelGGL(path_walk_staged_kernel<32>, g, blk, lds, stream, p);
+        else hipLaunchKernelGGL(path_walk_staged_kernel<64>, g, blk, lds, stream, p);
     } else if (p.K <= 64) {
         hipLaunchKernelGGL(path_walk_wave_kernel, dim3(p.B), dim3(64), 0, stream, p);
     } else {
