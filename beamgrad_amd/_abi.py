@@ -127,6 +127,7 @@ SIGNATURES = {
     "dbs_hip_profile_read": (C.c_int, [C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
     "dbs_hip_set_row_pass": (C.c_int, [C.c_int]),
     "dbs_hip_set_decode_overlap": (C.c_int, [C.c_int]),
+    "dbs_hip_set_select_pass": (C.c_int, [C.c_int]),
 }
 
 

@@ -727,6 +727,11 @@ DBS_CUDA_EXPORT int dbs_hip_set_row_pass(int kind) {
     return dbs_hip::g_row_pass_kind.exchange(kind);
 }
 
+DBS_CUDA_EXPORT int dbs_hip_set_select_pass(int kind) {
+    if (kind < 0 || kind > 1) return -2;
+    return dbs_hip::g_select_kind.exchange(kind);
+}
+
 DBS_CUDA_EXPORT int dbs_hip_profile_enable(int on) {
     if (on != 0 && on != 1) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lock(g_profile_mutex);

@@ -265,7 +265,8 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
         e = aux_for(device, stream, aux);
         if (e != hipSuccess) return e;
     }
-    if (!aux || 2 * p.B > aux->cus) {
+    const int reserve = select_reserve_cus(p);
+    if (!aux || 2 * reserve > aux->cus) {
         e = launch_row_pass(p, stream);
         if (e != hipSuccess) return e;
         return launch_select(p, L.sel, stream);
@@ -275,7 +276,7 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     p.step_done = reinterpret_cast<int32_t*>(sync);
     p.fault = reinterpret_cast<int32_t*>(sync + counts);
     p.row_ticket = reinterpret_cast<unsigned long long*>(sync + counts + 8);
-    p.reserve_cus = p.B;  // a persistent row pass would otherwise hold every CU until it ends
+    p.reserve_cus = reserve;  // a persistent row pass would otherwise hold every CU until it ends
     wait_policy(p);
     std::lock_guard<std::mutex> lock(aux->mutex);
     // the counters, and the RowInfo and shortlist words (tag 0: not written)

@@ -124,6 +124,15 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     return bits_f32(static_cast<uint32_t>(__builtin_amdgcn_readlane(x, 63)));
 }
 
+// Workgroup barrier for LDS data only: the wavefront's LDS operations have
+// completed; its global loads and stores may still be in flight across it
+// (the barrier orders nothing in global memory).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Orders the LDS accesses of one wavefront (its lanes run in lockstep and the
 // LDS serves a wavefront's requests in issue order).
 __device__ __forceinline__ void wave_sync() {

@@ -178,6 +178,13 @@ hipError_t launch_row_logprob(const DecodeParams& p, int64_t rows, hipStream_t s
 extern std::atomic<int> g_row_pass_kind;  // dbs_hip_set_row_pass
 hipError_t launch_row_pipe(const DecodeParams& p, int64_t rows, hipStream_t stream);
 hipError_t launch_select(const DecodeParams& p, const SelectLayout& L, hipStream_t stream);
+// The select pass runs one wavefront per example (narrow, unconstrained
+// decodes with shortlists) instead of one workgroup; dbs_hip_set_select_pass
+// (g_select_kind 1) keeps the workgroup pass.
+bool select_narrow(const DecodeParams& p);
+extern std::atomic<int> g_select_kind;
+// CUs the overlapped decode leaves free for the select pass.
+int select_reserve_cus(const DecodeParams& p);
 
 // Rows the select pass rescanned in full (reset = 1 clears the count).
 hipError_t rescan_counter(int reset, unsigned long long* value);

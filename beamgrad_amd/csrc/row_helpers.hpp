@@ -55,13 +55,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const uint16_t* row
 typedef unsigned int v2u32 __attribute__((ext_vector_type(2)));
 typedef unsigned int v4u32 __attribute__((ext_vector_type(4)));
 
-// Workgroup barrier for LDS data only: the wavefront's LDS operations have
-// completed; its global loads may still be in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
 
 template <int DT>
 __device__ __forceinline__ float pattern_value(uint32_t h) {

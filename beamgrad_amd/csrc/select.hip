@@ -99,6 +99,16 @@ struct Lds {
     int sig_shift;    // 32 - log2(32 sig_words): hash bits kept
 };
 
+// The select pass's barriers order LDS only (lds_barrier): a step's global
+// loads (the next step's prefetch) and its trace stores stay in flight across
+// them. The beams' prefixes and n-gram-blocked lists live in global memory
+// when LDS cannot hold them (long constrained decodes); the barriers after
+// they are written then also wait for global memory.
+__device__ __forceinline__ void step_barrier(bool lists_global) {
+    if (lists_global) __syncthreads();
+    else lds_barrier();
+}
+
 struct State {
     int gave_up;  // a wait of the overlapped decode gave up
     int first_bad;  // the first invalid row read (t * K + k), else INT_MAX
@@ -212,7 +222,7 @@ __device__ __forceinline__ void sort_cands(Cand* buf, int np) {
                     }
                 }
             }
-            __syncthreads();
+            lds_barrier();
         }
     }
 }
@@ -289,7 +299,7 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
         if (by_score) s.part[tid] = static_cast<int32_t>(tid < n ? ordered_key(c.score) : 0u);
     }
     if (by_score && tid == 0) s.nsurv[0] = 0;
-    __syncthreads();
+    lds_barrier();
     if (by_score) {
         if (tid < n) {
             const uint32_t mine = ordered_key(c.score);
@@ -313,7 +323,7 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
                 if (slot < 64) s.surv[slot] = tid;
             }
         }
-        __syncthreads();
+        lds_barrier();
         const int ns = __builtin_amdgcn_readfirstlane(s.nsurv[0]);
         if (ns <= 64) {
             if (tid < ns) {
@@ -329,7 +339,7 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
                 if (rank == K - 1 && before(ci, st.thr)) st.thr = ci;
             }
             if (tid == 0) st.count = n < K ? n : K;
-            __syncthreads();
+            lds_barrier();
             return;
         }
         // many equal scores: every candidate is ranked
@@ -366,7 +376,7 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
         }
     }
     s.part[tid] = part;
-    __syncthreads();
+    lds_barrier();
     if (tid < n) {
         const int gi_t = tid >> 6;
         int rank = 0;
@@ -375,13 +385,13 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
         if (rank == K - 1 && before(c, st.thr)) st.thr = c;
     }
     if (tid == 0) st.count = n < K ? n : K;
-    __syncthreads();
+    lds_barrier();
 }
 
 // Sorts the collected candidates, keeps the best K, and raises the admission
 // threshold to the K-th kept one when that is better.
 __device__ __forceinline__ void compact(Lds& s, State& st, int K) {
-    __syncthreads();
+    lds_barrier();
     const int n = __builtin_amdgcn_readfirstlane(st.count);
     if (n <= kRankMax) {
         compact_by_rank(s, st, K, n);
@@ -390,13 +400,13 @@ __device__ __forceinline__ void compact(Lds& s, State& st, int K) {
     int np = 1;
     while (np < n) np <<= 1;
     for (int i = n + static_cast<int>(threadIdx.x); i < np; i += kSelectThreads) s.buf[i] = dead_cand();
-    __syncthreads();
+    lds_barrier();
     sort_cands(s.buf, np);
     if (threadIdx.x == 0) {
         st.count = n < K ? n : K;
         if (st.count == K && before(s.buf[K - 1], st.thr)) st.thr = s.buf[K - 1];
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Admits c unless it ranks after the threshold (a candidate offered earlier,
@@ -409,7 +419,7 @@ __device__ __forceinline__ void offer(Lds& s, State& st, const Cand& c) {
 }
 
 __device__ __forceinline__ void end_round(Lds& s, State& st, int K, int sort_cap) {
-    __syncthreads();
+    lds_barrier();
     if (st.count > sort_cap - kSelectThreads) compact(s, st, K);
 }
 
@@ -429,7 +439,7 @@ __device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State&
         st.rcount = 0;
         st.overflow = 0;
     }
-    __syncthreads();
+    lds_barrier();
     const Cand thr = st.thr;
     for (int v0 = 0; v0 < V; v0 += kSelectThreads * kRescanPerThread) {
         float xs[kRescanPerThread];
@@ -455,7 +465,7 @@ __device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State&
             else st.overflow = 1;
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (!st.overflow) {
         const int n = st.rcount;
         for (int r0 = 0; r0 < n; r0 += kSelectThreads) {
@@ -522,6 +532,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     s.sig = L.sig_in_lds && !p.step_mode ? reinterpret_cast<uint32_t*>(smem + L.off_sig) : nullptr;
     s.sig_words = L.sig_words;
     s.sig_shift = L.sig_words == kSigWordsMax ? 19 : 21;
+    const bool lists_global = p.constrained && (!L.prefix_in_lds || !L.blk_in_lds);
 
     const int steps_b = p.step_mode ? 1 : example_steps(p, b);
     // this example's beams (slots past them stay empty) and EOS token
@@ -558,7 +569,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         st.gave_up = 0;
         st.first_bad = 0x7fffffff;
     }
-    __syncthreads();
+    lds_barrier();
 
     // Prefetch (the row pass has finished before this kernel: not the
     // overlapped decode): the next step's RowInfo and shortlists sit at fixed
@@ -610,7 +621,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             // example's remaining steps are padding and it is reported
             // invalid.
             if (tid == 0 && !st.gave_up && !wait_step_rows(p, b, t)) st.gave_up = 1;
-            __syncthreads();
+            lds_barrier();
             if (st.gave_up) {
                 pad_step(trace0);
                 continue;
@@ -661,7 +672,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         }
         if (coherent) {
             // a shortlist is read only as far as its row's count
-            __syncthreads();
+            lds_barrier();
             if (st.gave_up) {
                 pad_step(trace0);
                 continue;
@@ -729,7 +740,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             have_pf = t + 1 < steps_b;
             if (have_pf) prefetch(t + 1);
         }
-        __syncthreads();
+        lds_barrier();
         if (coherent && st.gave_up) {
             pad_step(trace0);
             continue;
@@ -754,7 +765,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                     s.blk[static_cast<int64_t>(k) * P + slot] = pre.tok[i + n - 1];
                 }
             }
-            __syncthreads();
+            step_barrier(lists_global);
         }
         if (p.use_tau) {
             // Lower bounds of the K-th best expanded raw (unconstrained: raw =
@@ -781,7 +792,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 v = i < s.rcount[k] ? s.raw[k] + s.sl[sl_at(k, i, SL)].lp : -kInf;
                 vk[tid] = make_uint2(0xffffffffu - static_cast<uint32_t>(tid), ordered_key(v));
             }
-            if (K >= kWideBeam) __syncthreads();  // (a) and the keys are in
+            if (K >= kWideBeam) lds_barrier();  // (a) and the keys are in
             if (K >= kWideBeam && tid < nv) {
                 const uint32_t mlo = 0xffffffffu - static_cast<uint32_t>(tid), mhi = ordered_key(v);
                 const uint4* w4 = reinterpret_cast<const uint4*>(vk);
@@ -804,7 +815,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 }
                 if (rank == K - 1 && v > st.tau) st.tau = v;
             }
-            __syncthreads();
+            lds_barrier();
         }
 
         // Carried-forward beams (reference src/decoder.cpp:131-139).
@@ -858,7 +869,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 s.part[64 + k] = n;
                 if (tid == 0) st.rcount = base + total <= L.sort_cap ? base + total : -1;
             }
-            __syncthreads();
+            lds_barrier();
             one_pass = st.rcount >= 0;
             if (one_pass) {
                 const int k = tid & 63, w = tid >> 6;
@@ -922,7 +933,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 atomicOr(&st.any_fail, 1);
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (st.any_fail) {
             for (int k = 0; k < K; ++k) {
                 if (s.rcount[k] != -3) continue;
@@ -930,7 +941,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 // drop the row's shortlisted candidates, then offer the whole row
                 for (int i = tid; i < st.count; i += kSelectThreads)
                     if (s.buf[i].parent == k && s.buf[i].flp) s.buf[i] = dead_cand();
-                __syncthreads();
+                lds_barrier();
                 const float praw = s.raw[k];
                 const int new_len = s.len[k] + 1;
                 const int64_t row = p.step_mode ? static_cast<int64_t>(b) * K + k : trace0 + k;
@@ -962,7 +973,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                     c.parent >= 0 ? s.plen[cur * K + c.parent] + ((c.flp && c.token >= 0) ? 1 : 0) : 0;
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (p.constrained && !p.step_mode) {
             // each selected beam: its parent's prefix, then its token, and
             // the signature of both (one pass over every beam's positions)
@@ -1009,7 +1020,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             s.last[k] = s.nlast[k];
             s.ended[k] = s.nended[k];
         }
-        __syncthreads();
+        step_barrier(lists_global);
     }
 
     if (st.gave_up) {
@@ -1019,7 +1030,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             s.len[k] = 0;
         }
         if (tid == 0 && p.fault) __hip_atomic_store(p.fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
+        lds_barrier();
     }
     // Final scores (reference src/decoder.cpp:179-187) and the state (step mode).
     for (int k = tid; k < K; k += kSelectThreads) {
@@ -1037,6 +1048,531 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     // example did not complete (an overlapped wait gave up)
     if (tid == 0 && p.invalid) p.invalid[b] = static_cast<uint8_t>(st.gave_up ? 2 : (st.invalid != 0 ? 1 : 0));
     if (tid == 0 && p.first_invalid) p.first_invalid[b] = st.first_bad == 0x7fffffff ? -1 : st.first_bad;
+}
+
+// ---------------------------------------------------------------------------
+// The narrow select pass: decodes with at most kNarrowMaxK beams, shortlists
+// and neither n-gram blocking, a repetition penalty nor the step API take
+// one wavefront per example, up to kNarrowWaves examples per workgroup (a CU
+// beside a persistent row pass takes one workgroup of the select pass at a
+// time, so the overlapped decode leaves about B / kNarrowWaves CUs to it,
+// the same number on each XCD). Lane k holds beam
+// k's state in registers, and a step has no workgroup barrier and few LDS
+// round trips:
+//   * RowInfo of each read row (lane k) and the shortlists (LDS);
+//   * tau, the largest fl(p_k + lp) over the K-th entries of the beams'
+//     shortlists (as in the workgroup pass): at least K candidates reach it,
+//     so none below it is selected;
+//   * the survivors, each beam's entries that reach tau (a prefix of its
+//     shortlist: fl(p_k + lp) is monotone in lp), and the carried-forward
+//     beams. Up to 64 are ranked in the lanes (the count of candidates before
+//     each one); more go through a running list of the best Kb in lanes
+//     0 .. Kb - 1 (insertion in order, as keep_best);
+//   * the workgroup pass's exactness check; when a row fails it, the
+//     selection is redone through the running list from the passing rows'
+//     survivors, the carried-forward beams and every token of the failing
+//     rows (the candidate set only grows, so rows that passed still pass);
+//   * the trace and the next state.
+// The kept set is the best Kb of the same candidates under the same total
+// order as the workgroup pass, so the trace is the same bit for bit.
+constexpr int kNarrowMaxK = 16;       // the running list lives in one 16-lane DPP row
+constexpr int kNarrowPf = 4;          // 16-byte prefetch registers per lane (K * M <= 512)
+constexpr int kNarrowPenCap = 1024;   // lengths with a penalty in LDS (larger ones are computed)
+constexpr int kNarrowRescanUnroll = 16;
+constexpr int kNarrowTagLoads = 4;    // tagged shortlist loads per lane in flight (overlapped decode)
+constexpr int kNarrowWaves = 4;       // examples (wavefronts) per workgroup, at most: one workgroup per CU
+constexpr int kXcds = 8;              // MI355X: 8 XCDs of 32 CUs
+constexpr int kNarrowWaveLds = 16384; // LDS per wavefront, at most (else the workgroup pass)
+
+// rank += (96-bit key j > key i): the borrow out of i - j.
+__device__ __forceinline__ void count_above96(int& rank, uint32_t i0, uint32_t i1, uint32_t i2, uint32_t j0,
+                                              uint32_t j1, uint32_t j2) {
+    uint32_t t;
+    asm("v_sub_co_u32 %0, vcc, %2, %5\n\t"
+        "v_subb_co_u32 %0, vcc, %3, %6, vcc\n\t"
+        "v_subb_co_u32 %0, vcc, %4, %7, vcc\n\t"
+        "v_addc_co_u32 %1, vcc, 0, %1, vcc"
+        : "=&v"(t), "+v"(rank)
+        : "v"(i0), "v"(i1), "v"(i2), "v"(j0), "v"(j1), "v"(j2)
+        : "vcc");
+}
+
+// Lane j's candidate, wave-uniform.
+__device__ __forceinline__ Cand lane_cand(const Cand& c, int j) {
+    Cand r;
+    r.score = bits_f32(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(f32_bits(c.score)), j)));
+    r.raw = bits_f32(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(f32_bits(c.raw)), j)));
+    r.parent = __builtin_amdgcn_readlane(c.parent, j);
+    r.token = __builtin_amdgcn_readlane(c.token, j);
+    r.length = __builtin_amdgcn_readlane(c.length, j);
+    r.flp = __builtin_amdgcn_readlane(c.flp, j);
+    return r;
+}
+
+// The value of lane - 1 (row_shr:1 within a 16-lane row; lane 0 keeps x).
+__device__ __forceinline__ int from_lane_below(int x) { return __builtin_amdgcn_update_dpp(x, x, 0x111, 0xf, 0xf, false); }
+
+// The running list: lanes [0, n) hold the best candidates so far, best first
+// (dead past what it holds); thr is its last entry (wave-uniform). c
+// (wave-uniform) goes in when it ranks before thr.
+__device__ __forceinline__ void list_insert(Cand& top, Cand& thr, const Cand& c, int n, int lane) {
+    if (!before(c, thr)) return;
+    const bool above = lane < n && before(top, c);
+    const int pos = __popcll(__builtin_amdgcn_ballot_w64(above));  // the list is sorted: a prefix stays
+    Cand prev;
+    prev.score = bits_f32(static_cast<uint32_t>(from_lane_below(static_cast<int>(f32_bits(top.score)))));
+    prev.raw = bits_f32(static_cast<uint32_t>(from_lane_below(static_cast<int>(f32_bits(top.raw)))));
+    prev.parent = from_lane_below(top.parent);
+    prev.token = from_lane_below(top.token);
+    prev.length = from_lane_below(top.length);
+    prev.flp = from_lane_below(top.flp);
+    if (lane == pos) top = c;
+    else if (lane > pos) top = prev;
+    thr = lane_cand(top, n - 1);
+}
+
+// Offers every lane's candidate where `offer` is set, in lane order.
+__device__ __forceinline__ void list_offer(Cand& top, Cand& thr, const Cand& c, bool offer, int n, int lane) {
+    uint64_t m = __builtin_amdgcn_ballot_w64(offer && before(c, thr));
+    while (m != 0) {
+        const int j = __ffsll(static_cast<long long>(m)) - 1;
+        m &= m - 1;
+        list_insert(top, thr, lane_cand(c, j), n, lane);
+    }
+}
+
+template <int DT, bool LOGITS, bool PF>
+__global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(DecodeParams p, int pen_len, int wave_bytes) {
+    extern __shared__ __align__(16) unsigned char smem_all[];
+    const int K = p.K, T = p.T, M = p.M, V = p.V;
+    // up to kNarrowWaves examples per workgroup, one per wavefront, each with
+    // its own LDS; the wavefronts never wait for each other
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+    const int b = static_cast<int>(blockIdx.x) * (static_cast<int>(blockDim.x) >> 6) + wave;
+    const int lane = static_cast<int>(threadIdx.x) & 63;
+    if (b >= p.B) return;
+    unsigned char* smem = smem_all + static_cast<size_t>(wave) * wave_bytes;
+    uint4* s_key = reinterpret_cast<uint4*>(smem);                   // [64] rank keys
+    ShortEntry* s_sl = reinterpret_cast<ShortEntry*>(smem + 1024);  // [K * M], beam k's list at k * M
+    Cand* s_cand = reinterpret_cast<Cand*>(smem + 1024 + sizeof(ShortEntry) * static_cast<size_t>(K) * M);  // [64]
+    float* s_pen = reinterpret_cast<float*>(s_cand + 64);  // [pen_len]
+    float* s_inv = s_pen + pen_len;                        // [pen_len]
+    for (int l = lane; l < pen_len; l += 64) {
+        const float pl = length_penalty(l, p.alpha);
+        s_pen[l] = pl;
+        s_inv[l] = 1.0f / pl;
+    }
+    auto pen_at = [&](int l) {
+        const int c = l > 1 ? l : 1;
+        return c < pen_len ? s_pen[c] : length_penalty(c, p.alpha);
+    };
+    auto inv_at = [&](int l) {
+        const int c = l > 1 ? l : 1;
+        return c < pen_len ? s_inv[c] : 1.0f / length_penalty(c, p.alpha);
+    };
+    const int steps_b = example_steps(p, b);
+    const int Kb = beams_of(p, b), eos_b = eos_of(p, b);
+    const bool coherent = p.step_done != nullptr;
+    const bool beam = lane < K;
+    const Cand dead = dead_cand();
+
+    // beam `lane`'s state (reference src/decoder.cpp:46-56)
+    float raw = lane == 0 ? 0.0f : -kInf;
+    int len = 0, last = -1;
+    bool ended = false;
+    bool gave_up = false, any_invalid = false;
+    int first_bad = 0x7fffffff;
+
+    // the next step's RowInfo and shortlists (all rows written before this
+    // kernel started: not the overlapped decode)
+    // (four named registers: an array here would be kept in scratch memory)
+    static_assert(kNarrowPf == 4, "four prefetch registers");
+    uint4 pf0 = make_uint4(0u, 0u, 0u, 0u), pf1 = pf0, pf2 = pf0, pf3 = pf0, pf_info = pf0;
+    auto prefetch = [&](int tn) __attribute__((always_inline)) {
+        const int64_t base = (static_cast<int64_t>(b) * T + tn) * K;
+        if (beam) pf_info = reinterpret_cast<const uint4*>(p.rowinfo)[base + lane];
+        const uint4* src4 = reinterpret_cast<const uint4*>(p.shortlist + base * M);
+        const int n4 = K * M / 2;
+        if (lane < n4) pf0 = src4[lane];
+        if (lane + 64 < n4) pf1 = src4[lane + 64];
+        if (lane + 128 < n4) pf2 = src4[lane + 128];
+        if (lane + 192 < n4) pf3 = src4[lane + 192];
+    };
+    bool have_pf = false;
+    if constexpr (PF) {
+        have_pf = steps_b > 0;
+        if (have_pf) prefetch(0);
+    }
+    wave_sync();
+
+    for (int t = 0; t < T; ++t) {
+        const int64_t trace0 = (static_cast<int64_t>(b) * T + t) * K;
+        bool pad = t >= steps_b || gave_up;
+        const bool live = beam && raw < kInf && raw > -kInf;
+        const bool carried = live && eos_b >= 0 && ended;
+        bool read = !pad && live && !carried;
+        int cnt = -2;
+        float bound = -kInf, lse = 0.0f;
+        bool bad = false, lost = false;
+        // Overlapped decode: the step's row count (a hint of when to read),
+        // the read rows' RowInfo words and the first shortlist words are
+        // loaded together, so a step whose rows are all written costs one
+        // round trip; a word not yet written (tag 0) is waited for after.
+        const uint64_t read_m = __builtin_amdgcn_ballot_w64(read);
+        const uint32_t* sl32 = reinterpret_cast<const uint32_t*>(p.shortlist + trace0 * M);
+        uint32_t tlo[kNarrowTagLoads], thi[kNarrowTagLoads];
+        uint32_t ilo0 = 0, ihi0 = 0, ilo1 = 0, ihi1 = 0;
+        if (!pad && coherent) {
+            const int need = (t == 0 ? 1 : Kb) + p.wait_extra;
+            int have = need;
+            if (lane == 0)
+                have = __hip_atomic_load(p.step_done + static_cast<int64_t>(b) * T + t, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t* info32 = reinterpret_cast<const uint32_t*>(p.rowinfo + trace0 + lane);
+            if (read) {
+                (void)read_tagged(info32, ilo0, ihi0);
+                (void)read_tagged(info32 + 2, ilo1, ihi1);
+            }
+#pragma unroll
+            for (int u = 0; u < kNarrowTagLoads; ++u) {
+                const int q = 64 * u + lane;
+                const int k = q / M;
+                tlo[u] = 0;
+                thi[u] = 0;
+                if (q < K * M && ((read_m >> (k & 63)) & 1ull) != 0) (void)read_tagged(sl32 + 2 * q, tlo[u], thi[u]);
+            }
+            if (__builtin_amdgcn_readfirstlane(have) < need) {
+                int ok = 1;
+                if (lane == 0) ok = wait_step_rows(p, b, t) ? 1 : 0;
+                if (__builtin_amdgcn_readfirstlane(ok) == 0) {
+                    gave_up = pad = true;
+                    read = false;
+                }
+            }
+        }
+        if (read) {
+            RowInfo info;
+            if (have_pf) {
+                __builtin_memcpy(&info, &pf_info, sizeof(info));
+            } else if (!coherent) {
+                info = p.rowinfo[trace0 + lane];
+            } else {
+                // the two tagged words (count + 2, invalid + 1)
+                const uint32_t* info32 = reinterpret_cast<const uint32_t*>(p.rowinfo + trace0 + lane);
+                bool ok = ihi0 != 0u || wait_tagged(p, info32, ilo0, ihi0);
+                ok = ok && (ihi1 != 0u || wait_tagged(p, info32 + 2, ilo1, ihi1));
+                if (!ok) {
+                    lost = true;
+                    ilo0 = ilo1 = 0;
+                    ihi0 = 2;
+                    ihi1 = 1;
+                }
+                info.lse = bits_f32(ilo0);
+                info.count = static_cast<int32_t>(ihi0) - 2;
+                info.bound = bits_f32(ilo1);
+                info.invalid = ihi1 - 1u;
+            }
+            bad = info.invalid != 0;
+            if (p.row_lse && LOGITS) p.row_lse[trace0 + lane] = info.lse;
+            lse = info.lse;
+            cnt = M > 0 ? info.count : -1;
+            bound = info.bound;
+        }
+        const uint64_t bad_m = __builtin_amdgcn_ballot_w64(bad);
+        if (bad_m != 0) {
+            any_invalid = true;
+            const int at = t * K + (__ffsll(static_cast<long long>(bad_m)) - 1);  // steps in order, beams in order
+            first_bad = at < first_bad ? at : first_bad;
+        }
+        if (__builtin_amdgcn_ballot_w64(lost) != 0) gave_up = pad = true;
+        if (pad) {
+            // a padding step (reference src/c_api.cpp:764-781): no token, no parent
+            if (beam) {
+                if (p.tokens) p.tokens[trace0 + lane] = -1;
+                if (p.parents) p.parents[trace0 + lane] = -1;
+                if (p.lengths) p.lengths[trace0 + lane] = 0;
+                if (p.scores) p.scores[trace0 + lane] = -kInf;
+                if (p.raw_scores) p.raw_scores[trace0 + lane] = -kInf;
+                if (p.from_logprob) p.from_logprob[trace0 + lane] = 0;
+            }
+            continue;
+        }
+
+        // the shortlists into LDS (an entry past its row's count is never read)
+        const ShortEntry* src = p.shortlist + trace0 * M;
+        if (have_pf) {
+            const int n4 = K * M / 2;
+            uint4* dst4 = reinterpret_cast<uint4*>(s_sl);
+            if (lane < n4) dst4[lane] = pf0;
+            if (lane + 64 < n4) dst4[lane + 64] = pf1;
+            if (lane + 128 < n4) dst4[lane + 128] = pf2;
+            if (lane + 192 < n4) dst4[lane + 192] = pf3;
+        } else if (!coherent) {
+            for (int q0 = 0; q0 < K * M; q0 += 8 * 64) {
+                ShortEntry e[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (q0 + 64 * u + lane < K * M) e[u] = src[q0 + 64 * u + lane];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (q0 + 64 * u + lane < K * M) s_sl[q0 + 64 * u + lane] = e[u];
+            }
+        } else {
+            // the entries the row pass wrote (tag token + 1): the first
+            // 64 kNarrowTagLoads were loaded with the RowInfo, the rest are
+            // loaded now, kNarrowTagLoads per lane in flight; an entry not
+            // yet written is waited for
+            bool lost_e = false;
+            for (int q0 = 0; q0 < K * M; q0 += 64 * kNarrowTagLoads) {
+                int cq[kNarrowTagLoads];
+#pragma unroll
+                for (int u = 0; u < kNarrowTagLoads; ++u) {
+                    const int q = q0 + 64 * u + lane;
+                    const int k = q / M;
+                    cq[u] = __shfl(cnt, k < K ? k : 0);  // every lane: the shuffle reads other lanes
+                    if (q0 > 0) {
+                        tlo[u] = 0;
+                        thi[u] = 0;
+                        if (q < K * M && q - k * M < cq[u]) (void)read_tagged(sl32 + 2 * q, tlo[u], thi[u]);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < kNarrowTagLoads; ++u) {
+                    const int q = q0 + 64 * u + lane;
+                    const int k = q / M;
+                    if (q >= K * M || q - k * M >= cq[u]) continue;
+                    if (thi[u] == 0u && !wait_tagged(p, sl32 + 2 * q, tlo[u], thi[u])) {
+                        lost_e = true;
+                        thi[u] = 1;
+                    }
+                    s_sl[q] = ShortEntry{bits_f32(tlo[u]), static_cast<int32_t>(thi[u]) - 1};
+                }
+            }
+            if (__builtin_amdgcn_ballot_w64(lost_e) != 0) {
+                gave_up = true;
+                if (beam) {
+                    if (p.tokens) p.tokens[trace0 + lane] = -1;
+                    if (p.parents) p.parents[trace0 + lane] = -1;
+                    if (p.lengths) p.lengths[trace0 + lane] = 0;
+                    if (p.scores) p.scores[trace0 + lane] = -kInf;
+                    if (p.raw_scores) p.raw_scores[trace0 + lane] = -kInf;
+                    if (p.from_logprob) p.from_logprob[trace0 + lane] = 0;
+                }
+                wave_sync();
+                continue;
+            }
+        }
+        // this step's rows are staged: the next step's loads go out now
+        if constexpr (PF) {
+            have_pf = t + 1 < steps_b;
+            if (have_pf) prefetch(t + 1);
+        }
+        wave_sync();
+
+        // tau (unconstrained: every expanded beam has the same length, so
+        // this step's shortlisted candidates rank by raw)
+        const int new_len = len + 1;
+        const float inv = inv_at(new_len);
+        float tv = -kInf;
+        if (read && cnt >= K) tv = raw + s_sl[lane * M + (K - 1)].lp;
+        const float tau = wave_max_dpp(tv);
+        // survivors of beam `lane`: a prefix of its shortlist
+        int ns = 0;
+        if (read) {
+            for (;;) {  // four entries a round, their reads in flight together
+                float lp4[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) lp4[u] = ns + u < cnt ? s_sl[lane * M + ns + u].lp : -kInf;
+                int reach = 0;
+                bool on = true;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    on = on && ns + u < cnt && !(raw + lp4[u] < tau);
+                    reach += on ? 1 : 0;
+                }
+                ns += reach;
+                if (reach < 4) break;
+            }
+        }
+        // the carried-forward candidate (reference src/decoder.cpp:131-139)
+        Cand carry = dead;
+        if (carried) {
+            const int l = len > 1 ? len : 1;
+            carry = Cand{raw / pen_at(l), raw, lane, is_eos_of(p, b, last) ? last : eos_b, l, 0};
+        }
+        const uint64_t carried_m = __builtin_amdgcn_ballot_w64(carried);
+        const int incl = wave_inclusive_sum(ns);
+        const int nsurv = __builtin_amdgcn_readlane(incl, 63);
+        const int ncand = nsurv + static_cast<int>(__popcll(carried_m));
+
+        // the selection: the best Kb candidates, lane k holding the k-th
+        Cand sel = dead;
+        int nsel = 0;
+        // survivor s (< nsurv) as a candidate: beam k with s in [off_k,
+        // off_k + ns_k). Every lane calls it (the shuffles read other lanes).
+        auto survivor = [&](int s) -> Cand {
+            int k = 0;
+            for (int kk = 1; kk < K; ++kk)
+                if (s >= __builtin_amdgcn_readlane(incl - ns, kk)) k = kk;
+            const int i = s - __shfl(incl - ns, k);
+            const ShortEntry e = s_sl[k * M + i];
+            const float r = __shfl(raw, k) + e.lp;
+            return Cand{r * __shfl(inv, k), r, k, e.token, __shfl(new_len, k), 1};
+        };
+        if (ncand <= 64) {
+            // one candidate per lane, ranked by the count of those before it
+            for (int i = 0; i < ns; ++i) {
+                const ShortEntry e = s_sl[lane * M + i];
+                const float r = raw + e.lp;
+                s_cand[incl - ns + i] = Cand{r * inv, r, lane, e.token, new_len, 1};
+            }
+            if (carried) {
+                const int slot = nsurv + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                             static_cast<uint32_t>(carried_m >> 32),
+                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(carried_m), 0u)));
+                s_cand[slot] = carry;
+            }
+            wave_sync();
+            const Cand c = lane < ncand ? s_cand[lane] : dead;
+            const bool valid = lane < ncand && before(c, dead);
+            // Its key, larger exactly when the candidate comes earlier in the
+            // total order: score, raw, then (parent, token), which no two of
+            // a step's candidates share (a carried beam is not expanded), so
+            // length and flp never decide. Parents < 64, tokens < 2^24.
+            const uint32_t k2 = ordered_key(c.score), k1 = ordered_key(c.raw);
+            const uint32_t k0 = 0xffffffffu - ((static_cast<uint32_t>(c.parent) << 24) |
+                                               (static_cast<uint32_t>(c.token) & 0xffffffu));
+            s_key[lane] = make_uint4(k0, k1, k2, 0u);
+            wave_sync();
+            int rank = 0;
+            int j = 0;
+            for (; j + 4 <= ncand; j += 4) {  // four broadcast reads in flight
+                uint4 w[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) w[u] = s_key[j + u];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) count_above96(rank, k0, k1, k2, w[u].x, w[u].y, w[u].z);
+            }
+            for (; j < ncand; ++j) {
+                const uint4 w = s_key[j];
+                count_above96(rank, k0, k1, k2, w.x, w.y, w.z);
+            }
+            nsel = static_cast<int>(__popcll(__builtin_amdgcn_ballot_w64(valid)));
+            nsel = nsel < Kb ? nsel : Kb;
+            wave_sync();
+            if (valid && rank < Kb) s_cand[rank] = c;
+            wave_sync();
+            if (lane < nsel) sel = s_cand[lane];
+        } else {
+            Cand thr = dead;
+            for (int s0 = 0; s0 < nsurv; s0 += 64) {
+                const bool has = s0 + lane < nsurv;
+                const Cand c = survivor(has ? s0 + lane : nsurv - 1);
+                list_offer(sel, thr, c, has, Kb, lane);
+            }
+            list_offer(sel, thr, carry, carried, Kb, lane);
+            nsel = static_cast<int>(__popcll(__builtin_amdgcn_ballot_w64(lane < Kb && before(sel, dead))));
+        }
+
+        // Exactness: every candidate left out of a row's shortlist has raw <=
+        // fl(p + bound); a row passes when the Kb-th selected candidate ranks
+        // strictly before that bound's score and raw.
+        {
+            const Cand kth = nsel >= Kb ? lane_cand(sel, Kb - 1) : dead;
+            bool fail = false;
+            if (read) {
+                fail = cnt < 0;
+                if (!fail && bound > -kInf) {
+                    const float X = raw + bound;
+                    if (X > -kInf) {
+                        const float SX = X * inv;
+                        fail = !((kth.score > SX) || (kth.score == SX && kth.raw > X));
+                    }
+                }
+            }
+            const uint64_t fail_m = __builtin_amdgcn_ballot_w64(fail);
+            if (fail_m != 0) {
+                if (lane == 0) atomicAdd(&g_rescanned_rows, static_cast<unsigned long long>(__popcll(fail_m)));
+                // the passing rows' survivors, the carried-forward beams,
+                // then every token of each failing row
+                Cand thr = dead;
+                sel = dead;
+                for (int s0 = 0; s0 < nsurv; s0 += 64) {
+                    const bool has = s0 + lane < nsurv;
+                    const Cand c = survivor(has ? s0 + lane : nsurv - 1);  // parent in [0, K)
+                    list_offer(sel, thr, c, has && ((fail_m >> c.parent) & 1ull) == 0, Kb, lane);
+                }
+                list_offer(sel, thr, carry, carried, Kb, lane);
+                const int min_len = min_length_of(p, b);
+                const size_t esz = DT == 0 ? 4 : 2;
+                for (uint64_t m = fail_m; m != 0; m &= m - 1) {
+                    // beam k's values, in every lane
+                    const int k = __ffsll(static_cast<long long>(m)) - 1;
+                    const float praw = __shfl(raw, k), lse_k = __shfl(lse, k), inv_k = __shfl(inv, k);
+                    const int nl = __shfl(new_len, k);
+                    const bool mask_eos = nl < min_len;
+                    const char* base = static_cast<const char*>(p.x) +
+                                       static_cast<size_t>(trace0 + k) * static_cast<size_t>(V) * esz;
+                    for (int v0 = 0; v0 < V; v0 += 64 * kNarrowRescanUnroll) {
+                        float xs[kNarrowRescanUnroll];
+#pragma unroll
+                        for (int u = 0; u < kNarrowRescanUnroll; ++u) {
+                            const int v = v0 + 64 * u + lane;
+                            xs[u] = v < V ? load_one<DT>(base, v) : -kInf;
+                        }
+#pragma unroll
+                        for (int u = 0; u < kNarrowRescanUnroll; ++u) {
+                            const int v = v0 + 64 * u + lane;
+                            const float lp = LOGITS ? xs[u] - lse_k : xs[u];
+                            const bool ok = v < V && lp < kInf && lp != -kInf;
+                            const float r = praw + lp;
+                            const Cand c{r * inv_k, r, k, v, nl, 1};
+                            const bool offer = ok && before(c, thr) && !static_masked(p, b, v, mask_eos);
+                            list_offer(sel, thr, c, offer, Kb, lane);
+                        }
+                    }
+                }
+                nsel = static_cast<int>(__popcll(__builtin_amdgcn_ballot_w64(lane < Kb && before(sel, dead))));
+            }
+        }
+
+        // Selection (reference src/decoder.cpp:314-350): the trace and the
+        // next state of each slot
+        const Cand c = lane < nsel ? sel : dead;
+        if (beam) {
+            const int64_t o = trace0 + lane;
+            if (p.tokens) p.tokens[o] = c.token;
+            if (p.parents) p.parents[o] = c.parent;
+            if (p.lengths) p.lengths[o] = c.length;
+            if (p.scores) p.scores[o] = c.score;
+            if (p.raw_scores) p.raw_scores[o] = c.raw;
+            if (p.from_logprob) p.from_logprob[o] = static_cast<uint8_t>(c.flp);
+        }
+        const int parent_ended = __shfl(ended ? 1 : 0, c.parent >= 0 ? c.parent : 0);
+        ended = c.parent >= 0 && (parent_ended != 0 || is_eos_of(p, b, c.token));
+        raw = c.raw;
+        len = c.length;
+        last = c.token;
+        wave_sync();
+    }
+
+    if (gave_up) {
+        // no hypothesis survives an abandoned decode
+        raw = -kInf;
+        len = 0;
+        if (lane == 0 && p.fault) __hip_atomic_store(p.fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Final scores (reference src/decoder.cpp:179-187).
+    if (beam) {
+        const int64_t i = static_cast<int64_t>(b) * K + lane;
+        if (p.final_scores) p.final_scores[i] = raw / pen_at(len);
+        if (p.final_raw) p.final_raw[i] = raw;
+        if (p.final_lengths) p.final_lengths[i] = len;
+    }
+    // 1: a row the search read holds NaN or +inf; 2: the decode of the
+    // example did not complete (an overlapped wait gave up)
+    if (lane == 0 && p.invalid) p.invalid[b] = static_cast<uint8_t>(gave_up ? 2 : (any_invalid ? 1 : 0));
+    if (lane == 0 && p.first_invalid) p.first_invalid[b] = first_bad == 0x7fffffff ? -1 : first_bad;
 }
 
 // The prefetch needs the row pass finished before the select pass starts (not
@@ -1059,13 +1595,62 @@ hipError_t launch_select_variant(const DecodeParams& p, const SelectLayout& L, h
     return hipGetLastError();
 }
 
+// Workgroups of the narrow pass: a multiple of kXcds (workgroups are dealt
+// to the XCDs in turn, and a persistent row pass of CUs - groups workgroups
+// leaves groups / kXcds CUs free on each), up to kNarrowWaves examples each.
+int narrow_groups(int B) { return kXcds * ((B + kXcds * kNarrowWaves - 1) / (kXcds * kNarrowWaves)); }
+int narrow_per_group(int B) {
+    const int g = narrow_groups(B);
+    return (B + g - 1) / g;
+}
+
+int narrow_pen_len(const DecodeParams& p) { return p.T + 2 < kNarrowPenCap ? p.T + 2 : kNarrowPenCap; }
+
+// One wavefront's LDS: rank keys, shortlists, candidates, penalty tables.
+size_t narrow_wave_bytes(const DecodeParams& p) {
+    const size_t n = 1024 + sizeof(ShortEntry) * static_cast<size_t>(p.K) * static_cast<size_t>(p.M) +
+                     sizeof(Cand) * 64 + 2 * sizeof(float) * static_cast<size_t>(narrow_pen_len(p));
+    return (n + 15) & ~static_cast<size_t>(15);
+}
+
+template <int DT, bool LOGITS>
+hipError_t launch_select_narrow(const DecodeParams& p, hipStream_t stream) {
+    const int pen_len = narrow_pen_len(p);
+    const int wave_bytes = static_cast<int>(narrow_wave_bytes(p));
+    // prefetch: rows all written before the kernel starts, shortlists as
+    // 16-byte pairs of entries within the prefetch registers
+    const bool pf = p.step_done == nullptr && (p.M & 1) == 0 && p.K * p.M <= 2 * 64 * kNarrowPf;
+    KernelTimer timer(kKindSelect, stream);
+    const int per = narrow_per_group(p.B);
+    const dim3 grid((p.B + per - 1) / per), block(64 * per);
+    const size_t smem = static_cast<size_t>(wave_bytes) * per;
+    if (pf)
+        hipLaunchKernelGGL((select_narrow_kernel<DT, LOGITS, true>), grid, block, smem, stream, p, pen_len, wave_bytes);
+    else
+        hipLaunchKernelGGL((select_narrow_kernel<DT, LOGITS, false>), grid, block, smem, stream, p, pen_len, wave_bytes);
+    return hipGetLastError();
+}
+
 template <int DT, bool LOGITS>
 hipError_t launch_select_typed(const DecodeParams& p, const SelectLayout& L, hipStream_t stream) {
+    if (select_narrow(p)) return launch_select_narrow<DT, LOGITS>(p, stream);
     return prefetch_fits(p) ? launch_select_variant<DT, LOGITS, true>(p, L, stream)
                             : launch_select_variant<DT, LOGITS, false>(p, L, stream);
 }
 
 }  // namespace
+
+std::atomic<int> g_select_kind{0};
+
+bool select_narrow(const DecodeParams& p) {
+    if (g_select_kind.load(std::memory_order_relaxed) == 1) return false;
+    return !p.step_mode && !p.constrained && p.M > 0 && p.use_tau && p.K <= kNarrowMaxK && p.V <= (1 << 24) &&
+           narrow_wave_bytes(p) <= static_cast<size_t>(kNarrowWaveLds);
+}
+
+int select_reserve_cus(const DecodeParams& p) {
+    return select_narrow(p) ? narrow_groups(p.B) : p.B;
+}
 
 SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool step_mode, int prefix_cap) {
     (void)B;

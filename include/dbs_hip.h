@@ -222,10 +222,18 @@ DBS_CUDA_EXPORT int dbs_hip_set_row_pass(int kind);
  * the reference; the results are the same either way): -1 automatic (the
  * default: constrained decodes, whose select pass is as long as the row
  * pass), 1 always, 0 never (the select pass after the row pass on the
- * caller's stream). Applies when at most half the CUs would hold the select
- * pass's workgroups (one per example). Returns the previous setting, or -2
- * for an invalid argument. */
+ * caller's stream). Applies when at most half the CUs would be left to the
+ * select pass (one per example for the workgroup pass, one per four examples
+ * for the one-wavefront pass). Returns the previous setting, or -2 for an
+ * invalid argument. */
 DBS_CUDA_EXPORT int dbs_hip_set_decode_overlap(int on);
+
+/* The select pass of a decode (no counterpart in the reference; the results
+ * are the same either way): 0 automatic (the default: one wavefront per
+ * example for unconstrained decodes of at most 16 beams with shortlists, one
+ * 256-thread workgroup per example otherwise), 1 always the workgroup pass.
+ * Returns the previous setting, or -2 for an invalid argument. */
+DBS_CUDA_EXPORT int dbs_hip_set_select_pass(int kind);
 
 #ifdef __cplusplus
 }
