@@ -283,9 +283,15 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     e = launch_clear(sync, sync_bytes(p.B, p.T), stream);
     if (e == hipSuccess) e = launch_clear(ws + L.off_rowinfo, L.off_prefix - L.off_rowinfo, stream);
     if (e == hipSuccess) e = hipEventRecord(aux->start, stream);
-    if (e == hipSuccess) e = launch_row_pass(p, stream);
+    // A persistent row pass is launched first: its grid leaves the select
+    // pass's CUs free. A row pass of one workgroup per row would fill every
+    // CU before the select pass's workgroups are placed, so the select pass
+    // goes first there (it waits for its rows).
+    const bool persistent = row_pass_persistent(p);
+    if (e == hipSuccess && persistent) e = launch_row_pass(p, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(aux->stream, aux->start, 0);
     if (e == hipSuccess) e = launch_select(p, L.sel, aux->stream);
+    if (e == hipSuccess && !persistent) e = launch_row_pass(p, stream);
     if (e == hipSuccess) e = hipEventRecord(aux->done, aux->stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(stream, aux->done, 0);
     if (e == hipSuccess) *fault = p.fault;

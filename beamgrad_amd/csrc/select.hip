@@ -1203,6 +1203,28 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         have_pf = steps_b > 0;
         if (have_pf) prefetch(0);
     }
+    // A step's trace is stored during the next step and its row logsumexps
+    // later in the same step, just before the prefetch goes out: stores count
+    // in vmcnt like loads, so a wait for a loaded value also waits for every
+    // store issued before that load.
+    int64_t pend_o = -1;  // the pending trace slot (lanes < K), or none
+    Cand pend_c = dead;
+    bool pend_lse = false;
+    int64_t pend_lse_o = 0;
+    float pend_lse_v = 0.0f;
+    auto flush = [&]() __attribute__((always_inline)) {
+        if (pend_lse) p.row_lse[pend_lse_o] = pend_lse_v;
+        if (pend_o >= 0) {
+            if (p.tokens) p.tokens[pend_o] = pend_c.token;
+            if (p.parents) p.parents[pend_o] = pend_c.parent;
+            if (p.lengths) p.lengths[pend_o] = pend_c.length;
+            if (p.scores) p.scores[pend_o] = pend_c.score;
+            if (p.raw_scores) p.raw_scores[pend_o] = pend_c.raw;
+            if (p.from_logprob) p.from_logprob[pend_o] = static_cast<uint8_t>(pend_c.flp);
+        }
+        pend_lse = false;
+        pend_o = -1;
+    };
     wave_sync();
 
     for (int t = 0; t < T; ++t) {
@@ -1228,18 +1250,19 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
             if (lane == 0)
                 have = __hip_atomic_load(p.step_done + static_cast<int64_t>(b) * T + t, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
-            const uint32_t* info32 = reinterpret_cast<const uint32_t*>(p.rowinfo + trace0 + lane);
-            if (read) {
-                (void)read_tagged(info32, ilo0, ihi0);
-                (void)read_tagged(info32 + 2, ilo1, ihi1);
-            }
+            // (every load is made, from a clamped address, and its result
+            // dropped where unneeded: a load in a branch is waited for
+            // inside it, one round trip each)
+            const uint32_t* info32 =
+                reinterpret_cast<const uint32_t*>(p.rowinfo + trace0 + (beam ? lane : 0));
+            (void)read_tagged(info32, ilo0, ihi0);
+            (void)read_tagged(info32 + 2, ilo1, ihi1);
 #pragma unroll
             for (int u = 0; u < kNarrowTagLoads; ++u) {
                 const int q = 64 * u + lane;
                 const int k = q / M;
-                tlo[u] = 0;
-                thi[u] = 0;
-                if (q < K * M && ((read_m >> (k & 63)) & 1ull) != 0) (void)read_tagged(sl32 + 2 * q, tlo[u], thi[u]);
+                (void)read_tagged(sl32 + 2 * (q < K * M ? q : K * M - 1), tlo[u], thi[u]);
+                if (!(q < K * M && ((read_m >> (k & 63)) & 1ull) != 0)) thi[u] = 0;
             }
             if (__builtin_amdgcn_readfirstlane(have) < need) {
                 int ok = 1;
@@ -1273,7 +1296,11 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                 info.invalid = ihi1 - 1u;
             }
             bad = info.invalid != 0;
-            if (p.row_lse && LOGITS) p.row_lse[trace0 + lane] = info.lse;
+            if (p.row_lse && LOGITS) {
+                pend_lse = true;
+                pend_lse_o = trace0 + lane;
+                pend_lse_v = info.lse;
+            }
             lse = info.lse;
             cnt = M > 0 ? info.count : -1;
             bound = info.bound;
@@ -1286,6 +1313,7 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         }
         if (__builtin_amdgcn_ballot_w64(lost) != 0) gave_up = pad = true;
         if (pad) {
+            flush();
             // a padding step (reference src/c_api.cpp:764-781): no token, no parent
             if (beam) {
                 if (p.tokens) p.tokens[trace0 + lane] = -1;
@@ -1311,8 +1339,10 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
             for (int q0 = 0; q0 < K * M; q0 += 8 * 64) {
                 ShortEntry e[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (q0 + 64 * u + lane < K * M) e[u] = src[q0 + 64 * u + lane];
+                for (int u = 0; u < 8; ++u) {  // clamped: every load in flight at once
+                    const int q = q0 + 64 * u + lane;
+                    e[u] = src[q < K * M ? q : K * M - 1];
+                }
 #pragma unroll
                 for (int u = 0; u < 8; ++u)
                     if (q0 + 64 * u + lane < K * M) s_sl[q0 + 64 * u + lane] = e[u];
@@ -1330,11 +1360,7 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                     const int q = q0 + 64 * u + lane;
                     const int k = q / M;
                     cq[u] = __shfl(cnt, k < K ? k : 0);  // every lane: the shuffle reads other lanes
-                    if (q0 > 0) {
-                        tlo[u] = 0;
-                        thi[u] = 0;
-                        if (q < K * M && q - k * M < cq[u]) (void)read_tagged(sl32 + 2 * q, tlo[u], thi[u]);
-                    }
+                    if (q0 > 0) (void)read_tagged(sl32 + 2 * (q < K * M ? q : K * M - 1), tlo[u], thi[u]);
                 }
 #pragma unroll
                 for (int u = 0; u < kNarrowTagLoads; ++u) {
@@ -1350,6 +1376,7 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
             }
             if (__builtin_amdgcn_ballot_w64(lost_e) != 0) {
                 gave_up = true;
+                flush();
                 if (beam) {
                     if (p.tokens) p.tokens[trace0 + lane] = -1;
                     if (p.parents) p.parents[trace0 + lane] = -1;
@@ -1362,7 +1389,9 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                 continue;
             }
         }
-        // this step's rows are staged: the next step's loads go out now
+        // this step's rows are staged: the pending stores, then the next
+        // step's loads go out
+        flush();
         if constexpr (PF) {
             have_pf = t + 1 < steps_b;
             if (have_pf) prefetch(t + 1);
@@ -1540,13 +1569,8 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         // next state of each slot
         const Cand c = lane < nsel ? sel : dead;
         if (beam) {
-            const int64_t o = trace0 + lane;
-            if (p.tokens) p.tokens[o] = c.token;
-            if (p.parents) p.parents[o] = c.parent;
-            if (p.lengths) p.lengths[o] = c.length;
-            if (p.scores) p.scores[o] = c.score;
-            if (p.raw_scores) p.raw_scores[o] = c.raw;
-            if (p.from_logprob) p.from_logprob[o] = static_cast<uint8_t>(c.flp);
+            pend_o = trace0 + lane;
+            pend_c = c;
         }
         const int parent_ended = __shfl(ended ? 1 : 0, c.parent >= 0 ? c.parent : 0);
         ended = c.parent >= 0 && (parent_ended != 0 || is_eos_of(p, b, c.token));
@@ -1555,6 +1579,7 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         last = c.token;
         wave_sync();
     }
+    flush();
 
     if (gave_up) {
         // no hypothesis survives an abandoned decode
