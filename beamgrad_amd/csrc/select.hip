@@ -1141,6 +1141,35 @@ __device__ __forceinline__ void list_offer(Cand& top, Cand& thr, const Cand& c, 
     }
 }
 
+// The overlapped decode's words of one step for one wavefront: the step's row
+// count (lane 0; a hint of when to read), lane k's RowInfo words and the
+// first 64 kNarrowTagLoads shortlist words. Every load is made, from a
+// clamped address (a load under a branch is waited for inside it), and the
+// caller drops what it does not need; a word not yet written has tag 0.
+struct TagWords {
+    int have;
+    uint32_t ilo0, ihi0, ilo1, ihi1;
+    uint32_t lo[kNarrowTagLoads], hi[kNarrowTagLoads];
+};
+
+__device__ __forceinline__ void issue_tagged(const DecodeParams& p, int b, int t, int lane, TagWords& w) {
+    const int K = p.K, M = p.M;
+    const int64_t tr0 = (static_cast<int64_t>(b) * p.T + t) * K;
+    w.have = 0;
+    if (lane == 0)
+        w.have = __hip_atomic_load(p.step_done + static_cast<int64_t>(b) * p.T + t, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t* info32 = reinterpret_cast<const uint32_t*>(p.rowinfo + tr0 + (lane < K ? lane : 0));
+    (void)read_tagged(info32, w.ilo0, w.ihi0);
+    (void)read_tagged(info32 + 2, w.ilo1, w.ihi1);
+    const uint32_t* sl32 = reinterpret_cast<const uint32_t*>(p.shortlist + tr0 * M);
+#pragma unroll
+    for (int u = 0; u < kNarrowTagLoads; ++u) {
+        const int q = 64 * u + lane;
+        (void)read_tagged(sl32 + 2 * (q < K * M ? q : K * M - 1), w.lo[u], w.hi[u]);
+    }
+}
+
 template <int DT, bool LOGITS, bool PF>
 __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(DecodeParams p, int pen_len, int wave_bytes) {
     extern __shared__ __align__(16) unsigned char smem_all[];
@@ -1225,6 +1254,10 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         pend_lse = false;
         pend_o = -1;
     };
+    // overlapped decode: a step's words, loaded a step ahead (spec) while the
+    // rows are already written, else at the step
+    TagWords tw;
+    bool spec = false;
     wave_sync();
 
     for (int t = 0; t < T; ++t) {
@@ -1240,31 +1273,19 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         // the read rows' RowInfo words and the first shortlist words are
         // loaded together, so a step whose rows are all written costs one
         // round trip; a word not yet written (tag 0) is waited for after.
-        const uint64_t read_m = __builtin_amdgcn_ballot_w64(read);
         const uint32_t* sl32 = reinterpret_cast<const uint32_t*>(p.shortlist + trace0 * M);
-        uint32_t tlo[kNarrowTagLoads], thi[kNarrowTagLoads];
-        uint32_t ilo0 = 0, ihi0 = 0, ilo1 = 0, ihi1 = 0;
+        uint32_t* const tlo = tw.lo;
+        uint32_t* const thi = tw.hi;
+        uint32_t& ilo0 = tw.ilo0;
+        uint32_t& ihi0 = tw.ihi0;
+        uint32_t& ilo1 = tw.ilo1;
+        uint32_t& ihi1 = tw.ihi1;
         if (!pad && coherent) {
+            // this step's words: loaded during the last step, or now
+            if (!spec) issue_tagged(p, b, t, lane, tw);
+            spec = false;
             const int need = (t == 0 ? 1 : Kb) + p.wait_extra;
-            int have = need;
-            if (lane == 0)
-                have = __hip_atomic_load(p.step_done + static_cast<int64_t>(b) * T + t, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-            // (every load is made, from a clamped address, and its result
-            // dropped where unneeded: a load in a branch is waited for
-            // inside it, one round trip each)
-            const uint32_t* info32 =
-                reinterpret_cast<const uint32_t*>(p.rowinfo + trace0 + (beam ? lane : 0));
-            (void)read_tagged(info32, ilo0, ihi0);
-            (void)read_tagged(info32 + 2, ilo1, ihi1);
-#pragma unroll
-            for (int u = 0; u < kNarrowTagLoads; ++u) {
-                const int q = 64 * u + lane;
-                const int k = q / M;
-                (void)read_tagged(sl32 + 2 * (q < K * M ? q : K * M - 1), tlo[u], thi[u]);
-                if (!(q < K * M && ((read_m >> (k & 63)) & 1ull) != 0)) thi[u] = 0;
-            }
-            if (__builtin_amdgcn_readfirstlane(have) < need) {
+            if (__builtin_amdgcn_readfirstlane(tw.have) < need) {
                 int ok = 1;
                 if (lane == 0) ok = wait_step_rows(p, b, t) ? 1 : 0;
                 if (__builtin_amdgcn_readfirstlane(ok) == 0) {
@@ -1395,6 +1416,10 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         if constexpr (PF) {
             have_pf = t + 1 < steps_b;
             if (have_pf) prefetch(t + 1);
+        }
+        if (coherent && t + 1 < steps_b) {
+            issue_tagged(p, b, t + 1, lane, tw);
+            spec = true;
         }
         wave_sync();
 
