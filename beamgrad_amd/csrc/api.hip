@@ -833,14 +833,15 @@ DBS_CUDA_EXPORT int dbs_hip_search_sequences(const int64_t* tokens, const int64_
 }
 
 DBS_CUDA_EXPORT int dbs_hip_minimum_risk(const float* scores, const float* costs, int batch_size, int beam_size,
-                                         float temperature, float scale, float* risk, float* grad_factor,
-                                         void* stream_ptr) {
+                                         float temperature, int reduction, float* risk, float* loss,
+                                         float* grad_factor, void* stream_ptr) {
     if (!scores || !costs || !risk || !grad_factor || batch_size <= 0 || beam_size <= 0 ||
-        !(temperature > 0.0f) || !(temperature < kInf) || !(scale == scale))
+        !(temperature > 0.0f) || !(temperature < kInf) || reduction < 0 || reduction > 2 ||
+        (reduction != 0 && !loss))
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    return finish(stream, launch_risk(scores, costs, batch_size, beam_size, temperature, scale, risk, grad_factor,
-                                      stream));
+    return finish(stream, launch_risk(scores, costs, batch_size, beam_size, temperature, reduction, risk, loss,
+                                      grad_factor, stream));
 }
 
 }  // extern "C"

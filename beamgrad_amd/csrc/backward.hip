@@ -712,12 +712,85 @@ __global__ __launch_bounds__(kRiskThreads) void risk_kernel(const float* scores,
     if (tid == 0) risk[b] = r;
 }
 
+// The same for every example of a small batch (K <= 64) in one workgroup,
+// then their mean or sum in index order: lane k of a wavefront holds beam k
+// (the same lanes, reductions and operations as risk_kernel, so the same
+// bits), each wavefront takes every fourth example.
+constexpr int kRiskAllMax = 1024;
+
+__global__ __launch_bounds__(kRiskThreads) void risk_all_kernel(const float* scores, const float* costs, int B, int K,
+                                                               float temperature, float scale, int reduction,
+                                                               float* risk, float* loss, float* factor) {
+    __shared__ float s_risk[kRiskAllMax];
+    const int tid = static_cast<int>(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+    // a wavefront's value as risk_kernel's block_reduce gives it: the wave
+    // tree, then the other (empty) wavefronts' identities added in order
+    auto wave_reduce = [&](float v, bool is_max) {
+        for (int off = 32; off > 0; off >>= 1) {
+            const float o = __shfl_xor(v, off);
+            v = is_max ? fmaxf(v, o) : v + o;
+        }
+        for (int w = 1; w < kRiskThreads / 64; ++w) v = is_max ? fmaxf(v, -kInf) : v + 0.0f;
+        return v;
+    };
+    for (int b = wave; b < B; b += kRiskThreads / 64) {
+        const bool in = lane < K;
+        const float sv = in ? scores[static_cast<int64_t>(b) * K + lane] : 0.0f;
+        const float cv = in ? costs[static_cast<int64_t>(b) * K + lane] : 0.0f;
+        const bool live = in && __builtin_fabsf(sv) < kInf;
+        const float m = wave_reduce(live ? sv / temperature : -kInf, true);
+        const float shift = m > -kInf ? m : 0.0f;
+        const float w_sum = wave_reduce(live ? expf(sv / temperature - shift) : 0.0f, false);
+        const float inv = w_sum > 0.0f ? 1.0f / w_sum : 0.0f;
+        const float r = wave_reduce(live ? expf(sv / temperature - shift) * inv * cv : 0.0f, false);
+        if (in) {
+            const float pk = live ? expf(sv / temperature - shift) * inv : 0.0f;
+            factor[static_cast<int64_t>(b) * K + lane] = live ? scale * pk * (cv - r) / temperature : 0.0f;
+        }
+        if (lane == 0) {
+            s_risk[b] = r;
+            risk[b] = r;
+        }
+    }
+    __syncthreads();
+    if (tid == 0 && loss) {
+        float acc = 0.0f;
+        for (int b = 0; b < B; ++b) acc = acc + s_risk[b];
+        loss[0] = reduction == 1 ? acc / static_cast<float>(B) : acc;
+    }
+}
+
+// Mean (reduction 1) or sum of risk[0, B): each thread sums a contiguous
+// slice in order, then the slices are added in order (one workgroup).
+__global__ __launch_bounds__(kRiskThreads) void risk_sum_kernel(const float* risk, int B, int reduction, float* loss) {
+    __shared__ float s_part[kRiskThreads];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int per = (B + kRiskThreads - 1) / kRiskThreads;
+    float acc = 0.0f;
+    for (int i = tid * per; i < B && i < (tid + 1) * per; ++i) acc = acc + risk[i];
+    s_part[tid] = acc;
+    __syncthreads();
+    if (tid == 0) {
+        float total = 0.0f;
+        for (int i = 0; i < kRiskThreads; ++i) total = total + s_part[i];
+        loss[0] = reduction == 1 ? total / static_cast<float>(B) : total;
+    }
+}
+
 }  // namespace
 
-hipError_t launch_risk(const float* scores, const float* costs, int B, int K, float temperature, float scale,
-                       float* risk, float* factor, hipStream_t stream) {
+hipError_t launch_risk(const float* scores, const float* costs, int B, int K, float temperature, int reduction,
+                       float* risk, float* loss, float* factor, hipStream_t stream) {
+    const float scale = reduction == 1 ? 1.0f / static_cast<float>(B) : 1.0f;
+    if (B <= kRiskAllMax && K <= 64) {
+        hipLaunchKernelGGL(risk_all_kernel, dim3(1), dim3(kRiskThreads), 0, stream, scores, costs, B, K, temperature,
+                           scale, reduction, risk, reduction != 0 ? loss : nullptr, factor);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(risk_kernel, dim3(B), dim3(kRiskThreads), 0, stream, scores, costs, K, temperature, scale,
                        risk, factor);
+    if (reduction != 0 && loss) hipLaunchKernelGGL(risk_sum_kernel, dim3(1), dim3(kRiskThreads), 0, stream, risk, B,
+                                                   reduction, loss);
     return hipGetLastError();
 }
 

@@ -246,9 +246,10 @@ hipError_t launch_backtrack(const int32_t* tokens, const int32_t* parents, const
 hipError_t launch_backtrack(const int64_t* tokens, const int64_t* parents, const int64_t* steps,
                             const int64_t* lengths, int B, int T, int K,
                             int64_t* seq, hipStream_t stream);
-// The minimum-risk loss of scores [B, K] under costs [B, K]: risk [B] and
-// the gradient factor [B, K] (scale * d risk_b / d score_bk).
-hipError_t launch_risk(const float* scores, const float* costs, int B, int K, float temperature, float scale,
-                       float* risk, float* factor, hipStream_t stream);
+// The minimum-risk loss of scores [B, K] under costs [B, K]: risk [B], with
+// reduction 1 (mean) or 2 (sum) also *loss, and the gradient factor [B, K]
+// (d loss / d score_bk: d risk_b / d score_bk, over B for the mean).
+hipError_t launch_risk(const float* scores, const float* costs, int B, int K, float temperature, int reduction,
+                       float* risk, float* loss, float* factor, hipStream_t stream);
 
 }  // namespace dbs_hip

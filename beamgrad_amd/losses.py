@@ -22,35 +22,34 @@ from ._search import BeamSearchResult
 
 __all__ = ["minimum_risk"]
 
-_REDUCTIONS = ("mean", "sum", "none")
+_REDUCTIONS = ("none", "mean", "sum")  # the operator's reduction codes 0, 1, 2
 
 
 class _ExpectedCost(torch.autograd.Function):
     """The loss (per-example risk [B], or its mean or sum) of scores [B, K]
     under costs [B, K], and the factor [B, K] that turns the loss's incoming
     gradient into the scores' gradient (the reduction's scale included). On
-    the GPU both come from one HIP launch (``beamgrad::minimum_risk``), the
-    reduction from one more; CPU tensors take the same formula in torch
+    the GPU both, the reduction too, come from one HIP launch
+    (``beamgrad::minimum_risk``); CPU tensors take the same formula in torch
     operations. The backward is one multiplication."""
 
     generate_vmap_rule = True  # elementwise and last-dim reductions only
 
     @staticmethod
     def forward(scores: torch.Tensor, costs: torch.Tensor, temperature: float, reduction: str):
-        scale = 1.0 / scores.shape[0] if reduction == "mean" else 1.0
         if scores.is_cuda:
-            risk, factor = torch.ops.beamgrad.minimum_risk(scores.float(), costs, temperature, scale)
-        else:
-            live = torch.isfinite(scores)
-            z = torch.where(live, scores / temperature, float("-inf"))
-            top = z.amax(-1, keepdim=True)
-            # rows without a live beam: every weight is 0 (exp(-inf - 0))
-            w = torch.exp(z - torch.where(torch.isfinite(top), top, 0.0))
-            total = w.sum(-1, keepdim=True)
-            p = w / torch.where(total > 0, total, 1.0)
-            c = torch.where(live, costs.to(device=p.device, dtype=p.dtype), 0.0)
-            risk = (p * c).sum(-1)
-            factor = (scale / temperature) * p * (c - risk[:, None])
+            return torch.ops.beamgrad.minimum_risk(scores.float(), costs, temperature, _REDUCTIONS.index(reduction))
+        scale = 1.0 / scores.shape[0] if reduction == "mean" else 1.0
+        live = torch.isfinite(scores)
+        z = torch.where(live, scores / temperature, float("-inf"))
+        top = z.amax(-1, keepdim=True)
+        # rows without a live beam: every weight is 0 (exp(-inf - 0))
+        w = torch.exp(z - torch.where(torch.isfinite(top), top, 0.0))
+        total = w.sum(-1, keepdim=True)
+        p = w / torch.where(total > 0, total, 1.0)
+        c = torch.where(live, costs.to(device=p.device, dtype=p.dtype), 0.0)
+        risk = (p * c).sum(-1)
+        factor = (scale / temperature) * p * (c - risk[:, None])
         loss = risk if reduction == "none" else (risk.sum() if reduction == "sum" else risk.mean())
         return loss, factor
 

@@ -147,22 +147,25 @@ DBS_CUDA_EXPORT int dbs_hip_search_sequences(
     int64_t* sequences,
     void* stream);
 
-/* The minimum-risk loss of the final beams in one launch (the objective of
- * reference python/beamgrad/losses.py:139-169): for each example b,
- * risk[b] = sum_k p_k c_k with p = softmax(scores[b] / temperature) over its
- * live beams (finite scores; dead beams get no probability and their costs
- * are not read), and grad_factor[b, k] = scale * p_k (c_k - risk[b]) /
- * temperature, the gradient of scale * risk[b] w.r.t. scores[b, k] (0 for
- * dead beams). An example without a live beam has risk 0. scores and costs
- * are float32 [B, K] on the device; temperature finite and positive. */
+/* The minimum-risk loss of the final beams (the objective of reference
+ * python/beamgrad/losses.py:139-169): for each example b, risk[b] =
+ * sum_k p_k c_k with p = softmax(scores[b] / temperature) over its live beams
+ * (finite scores; dead beams get no probability and their costs are not
+ * used). reduction 0: the loss is risk [B]; 1: *loss is their mean, 2: their
+ * sum (added in index order). grad_factor[b, k] = d loss / d scores[b, k] =
+ * p_k (c_k - risk[b]) / temperature, over B for the mean (0 for dead beams).
+ * An example without a live beam has risk 0. scores and costs are float32
+ * [B, K] on the device; temperature finite and positive; loss may be null
+ * for reduction 0. One launch for B <= 1024 and K <= 64, else two. */
 DBS_CUDA_EXPORT int dbs_hip_minimum_risk(
     const float* scores,
     const float* costs,
     int batch_size,
     int beam_size,
     float temperature,
-    float scale,
+    int reduction,
     float* risk,
+    float* loss,
     float* grad_factor,
     void* stream);
 

@@ -220,6 +220,39 @@ def test_minimum_risk_kernel_closed_form(K, reduction):
     assert torch.isfinite(st.grad).all()
 
 
+def test_minimum_risk_paths_agree():
+    """The one-workgroup kernel (B <= 1024, K <= 64; the reduction fused)
+    and the per-example kernel (larger batches; the reduction a second
+    launch) give each example the same risk and gradient factor, bit for
+    bit; the fused mean and sum add the risks in index order; the vmap rule
+    gives each slice the unbatched call's bits."""
+    from beamgrad_amd import _torch  # noqa: F401  (registers the operators)
+
+    rng = np.random.default_rng(11)
+    B, K = 1100, 8
+    s = rng.normal(0, 3, (B, K)).astype(np.float32)
+    s[rng.random((B, K)) < 0.1] = -np.inf
+    c = rng.random((B, K)).astype(np.float32)
+    st, ct = torch.tensor(s, device="cuda"), torch.tensor(c, device="cuda")
+    risk_big, f_big = torch.ops.beamgrad.minimum_risk(st, ct, 0.8, 0)
+    risk_small, f_small = torch.ops.beamgrad.minimum_risk(st[:1000].contiguous(), ct[:1000].contiguous(), 0.8, 0)
+    assert torch.equal(risk_big[:1000], risk_small) and torch.equal(f_big[:1000], f_small)
+    total, f_sum = torch.ops.beamgrad.minimum_risk(st[:1000].contiguous(), ct[:1000].contiguous(), 0.8, 2)
+    assert torch.equal(f_sum, f_small)
+    acc = np.float32(0.0)
+    for v in risk_small.cpu().numpy():
+        acc = np.float32(acc + v)
+    assert total.item() == acc
+    mean, f_mean = torch.ops.beamgrad.minimum_risk(st[:1000].contiguous(), ct[:1000].contiguous(), 0.8, 1)
+    assert mean.item() == np.float32(acc / np.float32(1000))
+    sl = st[:12].reshape(3, 4, K).contiguous()
+    cl = ct[:12].reshape(3, 4, K).contiguous()
+    got = torch.func.vmap(lambda a, b: torch.ops.beamgrad.minimum_risk(a, b, 0.8, 1))(sl, cl)
+    for i in range(3):
+        want = torch.ops.beamgrad.minimum_risk(sl[i], cl[i], 0.8, 1)
+        assert torch.equal(got[0][i], want[0]) and torch.equal(got[1][i], want[1])
+
+
 def test_decode_trace_engine_outputs():
     """decode_trace's widened trace and its engine trace (outputs 11-14, what
     the backward reads) against decode_ex's own outputs, bit for bit."""
