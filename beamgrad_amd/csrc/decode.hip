@@ -237,11 +237,13 @@ size_t sync_bytes(int B, int T) {
 // step: the row pass is queued first and never waits on the select pass, and
 // its rows are handed out by ticket, so it always progresses on the CUs left.
 // By default constrained decodes (n-gram blocking, repetition penalty) do,
-// whose select pass is as long as the row pass, and decodes whose row pass is
+// whose select pass is as long as the row pass; decodes whose row pass is
 // one of the persistent kernels (16-bit rows kept on chip), which lose only
-// the B CUs they leave free (MI355X: C2 2.00 -> 1.89 ms, C5 forward 2.35 ->
-// 1.75 ms). The one-read log-prob kernel runs several workgroups per CU and
-// loses more than the overlap saves (C4 3.03 -> 3.58 ms), so it does not.
+// the CUs they leave free (MI355X: C2 2.00 -> 1.89 ms, C5 forward 2.35 ->
+// 1.75 ms); and decodes with the workgroup select pass beside the one-read
+// log-prob kernel (one workgroup per row) when at most one example per 8 CUs
+// lets the select pass hold its CUs (C4 2.73 -> 2.13 ms; shared CUs made it
+// 3.53 ms).
 // *fault: the overlapped decode's fault word (non-zero once a select-pass
 // wait gave up), else null.
 hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStream_t stream, char* ws,
@@ -254,7 +256,7 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     Aux* aux = nullptr;
     const int mode = g_overlap.load(std::memory_order_relaxed);
     bool want = allow_overlap && !p.step_mode && p.T > 1 &&
-                (mode == 1 || (mode == -1 && (p.constrained || row_pass_persistent(p))));
+                (mode == 1 || (mode == -1 && (p.constrained || row_pass_persistent(p) || !select_narrow(p))));
     // Under stream capture the two passes run one after the other: a graph
     // may start its branches in any order, and a select pass started before
     // the row pass would wait for rows nobody is producing.
@@ -266,6 +268,14 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
         if (e != hipSuccess) return e;
     }
     const int reserve = select_reserve_cus(p);
+    const bool persistent = row_pass_persistent(p);
+    // Beside a row pass of one workgroup per row, a select pass of at most
+    // one workgroup per 8 CUs holds its CUs (select_hold); a larger one
+    // shares them. An unconstrained decode overlaps such a row pass only
+    // when its select pass holds its CUs (shared, its steps ran ~3x slower
+    // than alone).
+    const bool hold = !persistent && aux && 8 * p.B <= aux->cus;
+    if (aux && mode == -1 && !p.constrained && !persistent && !hold) aux = nullptr;
     if (!aux || 2 * reserve > aux->cus) {
         e = launch_row_pass(p, stream);
         if (e != hipSuccess) return e;
@@ -287,7 +297,7 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     // pass's CUs free. A row pass of one workgroup per row would fill every
     // CU before the select pass's workgroups are placed, so the select pass
     // goes first there (it waits for its rows).
-    const bool persistent = row_pass_persistent(p);
+    p.select_hold = hold ? 1 : 0;
     if (e == hipSuccess && persistent) e = launch_row_pass(p, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(aux->stream, aux->start, 0);
     if (e == hipSuccess) e = launch_select(p, L.sel, aux->stream);

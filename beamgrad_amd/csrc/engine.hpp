@@ -114,6 +114,7 @@ struct DecodeParams {
     int32_t* step_done;
     unsigned long long* row_ticket;
     int reserve_cus;  // CUs the persistent row-pass kernels leave free (the select pass's workgroups)
+    int select_hold;  // the select pass claims its SIMDs' registers (beside a row pass of one workgroup per row)
     // A select-pass wait that gives up (bounded by wait_ticks of the 100 MHz
     // counter) sets *fault and marks its example invalid (2); the example's
     // remaining steps are written as padding. wait_extra raises the count a

@@ -492,8 +492,14 @@ __device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State&
 // PF: the next step's RowInfo and shortlists are prefetched into registers
 // (chosen on the host: prefetch_fits); a separate instantiation, so the other
 // paths keep their register budget.
-template <int DT, bool LOGITS, bool PF>
+// HOLD: the kernel claims every accumulation register (a clobber of a255),
+// so no wavefront of another kernel fits on its SIMDs beside it: launched
+// before a row pass of one workgroup per row, it keeps its CUs to itself
+// (registers it never uses; its own occupancy, one wavefront per SIMD, is
+// unchanged).
+template <int DT, bool LOGITS, bool PF, bool HOLD = false>
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, SelectLayout L) {
+    if constexpr (HOLD) asm volatile("" ::: "a255");
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ State st;
     const int K = p.K, T = p.T, M = p.M;
@@ -1633,15 +1639,15 @@ bool prefetch_fits(const DecodeParams& p) {
            p.K * p.M <= 2 * kPfRegs * kSelectThreads;
 }
 
-template <int DT, bool LOGITS, bool PF>
+template <int DT, bool LOGITS, bool PF, bool HOLD = false>
 hipError_t launch_select_variant(const DecodeParams& p, const SelectLayout& L, hipStream_t stream) {
     if (L.smem > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<DT, LOGITS, PF>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<DT, LOGITS, PF, HOLD>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(L.smem));
         if (e != hipSuccess) return e;
     }
     KernelTimer timer(kKindSelect, stream);
-    hipLaunchKernelGGL((select_kernel<DT, LOGITS, PF>), dim3(p.B), dim3(kSelectThreads), L.smem, stream, p, L);
+    hipLaunchKernelGGL((select_kernel<DT, LOGITS, PF, HOLD>), dim3(p.B), dim3(kSelectThreads), L.smem, stream, p, L);
     return hipGetLastError();
 }
 
@@ -1684,6 +1690,7 @@ hipError_t launch_select_narrow(const DecodeParams& p, hipStream_t stream) {
 template <int DT, bool LOGITS>
 hipError_t launch_select_typed(const DecodeParams& p, const SelectLayout& L, hipStream_t stream) {
     if (select_narrow(p)) return launch_select_narrow<DT, LOGITS>(p, stream);
+    if (p.select_hold) return launch_select_variant<DT, LOGITS, false, true>(p, L, stream);
     return prefetch_fits(p) ? launch_select_variant<DT, LOGITS, true>(p, L, stream)
                             : launch_select_variant<DT, LOGITS, false>(p, L, stream);
 }
