@@ -73,7 +73,7 @@ constexpr int kScoreFilterMaxK = 32;  // beams up to which a rank compaction fir
 struct Lds {
     Cand* buf;        // [sort_cap] the collector
     Cand* rbuf;       // [kRescanBuf] one rescanned row's candidates
-    uint4* key;       // [2 * kRankMax] candidate keys of a rank compaction
+    uint4* key;       // [2 * kRankMax] candidate keys of a rank compaction (kRankMax used)
     int32_t* part;    // [kSelectThreads] partial ranks (or score keys)
     int32_t* surv;    // [64] candidates left by the score pass of a rank compaction
     int32_t* nsurv;   // [1] how many
@@ -96,6 +96,7 @@ struct Lds {
     int32_t* blk;     // [K, P] (LDS) or workspace
     uint32_t* sig;    // [2, K, sig_words] (LDS) prefix signatures, or null
     int sig_words;
+    int V;            // vocabulary size (the keys' token field)
     int sig_shift;    // 32 - log2(32 sig_words): hash bits kept
 };
 
@@ -231,35 +232,38 @@ __device__ __forceinline__ void sort_cands(Cand* buf, int np) {
 // the bitonic sort).
 constexpr int kRankMax = kSelectThreads;
 
-// The candidate at collector index idx as a 224-bit integer that is larger
+// The candidate at collector index idx as a 96-bit integer that is larger
 // exactly when the candidate comes earlier in the total order, least
-// significant word first: index (lower first; it decides only between
-// candidates that compare equal, i.e. dead sentinels), flp (desc), length,
-// token, parent (asc as signed integers), raw, score (desc; no NaN reaches
-// the collector).
-__device__ __forceinline__ void store_key(uint4* dst, const Cand& c, int idx) {
-    dst[0] = make_uint4(0xffffffffu - static_cast<uint32_t>(idx), static_cast<uint32_t>(c.flp) ^ 0x80000000u,
-                        0x7fffffffu - static_cast<uint32_t>(c.length), 0x7fffffffu - static_cast<uint32_t>(c.token));
-    dst[1] = make_uint4(0x7fffffffu - static_cast<uint32_t>(c.parent), ordered_key(c.raw), ordered_key(c.score), 0u);
+// significant word first: (parent, token) as parent * V + token (asc), raw,
+// score (desc; no NaN reaches the collector). No two candidates of a
+// collector share (parent, token) (a carried beam is not expanded, a rescan
+// first drops its row's shortlisted candidates), so length and from_logprob
+// never decide; K * V < 2^31 (the argument checks). Dead sentinels (parent
+// -1) rank below every other candidate by score and raw (a candidate is
+// admitted only if it ranks before the sentinel) and among themselves by
+// index, lower first.
+__device__ __forceinline__ uint4 cand_key(const Cand& c, int idx, int V) {
+    const uint32_t low = c.parent >= 0 ? static_cast<uint32_t>(c.parent) * static_cast<uint32_t>(V) +
+                                             static_cast<uint32_t>(c.token)
+                                       : static_cast<uint32_t>(idx);
+    return make_uint4(0xffffffffu - low, ordered_key(c.raw), ordered_key(c.score), 0u);
 }
 
-// rank += (key j > key i): the borrow out of key i - key j, kept in VCC
-// through the whole subtraction.
-__device__ __forceinline__ void count_before(int& rank, const uint4& ilo, const uint4& ihi, const uint4& jlo,
-                                             const uint4& jhi) {
+// rank += (96-bit key j > key i): the borrow out of i - j, kept in VCC
+// through the subtraction.
+__device__ __forceinline__ void count_above96(int& rank, uint32_t i0, uint32_t i1, uint32_t i2, uint32_t j0,
+                                              uint32_t j1, uint32_t j2) {
     uint32_t t;
-    asm("v_sub_co_u32 %0, vcc, %2, %9\n\t"
-        "v_subb_co_u32 %0, vcc, %3, %10, vcc\n\t"
-        "v_subb_co_u32 %0, vcc, %4, %11, vcc\n\t"
-        "v_subb_co_u32 %0, vcc, %5, %12, vcc\n\t"
-        "v_subb_co_u32 %0, vcc, %6, %13, vcc\n\t"
-        "v_subb_co_u32 %0, vcc, %7, %14, vcc\n\t"
-        "v_subb_co_u32 %0, vcc, %8, %15, vcc\n\t"
+    asm("v_sub_co_u32 %0, vcc, %2, %5\n\t"
+        "v_subb_co_u32 %0, vcc, %3, %6, vcc\n\t"
+        "v_subb_co_u32 %0, vcc, %4, %7, vcc\n\t"
         "v_addc_co_u32 %1, vcc, 0, %1, vcc"
         : "=&v"(t), "+v"(rank)
-        : "v"(ilo.x), "v"(ilo.y), "v"(ilo.z), "v"(ilo.w), "v"(ihi.x), "v"(ihi.y), "v"(ihi.z), "v"(jlo.x),
-          "v"(jlo.y), "v"(jlo.z), "v"(jlo.w), "v"(jhi.x), "v"(jhi.y), "v"(jhi.z)
+        : "v"(i0), "v"(i1), "v"(i2), "v"(j0), "v"(j1), "v"(j2)
         : "vcc");
+}
+__device__ __forceinline__ void count_before(int& rank, const uint4& i, const uint4& j) {
+    count_above96(rank, i.x, i.y, i.z, j.x, j.y, j.z);
 }
 
 // rank += (64-bit key (hi, lo) j > key i): the borrow out of i - j.
@@ -291,10 +295,9 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
     if (tid < n4) {
         if (tid < n) {
             c = s.buf[tid];
-            store_key(s.key + 2 * tid, c, tid);
+            s.key[tid] = cand_key(c, tid, s.V);
         } else {
-            s.key[2 * tid] = make_uint4(0u, 0u, 0u, 0u);  // below every key
-            s.key[2 * tid + 1] = make_uint4(0u, 0u, 0u, 0u);
+            s.key[tid] = make_uint4(0u, 0u, 0u, 0u);  // below every key
         }
         if (by_score) s.part[tid] = static_cast<int32_t>(tid < n ? ordered_key(c.score) : 0u);
     }
@@ -329,12 +332,9 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
             if (tid < ns) {
                 const int i = s.surv[tid];
                 const Cand ci = s.buf[i];
-                const uint4 ilo = s.key[2 * i], ihi = s.key[2 * i + 1];
+                const uint4 ki = s.key[i];
                 int rank = 0;
-                for (int j = 0; j < ns; ++j) {
-                    const int jj = s.surv[j];
-                    count_before(rank, ilo, ihi, s.key[2 * jj], s.key[2 * jj + 1]);
-                }
+                for (int j = 0; j < ns; ++j) count_before(rank, ki, s.key[s.surv[j]]);
                 if (rank < K) s.buf[rank] = ci;
                 if (rank == K - 1 && before(ci, st.thr)) st.thr = ci;
             }
@@ -352,27 +352,24 @@ __device__ __forceinline__ void compact_by_rank(Lds& s, State& st, int K, int n)
     int part = 0;
     if (gi < groups) {
         const int i = 64 * gi + lane;
-        const uint4 ilo = s.key[2 * i], ihi = s.key[2 * i + 1];
+        const uint4 ki = s.key[i];
         const int span = ((n4 / parts) + 3) & ~3;
         const int j0 = gj * span;
         const int j1 = j0 + span < n4 ? j0 + span : n4;
         int j = j0;
         for (; j + 8 <= j1; j += 8) {  // eight keys in flight
-            uint4 w[16];
+            uint4 w[8];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) w[u] = s.key[2 * j + u];
+            for (int u = 0; u < 8; ++u) w[u] = s.key[j + u];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) count_before(part, ilo, ihi, w[2 * u], w[2 * u + 1]);
+            for (int u = 0; u < 8; ++u) count_before(part, ki, w[u]);
         }
         for (; j < j1; j += 4) {
-            const uint4 a0 = s.key[2 * j], a1 = s.key[2 * j + 1];
-            const uint4 b0 = s.key[2 * j + 2], b1 = s.key[2 * j + 3];
-            const uint4 c0 = s.key[2 * j + 4], c1 = s.key[2 * j + 5];
-            const uint4 d0 = s.key[2 * j + 6], d1 = s.key[2 * j + 7];
-            count_before(part, ilo, ihi, a0, a1);
-            count_before(part, ilo, ihi, b0, b1);
-            count_before(part, ilo, ihi, c0, c1);
-            count_before(part, ilo, ihi, d0, d1);
+            const uint4 a = s.key[j], b2 = s.key[j + 1], c2 = s.key[j + 2], d = s.key[j + 3];
+            count_before(part, ki, a);
+            count_before(part, ki, b2);
+            count_before(part, ki, c2);
+            count_before(part, ki, d);
         }
     }
     s.part[tid] = part;
@@ -537,6 +534,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                          : p.blocked + static_cast<int64_t>(b) * K * p.prefix_cap;
     s.sig = L.sig_in_lds && !p.step_mode ? reinterpret_cast<uint32_t*>(smem + L.off_sig) : nullptr;
     s.sig_words = L.sig_words;
+    s.V = p.V;
     s.sig_shift = L.sig_words == kSigWordsMax ? 19 : 21;
     const bool lists_global = p.constrained && (!L.prefix_in_lds || !L.blk_in_lds);
 
@@ -1089,19 +1087,6 @@ constexpr int kNarrowTagLoads = 4;    // tagged shortlist loads per lane in flig
 constexpr int kNarrowWaves = 4;       // examples (wavefronts) per workgroup, at most: one workgroup per CU
 constexpr int kXcds = 8;              // MI355X: 8 XCDs of 32 CUs
 constexpr int kNarrowWaveLds = 16384; // LDS per wavefront, at most (else the workgroup pass)
-
-// rank += (96-bit key j > key i): the borrow out of i - j.
-__device__ __forceinline__ void count_above96(int& rank, uint32_t i0, uint32_t i1, uint32_t i2, uint32_t j0,
-                                              uint32_t j1, uint32_t j2) {
-    uint32_t t;
-    asm("v_sub_co_u32 %0, vcc, %2, %5\n\t"
-        "v_subb_co_u32 %0, vcc, %3, %6, vcc\n\t"
-        "v_subb_co_u32 %0, vcc, %4, %7, vcc\n\t"
-        "v_addc_co_u32 %1, vcc, 0, %1, vcc"
-        : "=&v"(t), "+v"(rank)
-        : "v"(i0), "v"(i1), "v"(i2), "v"(j0), "v"(j1), "v"(j2)
-        : "vcc");
-}
 
 // Lane j's candidate, wave-uniform.
 __device__ __forceinline__ Cand lane_cand(const Cand& c, int j) {
