@@ -250,6 +250,9 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
                          int32_t** fault, bool allow_overlap) {
     DecodeParams p = p0;
     *fault = nullptr;
+    // Row indices are 31-bit on the device.
+    const int64_t rows = static_cast<int64_t>(p.B) * (p.step_mode ? 1 : p.T) * p.K;
+    if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
     int device = 0;
     hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess) return e;

@@ -143,44 +143,37 @@ __device__ __forceinline__ void wave_sync() {
 
 // Whether the search may read row r, with its example and the length a token
 // taken from it gives (decode: row (b, t, k) is read only for t < steps[b],
-// and at t = 0 only beam 0; step: live, unfinished beams).
+// and at t = 0 only beam 0; step: live, unfinished beams). Row indices fit in
+// 31 bits (launch_decode refuses more rows), so the quotients are 32-bit.
 __device__ __forceinline__ bool row_is_read(const DecodeParams& p, int64_t r, int& b, int& new_len) {
-    const int K = p.K;
+    const uint32_t r32 = static_cast<uint32_t>(r), K32 = static_cast<uint32_t>(p.K);
+    const uint32_t bt = r32 / K32;
+    const int k = static_cast<int>(r32 - bt * K32);
     if (p.step_mode) {
-        b = static_cast<int>(r / K);
-        if (static_cast<int>(r % K) >= beams_of(p, b)) return false;  // past the example's beams
+        b = static_cast<int>(bt);
+        if (k >= beams_of(p, b)) return false;  // past the example's beams
         const float praw = gload(p.st_raw, r);
         if (!(praw < kInf && praw > -kInf)) return false;  // dead beam
         if (eos_of(p, b) >= 0 && gload(p.st_fin, r)) return false;  // finished
         new_len = gload(p.st_len, r) + 1;
         return true;
     }
-    int t = 0, k = 0;
-    if (r < 0x7fffffff) {  // 32-bit quotients (the usual case)
-        const uint32_t r32 = static_cast<uint32_t>(r), K32 = static_cast<uint32_t>(K);
-        const uint32_t bt = r32 / K32;
-        k = static_cast<int>(r32 - bt * K32);
-        b = static_cast<int>(bt / static_cast<uint32_t>(p.T));
-        t = static_cast<int>(bt - static_cast<uint32_t>(b) * static_cast<uint32_t>(p.T));
-    } else {
-        b = static_cast<int>(r / (static_cast<int64_t>(p.T) * K));
-        t = static_cast<int>((r / K) % p.T);
-        k = static_cast<int>(r % K);
-    }
+    b = static_cast<int>(bt / static_cast<uint32_t>(p.T));
+    const int t = static_cast<int>(bt - static_cast<uint32_t>(b) * static_cast<uint32_t>(p.T));
     if (t >= example_steps(p, b) || (t == 0 && k != 0) || k >= beams_of(p, b)) return false;
     new_len = t + 1;  // every unfinished live beam has length t at step t
     return true;
 }
 
-// The row a processing index stands for: step-major (every example's step t
-// before step t + 1) in the overlapped decode, so the select pass can follow
-// the row pass step by step; the index itself otherwise.
+// The row a processing index q < rows stands for: step-major (every example's
+// step t before step t + 1) in the overlapped decode, so the select pass can
+// follow the row pass step by step; the index itself otherwise.
 __device__ __forceinline__ int64_t row_of_ticket(const DecodeParams& p, int64_t q) {
     if (!p.step_done) return q;
-    const int64_t K = p.K, B = p.B;
-    const int64_t k = q % K, bt = q / K;
-    const int64_t b = bt % B, t = bt / B;
-    return (b * p.T + t) * K + k;
+    const uint32_t q32 = static_cast<uint32_t>(q), K = static_cast<uint32_t>(p.K), B = static_cast<uint32_t>(p.B);
+    const uint32_t bt = q32 / K, k = q32 - bt * K;
+    const uint32_t t = bt / B, b = bt - t * B;
+    return static_cast<int64_t>((b * static_cast<uint32_t>(p.T) + t) * K + k);
 }
 
 // The next processing index of a persistent row-pass workgroup: its own
@@ -245,48 +238,43 @@ __device__ __forceinline__ void signal_row_done(const DecodeParams& p, int64_t r
     }
 }
 
-// Bitonic sort (descending) of 256 values held 4 per lane (element i = 4 *
-// lane + e) across one wavefront.
-__device__ __forceinline__ void sort256_desc(float (&a)[4], int lane) {
-    for (int k = 2; k <= 256; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            if (j >= 4) {
-                const int lj = j >> 2;
+// The key of the M-th largest of 256 keys held 4 per lane across one
+// wavefront (1 <= M <= 256, keys below 2^BITS), by a radix select from the
+// most significant bit: each round counts, with ballots, the keys that agree
+// with the bits decided so far and have the next bit set, and keeps that half
+// when it holds at least the rank still sought. Exact, ties included, and the
+// same in every lane; no LDS and no lane exchange besides the ballots.
+template <int BITS>
+__device__ __forceinline__ uint32_t mth_largest_key(const uint32_t (&k)[4], int M) {
+    uint32_t prefix = 0;
+    int need = M;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float other = __shfl_xor(a[e], lj);
-                    const int i = 4 * lane + e;
-                    const bool desc = (i & k) == 0;
-                    const bool is_lo = (i & j) == 0;
-                    a[e] = (is_lo == desc) ? fmaxf(a[e], other) : fminf(a[e], other);
-                }
-            } else {
+    for (int bit = BITS - 1; bit >= 0; --bit) {
+        const uint32_t want = (prefix >> bit) | 1u;
+        int c = 0;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int i = 4 * lane + e;
-                    if ((i & j) == 0) {
-                        const int e2 = e + j;
-                        const bool desc = (i & k) == 0;
-                        const float lo = a[e], hi = a[e2];
-                        const bool swap = desc ? (hi > lo) : (lo > hi);
-                        if (swap) {
-                            a[e] = hi;
-                            a[e2] = lo;
-                        }
-                    }
-                }
-            }
+        for (int e = 0; e < 4; ++e) c += __popcll(__ballot((k[e] >> bit) == want));
+        if (c >= need) {
+            prefix |= 1u << bit;
+        } else {
+            need -= c;
         }
     }
+    return prefix;
 }
 
-// The M-th largest of 256 lane maxima held 4 per lane (M <= 256): at least M
-// elements of the row are >= it.
-__device__ __forceinline__ float shortlist_threshold(float (&a)[4], int lane, int M) {
-    sort256_desc(a, lane);
-    const int idx = M - 1;
-    const float mine = a[idx & 3];
-    return __shfl(mine, idx >> 2);
+// Inverse of ordered_key (+0 for the key of zero).
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return bits_f32((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// The M-th largest of 256 lane maxima held 4 per lane (M <= 256, none NaN):
+// at least M elements of the row are >= it.
+__device__ __forceinline__ float shortlist_threshold(const float (&a)[4], int M) {
+    uint32_t k[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) k[e] = ordered_key(a[e]);
+    return key_value(mth_largest_key<32>(k, M));
 }
 
 // lane + d's value of v for the lanes < d (d = 1, 2, 4, 8: DPP row shifts;

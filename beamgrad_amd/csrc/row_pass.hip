@@ -90,8 +90,8 @@ __device__ void row_pass_one(const DecodeParams& p, int64_t r, int b, int new_le
     // least M elements are >= theta.
     float theta = -kInf;
     if (M > 0) {
-        float a[4] = {lmax[0], lmax[1], lmax[2], lmax[3]};
-        theta = shortlist_threshold(a, lane, M);
+        const float a[4] = {lmax[0], lmax[1], lmax[2], lmax[3]};
+        theta = shortlist_threshold(a, M);
     }
     if (lane == 0) s_count = 0;
     __syncthreads();

@@ -23,6 +23,8 @@ __device__ unsigned long long g_rescanned_rows;
 // Waits for a step of the overlapped decode that gave up (should stay 0).
 __device__ unsigned long long g_wait_timeouts;
 
+constexpr int kStageTags = 8;  // tagged shortlist loads per thread in flight (workgroup pass, overlapped decode)
+
 // Overlapped decode: waits until the row pass has counted every row of
 // example b's step t: one at step 0, else one per beam of the example (the
 // row pass reads, and counts, exactly those rows). The count is a relaxed
@@ -647,10 +649,13 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 } else if (!coherent) {
                     info = p.rowinfo[trace0 + k];
                 } else {
-                    // the two tagged words (count + 2, invalid + 1)
+                    // the two tagged words (count + 2, invalid + 1), both
+                    // loads issued before either is waited for
                     const uint32_t* src = reinterpret_cast<const uint32_t*>(p.rowinfo + trace0 + k);
                     uint32_t lo0 = 0, hi0 = 2, lo1 = 0, hi1 = 1;
-                    if (!wait_tagged(p, src, lo0, hi0) || !wait_tagged(p, src + 2, lo1, hi1)) {
+                    (void)read_tagged(src, lo0, hi0);
+                    (void)read_tagged(src + 2, lo1, hi1);
+                    if ((hi0 == 0u && !wait_tagged(p, src, lo0, hi0)) || (hi1 == 0u && !wait_tagged(p, src + 2, lo1, hi1))) {
                         atomicOr(&st.gave_up, 1);
                         lo0 = lo1 = 0;
                         hi0 = 2;
@@ -718,25 +723,35 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                         }
                     }
                 }
-            } else {
+            } else if (coherent) {
+                // The entries the row pass wrote (tag token + 1): eight tagged
+                // loads per thread issued together (every one made, from a
+                // clamped index), then each entry not yet written waited for.
                 const uint32_t* src32 = reinterpret_cast<const uint32_t*>(src);
-                for (int i = tid; i < K * M; i += kSelectThreads) {
-                    ShortEntry e;
-                    if (!coherent) {
-                        e = src[i];
-                    } else {
-                        // the entries the row pass wrote (tag token + 1)
-                        if (i % M >= s.rcount[i / M]) continue;
-                        uint32_t lo = 0, hi = 1;
-                        if (!wait_tagged(p, src32 + 2 * i, lo, hi)) {
-                            atomicOr(&st.gave_up, 1);
-                            hi = 1;
-                        }
-                        e.lp = bits_f32(lo);
-                        e.token = static_cast<int32_t>(hi) - 1;
+                const int n = K * M;
+                for (int i0 = tid; i0 < n; i0 += kStageTags * kSelectThreads) {
+                    uint32_t lo[kStageTags], hi[kStageTags];
+#pragma unroll
+                    for (int u = 0; u < kStageTags; ++u) {
+                        const int i = i0 + u * kSelectThreads;
+                        (void)read_tagged(src32 + 2 * (i < n ? i : n - 1), lo[u], hi[u]);
                     }
-                    s.sl[SL == M ? i : sl_at(i / M, i % M, SL)] = e;
+#pragma unroll
+                    for (int u = 0; u < kStageTags; ++u) {
+                        const int i = i0 + u * kSelectThreads;
+                        if (i >= n || i % M >= s.rcount[i / M]) continue;
+                        if (hi[u] == 0u && !wait_tagged(p, src32 + 2 * i, lo[u], hi[u])) {
+                            atomicOr(&st.gave_up, 1);
+                            hi[u] = 1;
+                        }
+                        ShortEntry e;
+                        e.lp = bits_f32(lo[u]);
+                        e.token = static_cast<int32_t>(hi[u]) - 1;
+                        s.sl[SL == M ? i : sl_at(i / M, i % M, SL)] = e;
+                    }
                 }
+            } else {
+                for (int i = tid; i < K * M; i += kSelectThreads) s.sl[SL == M ? i : sl_at(i / M, i % M, SL)] = src[i];
             }
         }
         // this step's rows are staged: the next step's loads go out now
