@@ -273,11 +273,12 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     const int reserve = select_reserve_cus(p);
     const bool persistent = row_pass_persistent(p);
     // Beside a row pass of one workgroup per row, a select pass of at most
-    // one workgroup per 8 CUs holds its CUs (select_hold); a larger one
+    // one workgroup per 8 CUs holds its CUs (select_hold: the workgroup pass,
+    // and the one-wavefront pass of a constrained decode); a larger one
     // shares them. An unconstrained decode overlaps such a row pass only
     // when its select pass holds its CUs (shared, its steps ran ~3x slower
     // than alone).
-    const bool hold = !persistent && aux && 8 * p.B <= aux->cus;
+    const bool hold = !persistent && aux && 8 * reserve <= aux->cus;
     if (aux && mode == -1 && !p.constrained && !persistent && !hold) aux = nullptr;
     if (!aux || 2 * reserve > aux->cus) {
         e = launch_row_pass(p, stream);

@@ -1070,9 +1070,9 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
 }
 
 // ---------------------------------------------------------------------------
-// The narrow select pass: decodes with at most kNarrowMaxK beams, shortlists
-// and neither n-gram blocking, a repetition penalty nor the step API take
-// one wavefront per example, up to kNarrowWaves examples per workgroup (a CU
+// The narrow select pass: decodes with at most kNarrowMaxK beams and
+// shortlists, not the step API and not n = 1 blocking, take one wavefront
+// per example, up to kNarrowWaves examples per workgroup (a CU
 // beside a persistent row pass takes one workgroup of the select pass at a
 // time, so the overlapped decode leaves about B / kNarrowWaves CUs to it,
 // the same number on each XCD). Lane k holds beam
@@ -1092,6 +1092,15 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
 //     survivors, the carried-forward beams and every token of the failing
 //     rows (the candidate set only grows, so rows that passed still pass);
 //   * the trace and the next state.
+// With constraints (CON: n-gram blocking of n >= 2, a repetition penalty)
+// each beam's prefix lives in LDS with a 32 W-bit signature (two hashed bits
+// per token), both double-buffered and rebuilt from the parent's at every
+// step; each step lists a read beam's n-gram-blocked tokens (one lane per
+// prefix position), and every candidate takes make_cand's value (blocked:
+// none; in the prefix: lp - log(rep)). Constraints only lower a value, so the
+// row pass's bound still covers every token left out, and tau counts on K of
+// a row's first K + nblk entries (a blocked token is one entry at most),
+// each worth at least lp - log(rep).
 // The kept set is the best Kb of the same candidates under the same total
 // order as the workgroup pass, so the trace is the same bit for bit.
 constexpr int kNarrowMaxK = 16;       // the running list lives in one 16-lane DPP row
@@ -1176,8 +1185,12 @@ __device__ __forceinline__ void issue_tagged(const DecodeParams& p, int b, int t
     }
 }
 
-template <int DT, bool LOGITS, bool PF>
-__global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(DecodeParams p, int pen_len, int wave_bytes) {
+// HOLD: as the workgroup pass's (every register of its SIMDs claimed, so
+// no row-pass wavefront joins a CU that holds one of its workgroups).
+template <int DT, bool LOGITS, bool PF, bool CON, bool HOLD = false>
+__global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(DecodeParams p, int pen_len, int wave_bytes,
+                                                                         int sig_words) {
+    if constexpr (HOLD) asm volatile("" ::: "a255");
     extern __shared__ __align__(16) unsigned char smem_all[];
     const int K = p.K, T = p.T, M = p.M, V = p.V;
     // up to kNarrowWaves examples per workgroup, one per wavefront, each with
@@ -1192,6 +1205,20 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
     Cand* s_cand = reinterpret_cast<Cand*>(smem + 1024 + sizeof(ShortEntry) * static_cast<size_t>(K) * M);  // [64]
     float* s_pen = reinterpret_cast<float*>(s_cand + 64);  // [pen_len]
     float* s_inv = s_pen + pen_len;                        // [pen_len]
+    // Constraints (n-gram blocking, repetition penalty): the beams' prefixes
+    // and signatures (two buffers: the step's and the next), each read beam's
+    // n-gram-blocked tokens, and per beam its read state and next prefix.
+    const int P = p.prefix_cap, P4 = (P + 3) & ~3, W = sig_words;  // prefix rows P4 words apart (16-byte aligned)
+    uint32_t* s_sig = reinterpret_cast<uint32_t*>(
+        smem + ((1024 + sizeof(ShortEntry) * static_cast<size_t>(K) * M + sizeof(Cand) * 64 +
+                 2 * sizeof(float) * static_cast<size_t>(pen_len) + 15) & ~static_cast<size_t>(15)));  // [2][K][W]
+    int32_t* s_pre = reinterpret_cast<int32_t*>(s_sig + 2 * K * W);  // [2][K][P4]
+    int32_t* s_blk = s_pre + 2 * K * P4;                             // [K][P]
+    int32_t* s_nblk = s_blk + K * P;                                 // [K]
+    int32_t* s_plen = s_nblk + K;                                    // [K] prefix length of a read beam, else -1
+    int4* s_next = reinterpret_cast<int4*>(((reinterpret_cast<uintptr_t>(s_plen + K)) + 15) & ~static_cast<uintptr_t>(15));  // [K]
+    const int sig_shift = 32 - (31 - __builtin_clz(32 * static_cast<uint32_t>(W > 0 ? W : 1)));
+    int cur = 0;  // the step's prefix buffer
     for (int l = lane; l < pen_len; l += 64) {
         const float pl = length_penalty(l, p.alpha);
         s_pen[l] = pl;
@@ -1264,6 +1291,24 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
     // rows are already written, else at the step
     TagWords tw;
     bool spec = false;
+    // Constraints: membership of v in beam k's prefix of length lk (the
+    // step's buffer; its signature rules most tokens out with two bits), and
+    // the value of token v's log-prob lp in beam k's row (make_cand's rules:
+    // false when n-gram blocking removes it, the penalty when it repeats).
+    auto in_pre = [&](int k, int lk, int v) -> bool {
+        const uint32_t* sg = s_sig + (cur * K + k) * W;
+        const uint32_t h0 = sig_bit0(v, sig_shift), h1 = sig_bit1(v, sig_shift);
+        if ((((sg[h0 >> 5] >> (h0 & 31u)) & (sg[h1 >> 5] >> (h1 & 31u))) & 1u) == 0u) return false;
+        return in_list(s_pre + (cur * K + k) * P4, lk, v);
+    };
+    auto constrain = [&](int k, int lk, int nbk, int v, float lp, float& val) -> bool {
+        if (p.ngram > 1 && in_list(s_blk + k * P, nbk, v)) return false;
+        val = (p.penalise && in_pre(k, lk, v)) ? lp - p.log_rep : lp;
+        return true;
+    };
+    if constexpr (CON) {
+        for (int i = lane; i < K * W; i += 64) s_sig[i] = 0u;  // every prefix starts empty
+    }
     wave_sync();
 
     for (int t = 0; t < T; ++t) {
@@ -1429,12 +1474,73 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         }
         wave_sync();
 
-        // tau (unconstrained: every expanded beam has the same length, so
-        // this step's shortlisted candidates rank by raw)
+        // Constraints: each read beam's n-gram-blocked tokens, the tokens
+        // that followed an earlier occurrence of its last n - 1 tokens (one
+        // lane per (beam, prefix position); a read beam's prefix holds t
+        // tokens)
+        int nblk = 0;
+        if constexpr (CON) {
+            if (beam) s_plen[lane] = read ? len : -1;
+            if (p.ngram > 1) {
+                if (beam) s_nblk[lane] = 0;
+                wave_sync();
+                // item = (beam k, position i); eight items per lane a round,
+                // every read of a round in flight together
+                const int n = p.ngram, Pt = min(P, t), total = K * Pt;
+                for (int j0 = 0; j0 < total; j0 += 8 * 64) {
+                    int kk[8], ii[8], tl[8];
+                    bool on[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int j = j0 + 64 * u + lane;
+                        const int jc = j < total ? j : 0;
+                        kk[u] = jc / Pt;
+                        ii[u] = jc - kk[u] * Pt;
+                        const int Lk = s_plen[kk[u]];
+                        on[u] = j < total && ii[u] + n <= Lk;  // (a beam not read: -1)
+                        tl[u] = on[u] ? Lk - (n - 1) : 0;
+                    }
+                    bool same[8] = {true, true, true, true, true, true, true, true};
+                    for (int q = 0; q < n - 1; ++q) {
+                        int32_t a[8], c[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            const int32_t* pre = s_pre + (cur * K + kk[u]) * P4;
+                            a[u] = pre[on[u] ? ii[u] + q : 0];
+                            c[u] = pre[tl[u] + q];
+                        }
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) same[u] = same[u] && a[u] == c[u];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        if (on[u] && same[u]) {
+                            const int slot = atomicAdd(&s_nblk[kk[u]], 1);
+                            s_blk[kk[u] * P + slot] = s_pre[(cur * K + kk[u]) * P4 + ii[u] + n - 1];
+                        }
+                    }
+                }
+                wave_sync();
+                nblk = beam ? s_nblk[lane] : 0;
+            }
+        }
+
+        // tau (every expanded beam has the same length, so this step's
+        // shortlisted candidates rank by raw): at least K candidates reach it
         const int new_len = len + 1;
         const float inv = inv_at(new_len);
         float tv = -kInf;
-        if (read && cnt >= K) tv = raw + s_sl[lane * M + (K - 1)].lp;
+        if constexpr (CON) {
+            // K of a row's first K + nblk entries are not blocked (a blocked
+            // token is at most one entry), each worth at least its log-prob
+            // less the penalty
+            if (read && cnt >= K + nblk) {
+                const float lpk = s_sl[lane * M + (K - 1 + nblk)].lp;
+                tv = raw + (p.penalise ? lpk - p.log_rep : lpk);
+            }
+        } else {
+            if (read && cnt >= K) tv = raw + s_sl[lane * M + (K - 1)].lp;
+        }
         const float tau = wave_max_dpp(tv);
         // survivors of beam `lane`: a prefix of its shortlist
         int ns = 0;
@@ -1476,15 +1582,27 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                 if (s >= __builtin_amdgcn_readlane(incl - ns, kk)) k = kk;
             const int i = s - __shfl(incl - ns, k);
             const ShortEntry e = s_sl[k * M + i];
-            const float r = __shfl(raw, k) + e.lp;
-            return Cand{r * __shfl(inv, k), r, k, e.token, __shfl(new_len, k), 1};
+            const int lk = __shfl(len, k), nbk = __shfl(nblk, k);
+            float val = e.lp;
+            bool ok = true;
+            if constexpr (CON) ok = constrain(k, lk, nbk, e.token, e.lp, val);
+            const float r = __shfl(raw, k) + val;
+            const float ik = __shfl(inv, k);
+            const int nlk = __shfl(new_len, k);
+            return ok ? Cand{r * ik, r, k, e.token, nlk, 1} : dead;
         };
         if (ncand <= 64) {
             // one candidate per lane, ranked by the count of those before it
             for (int i = 0; i < ns; ++i) {
                 const ShortEntry e = s_sl[lane * M + i];
-                const float r = raw + e.lp;
-                s_cand[incl - ns + i] = Cand{r * inv, r, lane, e.token, new_len, 1};
+                if constexpr (CON) {
+                    // the log-prob in the score field: the constraints are
+                    // applied below, one candidate per lane
+                    s_cand[incl - ns + i] = Cand{e.lp, 0.0f, lane, e.token, new_len, 1};
+                } else {
+                    const float r = raw + e.lp;
+                    s_cand[incl - ns + i] = Cand{r * inv, r, lane, e.token, new_len, 1};
+                }
             }
             if (carried) {
                 const int slot = nsurv + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
@@ -1493,7 +1611,23 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                 s_cand[slot] = carry;
             }
             wave_sync();
-            const Cand c = lane < ncand ? s_cand[lane] : dead;
+            Cand c = lane < ncand ? s_cand[lane] : dead;
+            if constexpr (CON) {
+                const bool surv = lane < nsurv;  // (the carried-forward beams follow the survivors)
+                const int k = surv ? c.parent : 0;
+                const float pr = __shfl(raw, k), pi = __shfl(inv, k);
+                const int lk = __shfl(len, k), nbk = __shfl(nblk, k);
+                if (surv) {
+                    float val = c.score;
+                    if (constrain(k, lk, nbk, c.token, c.score, val)) {
+                        const float r = pr + val;
+                        c.score = r * pi;
+                        c.raw = r;
+                    } else {
+                        c = dead;
+                    }
+                }
+            }
             const bool valid = lane < ncand && before(c, dead);
             // Its key, larger exactly when the candidate comes earlier in the
             // total order: score, raw, then (parent, token), which no two of
@@ -1569,7 +1703,7 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                     // beam k's values, in every lane
                     const int k = __ffsll(static_cast<long long>(m)) - 1;
                     const float praw = __shfl(raw, k), lse_k = __shfl(lse, k), inv_k = __shfl(inv, k);
-                    const int nl = __shfl(new_len, k);
+                    const int nl = __shfl(new_len, k), lk = __shfl(len, k), nbk = __shfl(nblk, k);
                     const bool mask_eos = nl < min_len;
                     const char* base = static_cast<const char*>(p.x) +
                                        static_cast<size_t>(trace0 + k) * static_cast<size_t>(V) * esz;
@@ -1584,8 +1718,10 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                         for (int u = 0; u < kNarrowRescanUnroll; ++u) {
                             const int v = v0 + 64 * u + lane;
                             const float lp = LOGITS ? xs[u] - lse_k : xs[u];
-                            const bool ok = v < V && lp < kInf && lp != -kInf;
-                            const float r = praw + lp;
+                            bool ok = v < V && lp < kInf && lp != -kInf;
+                            float val = lp;
+                            if constexpr (CON) ok = ok && constrain(k, lk, nbk, v, lp, val);
+                            const float r = praw + val;
                             const Cand c{r * inv_k, r, k, v, nl, 1};
                             const bool offer = ok && before(c, thr) && !static_masked(p, b, v, mask_eos);
                             list_offer(sel, thr, c, offer, Kb, lane);
@@ -1602,6 +1738,68 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         if (beam) {
             pend_o = trace0 + lane;
             pend_c = c;
+        }
+        if constexpr (CON) {
+            // each selected beam: its parent's prefix, then its token, and the
+            // signature of both, into the other buffer
+            const int par = c.parent;
+            const int len_par = __shfl(len, par >= 0 ? par : 0);
+            if (beam) s_next[lane] = make_int4(par, (c.flp && c.token >= 0) ? c.token : -1, par >= 0 ? len_par : 0, 0);
+            wave_sync();
+            const int nxt = cur ^ 1;
+            const int Lc = min(P, t + 1);  // the new prefixes' length, at most
+            // 16 bytes an item: the parent's prefix (its appended token's
+            // word is written over after), then its signature with the
+            // token's two bits; four items per lane a round, their reads in
+            // flight together
+            const int C4 = (Lc + 3) >> 2, W4 = W / 4, np = K * C4, total = np + K * W4;
+            uint4* const s_pre4 = reinterpret_cast<uint4*>(s_pre);
+            uint4* const s_sig4 = reinterpret_cast<uint4*>(s_sig);
+            for (int j0 = 0; j0 < total; j0 += 4 * 64) {
+                int dst[4];
+                bool isp[4];
+                uint4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int j = j0 + 64 * u + lane;
+                    const int jc = j < total ? j : 0;
+                    isp[u] = jc < np;
+                    const int jj = isp[u] ? jc : jc - np, per = isp[u] ? C4 : W4;
+                    const int k = jj / per, q = jj - k * per;
+                    const int4 nx = s_next[k];
+                    const int pk = nx.x >= 0 ? nx.x : 0;
+                    if (isp[u]) {
+                        dst[u] = j < total && nx.x >= 0 ? ((nxt * K + k) * P4 >> 2) + q : -1;
+                        v[u] = s_pre4[((cur * K + pk) * P4 >> 2) + q];
+                    } else {
+                        dst[u] = j < total ? (nxt * K + k) * W4 + q : -1;
+                        v[u] = s_sig4[(cur * K + pk) * W4 + q];
+                        if (nx.x < 0) v[u] = make_uint4(0u, 0u, 0u, 0u);
+                        if (nx.x >= 0 && nx.y >= 0) {
+                            const uint32_t hs[2] = {sig_bit0(nx.y, sig_shift), sig_bit1(nx.y, sig_shift)};
+#pragma unroll
+                            for (int h2 = 0; h2 < 2; ++h2) {
+                                const uint32_t h = hs[h2];
+                                if (static_cast<int>(h >> 7) != q) continue;
+                                const uint32_t m = 1u << (h & 31u);
+                                switch ((h >> 5) & 3u) {
+                                    case 0: v[u].x |= m; break;
+                                    case 1: v[u].y |= m; break;
+                                    case 2: v[u].z |= m; break;
+                                    default: v[u].w |= m; break;
+                                }
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (dst[u] >= 0) (isp[u] ? s_pre4 : s_sig4)[dst[u]] = v[u];
+            }
+            wave_sync();
+            if (beam && par >= 0 && c.flp && c.token >= 0) s_pre[(nxt * K + lane) * P4 + len_par] = c.token;
+            wave_sync();
+            cur = nxt;
         }
         const int parent_ended = __shfl(ended ? 1 : 0, c.parent >= 0 ? c.parent : 0);
         ended = c.parent >= 0 && (parent_ended != 0 || is_eos_of(p, b, c.token));
@@ -1662,17 +1860,36 @@ int narrow_per_group(int B) {
 
 int narrow_pen_len(const DecodeParams& p) { return p.T + 2 < kNarrowPenCap ? p.T + 2 : kNarrowPenCap; }
 
-// One wavefront's LDS: rank keys, shortlists, candidates, penalty tables.
-size_t narrow_wave_bytes(const DecodeParams& p) {
-    const size_t n = 1024 + sizeof(ShortEntry) * static_cast<size_t>(p.K) * static_cast<size_t>(p.M) +
-                     sizeof(Cand) * 64 + 2 * sizeof(float) * static_cast<size_t>(narrow_pen_len(p));
+// One wavefront's LDS: rank keys, shortlists, candidates, penalty tables;
+// with constraints also signatures of W words per beam, prefixes, n-gram
+// lists and per-beam state (the kernel's layout).
+size_t narrow_wave_bytes(const DecodeParams& p, int W) {
+    const size_t K = static_cast<size_t>(p.K), P = static_cast<size_t>(p.prefix_cap);
+    size_t n = 1024 + sizeof(ShortEntry) * K * static_cast<size_t>(p.M) + sizeof(Cand) * 64 +
+               2 * sizeof(float) * static_cast<size_t>(narrow_pen_len(p));
+    n = (n + 15) & ~static_cast<size_t>(15);
+    if (p.constrained) {
+        const size_t P4 = (P + 3) & ~static_cast<size_t>(3);
+        n += sizeof(uint32_t) * 2 * K * static_cast<size_t>(W) + sizeof(int32_t) * (2 * K * P4 + K * P + 2 * K);
+        n = ((n + 15) & ~static_cast<size_t>(15)) + sizeof(int4) * K;
+    }
     return (n + 15) & ~static_cast<size_t>(15);
 }
 
-template <int DT, bool LOGITS>
+// Signature words per beam of a constrained decode (the most of 64, 32, 16
+// that fit one wavefront's LDS), else 0; 0 for an unconstrained one.
+int narrow_sig_words(const DecodeParams& p) {
+    if (!p.constrained) return 0;
+    for (int W = 64; W >= 16; W /= 2)
+        if (narrow_wave_bytes(p, W) <= static_cast<size_t>(kNarrowWaveLds)) return W;
+    return 0;
+}
+
+template <int DT, bool LOGITS, bool CON>
 hipError_t launch_select_narrow(const DecodeParams& p, hipStream_t stream) {
     const int pen_len = narrow_pen_len(p);
-    const int wave_bytes = static_cast<int>(narrow_wave_bytes(p));
+    const int W = narrow_sig_words(p);
+    const int wave_bytes = static_cast<int>(narrow_wave_bytes(p, W));
     // prefetch: rows all written before the kernel starts, shortlists as
     // 16-byte pairs of entries within the prefetch registers
     const bool pf = p.step_done == nullptr && (p.M & 1) == 0 && p.K * p.M <= 2 * 64 * kNarrowPf;
@@ -1680,16 +1897,34 @@ hipError_t launch_select_narrow(const DecodeParams& p, hipStream_t stream) {
     const int per = narrow_per_group(p.B);
     const dim3 grid((p.B + per - 1) / per), block(64 * per);
     const size_t smem = static_cast<size_t>(wave_bytes) * per;
-    if (pf)
-        hipLaunchKernelGGL((select_narrow_kernel<DT, LOGITS, true>), grid, block, smem, stream, p, pen_len, wave_bytes);
+    if (smem > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(pf ? &select_narrow_kernel<DT, LOGITS, true, CON>
+                                                                           : &select_narrow_kernel<DT, LOGITS, false, CON>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
+        if (e == hipSuccess && CON)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&select_narrow_kernel<DT, LOGITS, false, true, true>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));
+        if (e != hipSuccess) return e;
+    }
+    // beside a row pass of one workgroup per row: constrained decodes hold
+    // their CUs (p.select_hold)
+    if (CON && p.select_hold)
+        hipLaunchKernelGGL((select_narrow_kernel<DT, LOGITS, false, true, true>), grid, block, smem, stream, p, pen_len,
+                           wave_bytes, W);
+    else if (pf)
+        hipLaunchKernelGGL((select_narrow_kernel<DT, LOGITS, true, CON>), grid, block, smem, stream, p, pen_len,
+                           wave_bytes, W);
     else
-        hipLaunchKernelGGL((select_narrow_kernel<DT, LOGITS, false>), grid, block, smem, stream, p, pen_len, wave_bytes);
+        hipLaunchKernelGGL((select_narrow_kernel<DT, LOGITS, false, CON>), grid, block, smem, stream, p, pen_len,
+                           wave_bytes, W);
     return hipGetLastError();
 }
 
 template <int DT, bool LOGITS>
 hipError_t launch_select_typed(const DecodeParams& p, const SelectLayout& L, hipStream_t stream) {
-    if (select_narrow(p)) return launch_select_narrow<DT, LOGITS>(p, stream);
+    if (select_narrow(p))
+        return p.constrained ? launch_select_narrow<DT, LOGITS, true>(p, stream)
+                             : launch_select_narrow<DT, LOGITS, false>(p, stream);
     if (p.select_hold) return launch_select_variant<DT, LOGITS, false, true>(p, L, stream);
     return prefetch_fits(p) ? launch_select_variant<DT, LOGITS, true>(p, L, stream)
                             : launch_select_variant<DT, LOGITS, false>(p, L, stream);
@@ -1701,8 +1936,11 @@ std::atomic<int> g_select_kind{0};
 
 bool select_narrow(const DecodeParams& p) {
     if (g_select_kind.load(std::memory_order_relaxed) == 1) return false;
-    return !p.step_mode && !p.constrained && p.M > 0 && p.use_tau && p.K <= kNarrowMaxK && p.V <= (1 << 24) &&
-           narrow_wave_bytes(p) <= static_cast<size_t>(kNarrowWaveLds);
+    if (p.step_mode || p.M <= 0 || p.K > kNarrowMaxK || p.V > (1 << 24)) return false;
+    // constrained: n-gram blocking of n >= 2 and/or a repetition penalty
+    // (n = 1 blocking would drop most of a long prefix's shortlist entries)
+    if (p.constrained) return p.ngram != 1 && narrow_sig_words(p) > 0;
+    return p.use_tau && narrow_wave_bytes(p, 0) <= static_cast<size_t>(kNarrowWaveLds);
 }
 
 int select_reserve_cus(const DecodeParams& p) {
