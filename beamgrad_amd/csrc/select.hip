@@ -1486,7 +1486,10 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                 wave_sync();
                 // item = (beam k, position i); eight items per lane a round,
                 // every read of a round in flight together
-                const int n = p.ngram, Pt = min(P, t), total = K * Pt;
+                // (beam k's positions at a power-of-two stride 2^ps >= t: no
+                // division)
+                const int n = p.ngram, Pt = min(P, t);
+                const int ps = Pt > 1 ? 32 - __builtin_clz(static_cast<uint32_t>(Pt - 1)) : 0, total = K << ps;
                 for (int j0 = 0; j0 < total; j0 += 8 * 64) {
                     int kk[8], ii[8], tl[8];
                     bool on[8];
@@ -1494,8 +1497,8 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                     for (int u = 0; u < 8; ++u) {
                         const int j = j0 + 64 * u + lane;
                         const int jc = j < total ? j : 0;
-                        kk[u] = jc / Pt;
-                        ii[u] = jc - kk[u] * Pt;
+                        kk[u] = jc >> ps;
+                        ii[u] = jc & ((1 << ps) - 1);
                         const int Lk = s_plen[kk[u]];
                         on[u] = j < total && ii[u] + n <= Lk;  // (a beam not read: -1)
                         tl[u] = on[u] ? Lk - (n - 1) : 0;
@@ -1752,7 +1755,11 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
             // word is written over after), then its signature with the
             // token's two bits; four items per lane a round, their reads in
             // flight together
-            const int C4 = (Lc + 3) >> 2, W4 = W / 4, np = K * C4, total = np + K * W4;
+            // (each beam's chunks at power-of-two strides: no division)
+            const int C4 = (Lc + 3) >> 2, W4 = W / 4;
+            const int cs = C4 > 1 ? 32 - __builtin_clz(static_cast<uint32_t>(C4 - 1)) : 0;
+            const int ws = 31 - __builtin_clz(static_cast<uint32_t>(W4));
+            const int np = K << cs, total = np + (K << ws);
             uint4* const s_pre4 = reinterpret_cast<uint4*>(s_pre);
             uint4* const s_sig4 = reinterpret_cast<uint4*>(s_sig);
             for (int j0 = 0; j0 < total; j0 += 4 * 64) {
@@ -1764,13 +1771,13 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                     const int j = j0 + 64 * u + lane;
                     const int jc = j < total ? j : 0;
                     isp[u] = jc < np;
-                    const int jj = isp[u] ? jc : jc - np, per = isp[u] ? C4 : W4;
-                    const int k = jj / per, q = jj - k * per;
+                    const int jj = isp[u] ? jc : jc - np, sh = isp[u] ? cs : ws;
+                    const int k = jj >> sh, q = jj & ((1 << sh) - 1);
                     const int4 nx = s_next[k];
                     const int pk = nx.x >= 0 ? nx.x : 0;
                     if (isp[u]) {
-                        dst[u] = j < total && nx.x >= 0 ? ((nxt * K + k) * P4 >> 2) + q : -1;
-                        v[u] = s_pre4[((cur * K + pk) * P4 >> 2) + q];
+                        dst[u] = j < total && nx.x >= 0 && q < C4 ? ((nxt * K + k) * P4 >> 2) + q : -1;
+                        v[u] = s_pre4[((cur * K + pk) * P4 >> 2) + (q < C4 ? q : 0)];
                     } else {
                         dst[u] = j < total ? (nxt * K + k) * W4 + q : -1;
                         v[u] = s_sig4[(cur * K + pk) * W4 + q];
