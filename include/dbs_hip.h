@@ -233,8 +233,10 @@ DBS_CUDA_EXPORT int dbs_hip_set_decode_overlap(int on);
 
 /* The select pass of a decode (no counterpart in the reference; the results
  * are the same either way): 0 automatic (the default: one wavefront per
- * example for unconstrained decodes of at most 16 beams with shortlists, one
- * 256-thread workgroup per example otherwise), 1 always the workgroup pass.
+ * example for decodes of at most 16 beams with shortlists, with n-gram
+ * blocking of n >= 2 and/or a repetition penalty too where their prefixes
+ * fit the wavefront's LDS; one 256-thread workgroup per example otherwise),
+ * 1 always the workgroup pass.
  * Returns the previous setting, or -2 for an invalid argument. */
 DBS_CUDA_EXPORT int dbs_hip_set_select_pass(int kind);
 
