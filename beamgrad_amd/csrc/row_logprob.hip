@@ -286,9 +286,11 @@ __global__ __launch_bounds__(kLpThreads) __attribute__((amdgpu_waves_per_eu(C <=
         // The banned bytes of this thread's first block, then the next row's
         // loads (the registers are free now), then the scan; the bytes are
         // waited for only after the next row's loads are issued.
-        const int v00 = keep && nblk_hit > 0 ? s_blk_v0[tid < nblk_hit ? tid : 0] : 0;
+        const bool mine = keep && tid < nblk_hit;  // a block to scan (the others read an empty view)
+        const int v00 = mine ? s_blk_v0[tid] : 0;
         uint32_t ban_by[epb];  // the per-example mask, else the shared one
-        load_mask_bytes<epb>(p.banned_pe ? p.banned_pe + static_cast<int64_t>(b) * V : p.banned, v00, V, ban_by);
+        load_mask_bytes<epb>(!mine ? nullptr : (p.banned_pe ? p.banned_pe + static_cast<int64_t>(b) * V : p.banned), v00,
+                             V, ban_by);
         int bn;
         const int64_t rn = read_row_slot(s_slot, bn, len_unused);
         const bool mask_eos_n = s_slot_mask_eos != 0;
