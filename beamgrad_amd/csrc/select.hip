@@ -1110,7 +1110,7 @@ constexpr int kNarrowRescanUnroll = 16;
 constexpr int kNarrowTagLoads = 4;    // tagged shortlist loads per lane in flight (overlapped decode)
 constexpr int kNarrowWaves = 4;       // examples (wavefronts) per workgroup, at most: one workgroup per CU
 constexpr int kXcds = 8;              // MI355X: 8 XCDs of 32 CUs
-constexpr int kNarrowWaveLds = 16384; // LDS per wavefront, at most (else the workgroup pass)
+constexpr int kNarrowWaveLds = 24576; // LDS per wavefront, at most (else the workgroup pass)
 
 // Lane j's candidate, wave-uniform.
 __device__ __forceinline__ Cand lane_cand(const Cand& c, int j) {
@@ -1205,18 +1205,21 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
     Cand* s_cand = reinterpret_cast<Cand*>(smem + 1024 + sizeof(ShortEntry) * static_cast<size_t>(K) * M);  // [64]
     float* s_pen = reinterpret_cast<float*>(s_cand + 64);  // [pen_len]
     float* s_inv = s_pen + pen_len;                        // [pen_len]
-    // Constraints (n-gram blocking, repetition penalty): the beams' prefixes
-    // and signatures (two buffers: the step's and the next), each read beam's
+    // Constraints (n-gram blocking, repetition penalty): the beams' prefixes,
+    // signatures of their tokens and of their (n - 1)-grams but the last (two
+    // buffers each: the step's and the next), each read beam's
     // n-gram-blocked tokens, and per beam its read state and next prefix.
     const int P = p.prefix_cap, P4 = (P + 3) & ~3, W = sig_words;  // prefix rows P4 words apart (16-byte aligned)
     uint32_t* s_sig = reinterpret_cast<uint32_t*>(
         smem + ((1024 + sizeof(ShortEntry) * static_cast<size_t>(K) * M + sizeof(Cand) * 64 +
                  2 * sizeof(float) * static_cast<size_t>(pen_len) + 15) & ~static_cast<size_t>(15)));  // [2][K][W]
-    int32_t* s_pre = reinterpret_cast<int32_t*>(s_sig + 2 * K * W);  // [2][K][P4]
+    uint32_t* s_gsig = s_sig + 2 * K * W;                             // [2][K][W]
+    int32_t* s_pre = reinterpret_cast<int32_t*>(s_gsig + 2 * K * W);  // [2][K][P4]
     int32_t* s_blk = s_pre + 2 * K * P4;                             // [K][P]
     int32_t* s_nblk = s_blk + K * P;                                 // [K]
     int32_t* s_plen = s_nblk + K;                                    // [K] prefix length of a read beam, else -1
     int4* s_next = reinterpret_cast<int4*>(((reinterpret_cast<uintptr_t>(s_plen + K)) + 15) & ~static_cast<uintptr_t>(15));  // [K]
+    uint32_t* s_gnew = reinterpret_cast<uint32_t*>(s_next + K);  // [K] the (n - 1)-gram a new beam's signature takes
     const int sig_shift = 32 - (31 - __builtin_clz(32 * static_cast<uint32_t>(W > 0 ? W : 1)));
     int cur = 0;  // the step's prefix buffer
     for (int l = lane; l < pen_len; l += 64) {
@@ -1307,8 +1310,16 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         return true;
     };
     if constexpr (CON) {
-        for (int i = lane; i < K * W; i += 64) s_sig[i] = 0u;  // every prefix starts empty
+        for (int i = lane; i < K * W; i += 64) {  // every prefix starts empty
+            s_sig[i] = 0u;
+            s_gsig[i] = 0u;
+        }
     }
+    // A beam's last n - 1 tokens (its tail), hashed (FNV-1a over the tokens),
+    // when it has them: the n-gram list is built only where the tail occurred
+    // before, and the tail joins the signature when the beam grows.
+    uint32_t tail_h = 0u;
+    bool tail_v = false;
     wave_sync();
 
     for (int t = 0; t < T; ++t) {
@@ -1480,8 +1491,27 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         // tokens)
         int nblk = 0;
         if constexpr (CON) {
-            if (beam) s_plen[lane] = read ? len : -1;
+            bool need = false;
             if (p.ngram > 1) {
+                // the tail, and whether it ended an earlier (n - 1)-gram of
+                // the prefix (the signature of those; a hit is checked in full)
+                const int n = p.ngram;
+                tail_v = read && len >= n - 1;
+                tail_h = 0x811C9DC5u;
+                if (tail_v) {
+                    const int32_t* pre = s_pre + (cur * K + lane) * P4;
+                    for (int q = len - (n - 1); q < len; ++q)
+                        tail_h = (tail_h ^ static_cast<uint32_t>(pre[q])) * 0x01000193u;
+                    if (len >= n) {
+                        const uint32_t* gs = s_gsig + (cur * K + lane) * W;
+                        const uint32_t h0 = sig_bit0(static_cast<int>(tail_h), sig_shift);
+                        const uint32_t h1 = sig_bit1(static_cast<int>(tail_h), sig_shift);
+                        need = (((gs[h0 >> 5] >> (h0 & 31u)) & (gs[h1 >> 5] >> (h1 & 31u))) & 1u) != 0u;
+                    }
+                }
+            }
+            if (beam) s_plen[lane] = need ? len : -1;
+            if (__builtin_amdgcn_ballot_w64(need) != 0) {
                 if (beam) s_nblk[lane] = 0;
                 wave_sync();
                 // item = (beam k, position i); eight items per lane a round,
@@ -1747,7 +1777,13 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
             // signature of both, into the other buffer
             const int par = c.parent;
             const int len_par = __shfl(len, par >= 0 ? par : 0);
-            if (beam) s_next[lane] = make_int4(par, (c.flp && c.token >= 0) ? c.token : -1, par >= 0 ? len_par : 0, 0);
+            const uint32_t gh_par = static_cast<uint32_t>(__shfl(static_cast<int>(tail_h), par >= 0 ? par : 0));
+            const int gv_par = __shfl(tail_v ? 1 : 0, par >= 0 ? par : 0);
+            const bool grows = par >= 0 && c.flp && c.token >= 0;
+            if (beam) {
+                s_next[lane] = make_int4(par, grows ? c.token : -1, par >= 0 ? len_par : 0, grows && gv_par ? 1 : 0);
+                s_gnew[lane] = gh_par;
+            }
             wave_sync();
             const int nxt = cur ^ 1;
             const int Lc = min(P, t + 1);  // the new prefixes' length, at most
@@ -1759,19 +1795,21 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
             const int C4 = (Lc + 3) >> 2, W4 = W / 4;
             const int cs = C4 > 1 ? 32 - __builtin_clz(static_cast<uint32_t>(C4 - 1)) : 0;
             const int ws = 31 - __builtin_clz(static_cast<uint32_t>(W4));
-            const int np = K << cs, total = np + (K << ws);
+            // the (n - 1)-gram signatures follow the token signatures
+            const int ns = K << ws, np = K << cs, total = np + (p.ngram > 1 ? 2 : 1) * ns;
             uint4* const s_pre4 = reinterpret_cast<uint4*>(s_pre);
             uint4* const s_sig4 = reinterpret_cast<uint4*>(s_sig);
-            for (int j0 = 0; j0 < total; j0 += 4 * 64) {
-                int dst[4];
-                bool isp[4];
-                uint4 v[4];
+            for (int j0 = 0; j0 < total; j0 += 5 * 64) {
+                int dst[5];
+                bool isp[5];
+                uint4 v[5];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int u = 0; u < 5; ++u) {
                     const int j = j0 + 64 * u + lane;
                     const int jc = j < total ? j : 0;
                     isp[u] = jc < np;
-                    const int jj = isp[u] ? jc : jc - np, sh = isp[u] ? cs : ws;
+                    const bool isg = jc >= np + ns;  // an (n - 1)-gram signature chunk
+                    const int jj = isp[u] ? jc : jc - np - (isg ? ns : 0), sh = isp[u] ? cs : ws;
                     const int k = jj >> sh, q = jj & ((1 << sh) - 1);
                     const int4 nx = s_next[k];
                     const int pk = nx.x >= 0 ? nx.x : 0;
@@ -1779,11 +1817,15 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                         dst[u] = j < total && nx.x >= 0 && q < C4 ? ((nxt * K + k) * P4 >> 2) + q : -1;
                         v[u] = s_pre4[((cur * K + pk) * P4 >> 2) + (q < C4 ? q : 0)];
                     } else {
-                        dst[u] = j < total ? (nxt * K + k) * W4 + q : -1;
-                        v[u] = s_sig4[(cur * K + pk) * W4 + q];
+                        // (s_gsig is s_sig + 2 K W words: the same buffers, 2 K W4 chunks on)
+                        const int g4 = isg ? 2 * K * W4 : 0;
+                        dst[u] = j < total ? g4 + (nxt * K + k) * W4 + q : -1;
+                        v[u] = s_sig4[g4 + (cur * K + pk) * W4 + q];
                         if (nx.x < 0) v[u] = make_uint4(0u, 0u, 0u, 0u);
-                        if (nx.x >= 0 && nx.y >= 0) {
-                            const uint32_t hs[2] = {sig_bit0(nx.y, sig_shift), sig_bit1(nx.y, sig_shift)};
+                        const bool add = isg ? nx.w != 0 : nx.x >= 0 && nx.y >= 0;
+                        if (add) {
+                            const int hv = isg ? static_cast<int>(s_gnew[k]) : nx.y;
+                            const uint32_t hs[2] = {sig_bit0(hv, sig_shift), sig_bit1(hv, sig_shift)};
 #pragma unroll
                             for (int h2 = 0; h2 < 2; ++h2) {
                                 const uint32_t h = hs[h2];
@@ -1800,7 +1842,7 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                     }
                 }
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
+                for (int u = 0; u < 5; ++u)
                     if (dst[u] >= 0) (isp[u] ? s_pre4 : s_sig4)[dst[u]] = v[u];
             }
             wave_sync();
@@ -1877,8 +1919,8 @@ size_t narrow_wave_bytes(const DecodeParams& p, int W) {
     n = (n + 15) & ~static_cast<size_t>(15);
     if (p.constrained) {
         const size_t P4 = (P + 3) & ~static_cast<size_t>(3);
-        n += sizeof(uint32_t) * 2 * K * static_cast<size_t>(W) + sizeof(int32_t) * (2 * K * P4 + K * P + 2 * K);
-        n = ((n + 15) & ~static_cast<size_t>(15)) + sizeof(int4) * K;
+        n += sizeof(uint32_t) * 4 * K * static_cast<size_t>(W) + sizeof(int32_t) * (2 * K * P4 + K * P + 2 * K);
+        n = ((n + 15) & ~static_cast<size_t>(15)) + sizeof(int4) * K + sizeof(uint32_t) * K;
     }
     return (n + 15) & ~static_cast<size_t>(15);
 }
