@@ -300,10 +300,6 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
     p.invalid = outputs->invalid_input;
     p.row_lse = row_lse;
     p.first_invalid = first_invalid;
-    if (row_lse) {
-        e = launch_fill_f32(row_lse, 0.0f, static_cast<int64_t>(a.batch_size) * a.steps * a.beam_size, stream);
-        if (e != hipSuccess) return finish(stream, e);
-    }
     int32_t* fault = nullptr;
     e = launch_decode(p, L, stream, ws, &fault, allow_overlap);
     // the fault word lives in the workspace: handed out only where that is
@@ -376,10 +372,6 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
     p.st_fin = state->finished;
     p.st_prefix = state->prefix_stride > 0 ? state->prefixes : nullptr;
     p.st_stride = state->prefix_stride;
-    if (row_lse) {
-        e = launch_fill_f32(row_lse, 0.0f, static_cast<int64_t>(a.batch_size) * a.beam_size, stream);
-        if (e != hipSuccess) return finish(stream, e);
-    }
     int32_t* fault = nullptr;
     e = launch_decode(p, L, stream, ws, &fault, true);
     return finish_decode(stream, e, fault);

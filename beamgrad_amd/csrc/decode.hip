@@ -25,10 +25,38 @@ namespace dbs_hip {
 
 namespace {
 
-__global__ void fill_f32_kernel(float* dst, float value, int64_t n) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t j = i; j < n; j += stride) dst[j] = value;
+// Zeroes up to three byte ranges in one launch (each 4-byte aligned and a
+// multiple of 4 bytes long; 16-byte stores where a range allows them).
+struct ClearRanges {
+    char* ptr[3];
+    int64_t bytes[3];
+    int n;
+};
+
+__global__ __launch_bounds__(256) void clear_ranges_kernel(ClearRanges c) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    for (int r = 0; r < c.n; ++r) {
+        char* const dst = c.ptr[r];
+        const int64_t bytes = c.bytes[r];
+        if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0 && (bytes & 15) == 0) {
+            uint4* d4 = reinterpret_cast<uint4*>(dst);
+            for (int64_t i = first; i < bytes / 16; i += stride) d4[i] = make_uint4(0u, 0u, 0u, 0u);
+        } else {
+            uint32_t* d1 = reinterpret_cast<uint32_t*>(dst);
+            for (int64_t i = first; i < bytes / 4; i += stride) d1[i] = 0u;
+        }
+    }
+}
+
+hipError_t launch_clear_ranges(const ClearRanges& c, hipStream_t stream) {
+    int64_t most = 0;
+    for (int r = 0; r < c.n; ++r) most = c.bytes[r] / 16 > most ? c.bytes[r] / 16 : most;
+    if (c.n == 0) return hipSuccess;
+    const int64_t blocks = (most + 255) / 256;
+    hipLaunchKernelGGL(clear_ranges_kernel, dim3(static_cast<unsigned>(blocks < 1 ? 1 : (blocks < 4096 ? blocks : 4096))),
+                       dim3(256), 0, stream, c);
+    return hipGetLastError();
 }
 
 // The decode trace in the dtypes torch returns it in: the int32 indices as
@@ -47,12 +75,6 @@ __global__ __launch_bounds__(256) void widen_trace_kernel(WidenTrace w) {
     for (int64_t i = first; i < w.n_steps; i += stride) w.steps64[i] = w.steps ? w.steps[i] : w.T;
 }
 
-// Zeroes n16 16-byte words.
-__global__ void clear_kernel(uint4* dst, int64_t n16) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t j = i; j < n16; j += stride) dst[j] = make_uint4(0u, 0u, 0u, 0u);
-}
 
 __global__ void length_penalty_kernel(const int32_t* lengths, int64_t n, float alpha, float* out) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -280,8 +302,17 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     // than alone).
     const bool hold = !persistent && aux && 8 * reserve <= aux->cus;
     if (aux && mode == -1 && !p.constrained && !persistent && !hold) aux = nullptr;
+    // One launch zeroes the row logsumexps (rows the search does not read keep
+    // 0) and, in the overlapped decode, the counters and the RowInfo and
+    // shortlist words (tag 0: not written).
+    ClearRanges clear{};
+    if (p.row_lse) {
+        clear.ptr[clear.n] = reinterpret_cast<char*>(p.row_lse);
+        clear.bytes[clear.n++] = static_cast<int64_t>(sizeof(float)) * rows;
+    }
     if (!aux || 2 * reserve > aux->cus) {
-        e = launch_row_pass(p, stream);
+        e = launch_clear_ranges(clear, stream);
+        if (e == hipSuccess) e = launch_row_pass(p, stream);
         if (e != hipSuccess) return e;
         return launch_select(p, L.sel, stream);
     }
@@ -293,9 +324,12 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     p.reserve_cus = reserve;  // a persistent row pass would otherwise hold every CU until it ends
     wait_policy(p);
     std::lock_guard<std::mutex> lock(aux->mutex);
-    // the counters, and the RowInfo and shortlist words (tag 0: not written)
-    e = launch_clear(sync, sync_bytes(p.B, p.T), stream);
-    if (e == hipSuccess) e = launch_clear(ws + L.off_rowinfo, L.off_prefix - L.off_rowinfo, stream);
+    // (the workspace ranges rounded up to 16 bytes, inside the workspace)
+    clear.ptr[clear.n] = sync;
+    clear.bytes[clear.n++] = static_cast<int64_t>((sync_bytes(p.B, p.T) + 15) & ~static_cast<size_t>(15));
+    clear.ptr[clear.n] = ws + L.off_rowinfo;
+    clear.bytes[clear.n++] = static_cast<int64_t>((L.off_prefix - L.off_rowinfo + 15) & ~static_cast<size_t>(15));
+    e = launch_clear_ranges(clear, stream);
     if (e == hipSuccess) e = hipEventRecord(aux->start, stream);
     // A persistent row pass is launched first: its grid leaves the select
     // pass's CUs free. A row pass of one workgroup per row would fill every
@@ -312,16 +346,6 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     return e;
 }
 
-// Zeroes [dst, dst + bytes rounded up to 16); dst 16-byte aligned, the
-// rounded range inside the allocation.
-hipError_t launch_clear(void* dst, size_t bytes, hipStream_t stream) {
-    const int64_t n16 = static_cast<int64_t>((bytes + 15) / 16);
-    if (n16 <= 0) return hipSuccess;
-    const int64_t blocks = (n16 + 255) / 256;
-    hipLaunchKernelGGL(clear_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)), dim3(256), 0, stream,
-                       static_cast<uint4*>(dst), n16);
-    return hipGetLastError();
-}
 
 hipError_t launch_widen_trace(const WidenTrace& w, hipStream_t stream) {
     const int64_t n = w.n_trace > w.n_final ? (w.n_trace > w.n_steps ? w.n_trace : w.n_steps)
@@ -333,13 +357,6 @@ hipError_t launch_widen_trace(const WidenTrace& w, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream) {
-    if (n <= 0) return hipSuccess;
-    const int64_t blocks = (n + 255) / 256;
-    hipLaunchKernelGGL(fill_f32_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)), dim3(256), 0,
-                       stream, dst, value, n);
-    return hipGetLastError();
-}
 
 hipError_t launch_length_penalty(const int32_t* lengths, int64_t n, float alpha, float* out, hipStream_t stream) {
     if (n <= 0) return hipSuccess;

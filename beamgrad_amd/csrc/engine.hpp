@@ -194,7 +194,6 @@ hipError_t rescan_counter(int reset, unsigned long long* value);
 hipError_t wait_timeout_counter(int reset, unsigned long long* value);
 
 // Elementwise helpers.
-hipError_t launch_fill_f32(float* dst, float value, int64_t n, hipStream_t stream);
 
 // A decode trace's int32 / uint8 outputs widened for torch (int64, bool), and
 // the per-example steps (T where steps is null).
@@ -207,7 +206,6 @@ struct WidenTrace {
     int T;
 };
 hipError_t launch_widen_trace(const WidenTrace& w, hipStream_t stream);
-hipError_t launch_clear(void* dst, size_t bytes, hipStream_t stream);
 hipError_t launch_length_penalty(const int32_t* lengths, int64_t n, float alpha, float* out, hipStream_t stream);
 hipError_t launch_check_steps(const int32_t* steps, int B, int T, int32_t* status, hipStream_t stream);
 // Range check of every per-example array (steps in [1, T], beams in [1, K],

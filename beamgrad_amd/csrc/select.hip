@@ -1269,9 +1269,9 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
         if (have_pf) prefetch(0);
     }
     // A step's trace is stored during the next step and its row logsumexps
-    // later in the same step, just before the prefetch goes out: stores count
-    // in vmcnt like loads, so a wait for a loaded value also waits for every
-    // store issued before that load.
+    // later in the same step, just after the next step's loads go out: stores
+    // count in vmcnt like loads, so a wait for a loaded value also waits for
+    // every store issued before that load.
     int64_t pend_o = -1;  // the pending trace slot (lanes < K), or none
     Cand pend_c = dead;
     bool pend_lse = false;
@@ -1472,9 +1472,9 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
                 continue;
             }
         }
-        // this step's rows are staged: the pending stores, then the next
-        // step's loads go out
-        flush();
+        // this step's rows are staged: the next step's loads go out, then
+        // the pending stores (after the loads, so that waiting for the loads
+        // never waits for them)
         if constexpr (PF) {
             have_pf = t + 1 < steps_b;
             if (have_pf) prefetch(t + 1);
@@ -1483,6 +1483,7 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
             issue_tagged(p, b, t + 1, lane, tw);
             spec = true;
         }
+        flush();
         wave_sync();
 
         // Constraints: each read beam's n-gram-blocked tokens, the tokens
