@@ -1435,26 +1435,39 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
             // 64 kNarrowTagLoads were loaded with the RowInfo, the rest are
             // loaded now, kNarrowTagLoads per lane in flight; an entry not
             // yet written is waited for
+            // (words written are stored as they are; only when one is not
+            // is each lane's row count looked up, to wait for the words
+            // within it)
             bool lost_e = false;
             for (int q0 = 0; q0 < K * M; q0 += 64 * kNarrowTagLoads) {
-                int cq[kNarrowTagLoads];
+                if (q0 > 0) {
 #pragma unroll
-                for (int u = 0; u < kNarrowTagLoads; ++u) {
-                    const int q = q0 + 64 * u + lane;
-                    const int k = q / M;
-                    cq[u] = __shfl(cnt, k < K ? k : 0);  // every lane: the shuffle reads other lanes
-                    if (q0 > 0) (void)read_tagged(sl32 + 2 * (q < K * M ? q : K * M - 1), tlo[u], thi[u]);
-                }
-#pragma unroll
-                for (int u = 0; u < kNarrowTagLoads; ++u) {
-                    const int q = q0 + 64 * u + lane;
-                    const int k = q / M;
-                    if (q >= K * M || q - k * M >= cq[u]) continue;
-                    if (thi[u] == 0u && !wait_tagged(p, sl32 + 2 * q, tlo[u], thi[u])) {
-                        lost_e = true;
-                        thi[u] = 1;
+                    for (int u = 0; u < kNarrowTagLoads; ++u) {
+                        const int q = q0 + 64 * u + lane;
+                        (void)read_tagged(sl32 + 2 * (q < K * M ? q : K * M - 1), tlo[u], thi[u]);
                     }
-                    s_sl[q] = ShortEntry{bits_f32(tlo[u]), static_cast<int32_t>(thi[u]) - 1};
+                }
+                bool missing = false;
+#pragma unroll
+                for (int u = 0; u < kNarrowTagLoads; ++u) {
+                    const int q = q0 + 64 * u + lane;
+                    if (q >= K * M) continue;
+                    if (thi[u] != 0u) s_sl[q] = ShortEntry{bits_f32(tlo[u]), static_cast<int32_t>(thi[u]) - 1};
+                    else missing = true;
+                }
+                if (__builtin_amdgcn_ballot_w64(missing) != 0) {
+#pragma unroll
+                    for (int u = 0; u < kNarrowTagLoads; ++u) {
+                        const int q = q0 + 64 * u + lane;
+                        const int k = q / M;
+                        const int cq = __shfl(cnt, k < K ? k : 0);  // every lane: the shuffle reads other lanes
+                        if (q >= K * M || q - k * M >= cq || thi[u] != 0u) continue;
+                        if (!wait_tagged(p, sl32 + 2 * q, tlo[u], thi[u])) {
+                            lost_e = true;
+                            thi[u] = 1;
+                        }
+                        s_sl[q] = ShortEntry{bits_f32(tlo[u]), static_cast<int32_t>(thi[u]) - 1};
+                    }
                 }
             }
             if (__builtin_amdgcn_ballot_w64(lost_e) != 0) {
