@@ -739,15 +739,21 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
 #pragma unroll
                     for (int u = 0; u < kStageTags; ++u) {
                         const int i = i0 + u * kSelectThreads;
-                        if (i >= n || i % M >= s.rcount[i / M]) continue;
-                        if (hi[u] == 0u && !wait_tagged(p, src32 + 2 * i, lo[u], hi[u])) {
-                            atomicOr(&st.gave_up, 1);
-                            hi[u] = 1;
+                        if (i >= n) continue;
+                        const int k = i / M, j = i - k * M;
+                        // a word not yet written is waited for only within its
+                        // row's count (the rest are never written)
+                        if (hi[u] == 0u) {
+                            if (j >= s.rcount[k]) continue;
+                            if (!wait_tagged(p, src32 + 2 * i, lo[u], hi[u])) {
+                                atomicOr(&st.gave_up, 1);
+                                hi[u] = 1;
+                            }
                         }
                         ShortEntry e;
                         e.lp = bits_f32(lo[u]);
                         e.token = static_cast<int32_t>(hi[u]) - 1;
-                        s.sl[SL == M ? i : sl_at(i / M, i % M, SL)] = e;
+                        s.sl[SL == M ? i : sl_at(k, j, SL)] = e;
                     }
                 }
             } else {
