@@ -245,7 +245,8 @@ int check_per_example(const DBSCudaDecodeArgs& a, int32_t* status, hipStream_t s
 int decode_common(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                   const DBSCudaSearchOptions* options, const uint8_t* banned_pe, const DBSCudaDecodeOutputs* outputs,
                   float* row_lse, void* workspace, int64_t workspace_bytes, void* stream_ptr,
-                  bool allow_overlap = true, int32_t* first_invalid = nullptr, int32_t** fault_out = nullptr) {
+                  bool allow_overlap = true, int32_t* first_invalid = nullptr, int32_t** fault_out = nullptr,
+                  const int32_t* forced = nullptr) {
     if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !outputs || !outputs->final_scores)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
@@ -283,6 +284,7 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
     p.steps = a.steps_per_example;
     p.banned = a.banned_tokens;
     p.banned_pe = banned_pe;
+    p.forced = forced;
     p.rowinfo = reinterpret_cast<RowInfo*>(ws + L.off_rowinfo);
     p.shortlist = reinterpret_cast<ShortEntry*>(ws + L.off_short);
     p.prefix = reinterpret_cast<int32_t*>(ws + L.off_prefix);
@@ -312,7 +314,7 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
 int step_common(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                 const DBSCudaSearchOptions* options, const DBSCudaBeamState* state,
                 const DBSCudaDecodeOutputs* outputs, float* row_lse, void* workspace, int64_t workspace_bytes,
-                void* stream_ptr) {
+                void* stream_ptr, const int32_t* forced = nullptr) {
     if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !state || !outputs)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
@@ -351,6 +353,7 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
     p.M = L.M;
     p.use_tau = 0;
     p.banned = a.banned_tokens;
+    p.forced = forced;
     p.rowinfo = reinterpret_cast<RowInfo*>(ws + L.off_rowinfo);
     p.shortlist = reinterpret_cast<ShortEntry*>(ws + L.off_short);
     p.blocked = reinterpret_cast<int32_t*>(ws + L.off_blocked);
@@ -433,10 +436,19 @@ namespace dbs_hip {
 
 int decode_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                     const DBSCudaSearchOptions* options, const uint8_t* banned_per_example,
-                    const DBSCudaDecodeOutputs* outputs, float* row_lse, int32_t* first_invalid, void* workspace,
-                    int64_t workspace_bytes, hipStream_t stream, int32_t** fault) {
+                    const DBSCudaDecodeOutputs* outputs, float* row_lse, int32_t* first_invalid,
+                    const int32_t* forced, void* workspace, int64_t workspace_bytes, hipStream_t stream,
+                    int32_t** fault) {
     return decode_common(inputs, data_type, from_logits, args, options, banned_per_example, outputs, row_lse,
-                         workspace, workspace_bytes, stream, true, first_invalid, fault);
+                         workspace, workspace_bytes, stream, true, first_invalid, fault, forced);
+}
+
+int step_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
+                  const DBSCudaSearchOptions* options, const DBSCudaBeamState* state,
+                  const DBSCudaDecodeOutputs* outputs, const int32_t* forced, void* workspace,
+                  int64_t workspace_bytes, hipStream_t stream) {
+    return step_common(inputs, data_type, from_logits, args, options, state, outputs, nullptr, workspace,
+                       workspace_bytes, stream, forced);
 }
 
 int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, float* draws,

@@ -82,6 +82,9 @@ struct DecodeParams {
     const int32_t* steps;     // device [B] or null
     const uint8_t* banned;    // device [V] or null
     const uint8_t* banned_pe; // device [B, V] or null
+    // device [B, T] (step mode: [B]) or null: an entry >= 0 is the one token
+    // a read beam may take at that step (reference src/decoder.cpp:125)
+    const int32_t* forced;
     RowInfo* rowinfo;         // [rows]
     ShortEntry* shortlist;    // [rows, M]
     int32_t* prefix;          // [B, 2, K, P] when constrained and not kept in LDS (P = prefix capacity)

@@ -179,6 +179,22 @@ void run_decode(DBSDecoderHandle* h, const DecodeJob& j) {
     a.min_lengths_per_example = upload(h, kMinLengths, j.min_lengths, static_cast<size_t>(B), st);
     a.banned_tokens = upload(h, kBanned, j.banned, static_cast<size_t>(V), st);
     const uint8_t* banned_pe = upload(h, kBannedPe, j.banned_pe, mul(static_cast<size_t>(B), V, "banned size"), st);
+    // forced tokens as the device reads them: [B, T], -1 past an example's
+    // steps; none at all when no step is forced (the decode keeps every
+    // select pass open to it)
+    std::vector<int32_t>& forced_bt = h->staged_forced;
+    bool any_forced = false;
+    if (j.forced) {
+        const std::vector<int32_t> steps_b = steps_of(j.steps, B, T);
+        forced_bt.assign(mul(static_cast<size_t>(B), static_cast<size_t>(T), "forced size"), -1);
+        for (int b = 0; b < B; ++b)
+            for (int t = 0; t < steps_b[static_cast<size_t>(b)]; ++t) {
+                const int32_t f = j.forced[static_cast<size_t>(b) * j.forced_stride + t];
+                forced_bt[static_cast<size_t>(b) * T + t] = f;
+                any_forced = any_forced || f >= 0;
+            }
+    }
+    const int32_t* forced = upload(h, kForced, any_forced ? forced_bt.data() : nullptr, forced_bt.size(), st);
     DBSCudaSearchOptions opts{};
     opts.extra_eos_count = static_cast<int>(h->extra_eos.size());
     for (size_t i = 0; i < h->extra_eos.size(); ++i) opts.extra_eos_tokens[i] = h->extra_eos[i];
@@ -202,7 +218,7 @@ void run_decode(DBSDecoderHandle* h, const DecodeJob& j) {
     void* ws = h->arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
     int32_t* fault = nullptr;
     engine_check(dbs_hip::decode_for_host(x, j.data_type, j.from_logits ? 1 : 0, &a, &opts, banned_pe, &o, row_lse,
-                                          first_invalid, ws, ws_bytes, st, &fault),
+                                          first_invalid, forced, ws, ws_bytes, st, &fault),
                  "HIP decode");
     int32_t gave_up = 0;
     if (fault) download(&gave_up, fault, 1, st);
@@ -360,13 +376,14 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
     for (int32_t tok : h->extra_eos)
         if (tok >= V) example_error(0, "an extra EOS token is outside the vocabulary");
     if (cons && cons->forced_tokens) {
-        for (int t = 0; t < steps_b[0]; ++t)
-            if (cons->forced_tokens[t] >= V) example_error(0, "forced token is outside the vocabulary");
+        // the shared array, as far as each example's own steps read it
+        for (int b = 0; b < B; ++b)
+            for (int t = 0; t < steps_b[static_cast<size_t>(b)]; ++t)
+                if (cons->forced_tokens[t] >= V) example_error(b, "forced token is outside the vocabulary");
     }
     if (cons && (!(rep > 0.0f) || !std::isfinite(rep)))
         example_error(0, "repetition_penalty must be finite and positive (1 disables it)");
     // What the GPU engine does not serve.
-    need(!(cons && cons->forced_tokens), "forced_tokens are not served by libdbs_hip (the HIP engine)");
     need(!(cons && cons->token_filter), "token_filter callbacks are not served by libdbs_hip (the HIP engine)");
     need(!pool, "relaxed-pool outputs are not served by libdbs_hip (the HIP engine)");
 
@@ -380,6 +397,7 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
     j.V = V;
     j.steps = steps_per_example;
     j.banned = cons ? cons->banned_tokens : nullptr;
+    j.forced = cons ? cons->forced_tokens : nullptr;
     j.min_length = min_length;
     j.ngram = cons && cons->no_repeat_ngram_size > 0 ? cons->no_repeat_ngram_size : 0;
     j.repetition_penalty = rep;

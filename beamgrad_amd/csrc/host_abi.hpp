@@ -28,7 +28,7 @@ namespace dbs_host {
 enum Slot : int {
     kInputs, kBanned, kBannedPe, kSteps, kBeams, kEos, kMinLengths, kFinalScores, kFinalRaw, kFinalLengths, kTokens,
     kParents, kLengths, kScores, kRawScores, kFromLogprob, kRowLse, kFirstInvalid, kWorkspace, kGradFinal,
-    kGradFinalRaw, kGradScores, kGradRaw, kDraws, kDense, kState, kSlotCount
+    kGradFinalRaw, kGradScores, kGradRaw, kDraws, kDense, kState, kForced, kSlotCount
 };
 
 struct Arena {
@@ -70,6 +70,9 @@ struct DBSDecoderHandle {
 
     std::mutex run_mutex;  // one GPU call at a time on a handle
     dbs_host::Arena arena;
+    // host arrays the handle builds for a copy to the device (they outlive
+    // the asynchronous copy; guarded by run_mutex)
+    std::vector<int32_t> staged_forced;
     hipStream_t stream = nullptr;
     int device = -1;
 
@@ -178,6 +181,10 @@ struct DecodeJob {
     const int32_t* min_lengths = nullptr;
     const uint8_t* banned = nullptr;     // [V], every example
     const uint8_t* banned_pe = nullptr;  // [B, V]
+    // forced tokens: example b's step t reads forced[b * forced_stride + t]
+    // (stride 0: one [T] array for every example), for t below its steps
+    const int32_t* forced = nullptr;
+    size_t forced_stride = 0;
     int min_length = 0;
     int ngram = 0;
     float repetition_penalty = 1.0f;

@@ -13,7 +13,7 @@
 // stages arrays, derives the selected-beam softmax weights of each step from
 // the selected scores, and turns the device's per-slot path gradients into
 // the reference's gradient layouts. What the engine does not serve (the
-// relaxed pool, forced tokens, token-filter callbacks) is refused with
+// relaxed pool, token-filter callbacks) is refused with
 // DBS_ERROR_INVALID_ARGUMENT and a message naming it.
 #include <algorithm>
 #include <chrono>
@@ -23,6 +23,7 @@
 
 #include "dbs_cuda.h"
 #include "host_abi.hpp"
+#include "host_entry.hpp"
 #include "numerics.hpp"
 
 struct DBSResultHandle {
@@ -98,7 +99,8 @@ DBSDecoderHandle& handle_of(DBSDecoderHandle* h) {
 
 // A decode's constraints as the decoder reads them (reference
 // src/c_api.cpp:191-203, src/decoder.cpp:385-406); the GPU serves banned
-// tokens, min_length, n-gram blocking and the repetition penalty.
+// tokens, forced tokens, min_length, n-gram blocking and the repetition
+// penalty.
 struct Constraints {
     const uint8_t* banned = nullptr;
     const int32_t* forced = nullptr;
@@ -139,15 +141,9 @@ void check_decode_args(const DBSDecoderHandle& h, int K, int eos, int steps, int
 }
 
 // What the HIP engine does not serve, after the reference's own checks.
-void check_served(const DBSDecoderHandle& h, const Constraints* c, int steps) {
+void check_served(const DBSDecoderHandle& h, const Constraints* c) {
     need(h.pool_multiplier <= 0, "relaxed-pool outputs are not served by libdbs_hip (the HIP engine)");
-    if (c) {
-        need(!c->filter, "token_filter callbacks are not served by libdbs_hip (the HIP engine)");
-        if (c->forced) {
-            for (int t = 0; t < steps; ++t)
-                need(c->forced[t] < 0, "forced_tokens are not served by libdbs_hip (the HIP engine)");
-        }
-    }
+    if (c) need(!c->filter, "token_filter callbacks are not served by libdbs_hip (the HIP engine)");
 }
 
 // Result b of a [B, T, Kmax] trace: its first `steps` steps and `beams`
@@ -202,6 +198,7 @@ struct BatchSpec {
     const int32_t* eos = nullptr;
     const int32_t* min_lengths = nullptr;
     const uint8_t* banned_pe = nullptr;
+    const int32_t* forced_pe = nullptr;  // [B, T] forced tokens per example
     const Constraints* cons = nullptr;  // every example
     bool batch_errors = true;
 };
@@ -225,6 +222,8 @@ std::vector<DBSResultHandle> decode_results(DBSDecoderHandle& h, const BatchSpec
     j.banned_pe = s.banned_pe;
     j.min_length = s.cons && s.cons->min_length >= 0 ? s.cons->min_length : h.min_length;
     j.banned = s.cons ? s.cons->banned : nullptr;
+    j.forced = s.cons ? s.cons->forced : s.forced_pe;
+    j.forced_stride = s.cons ? 0 : static_cast<size_t>(s.T);
     j.ngram = s.cons && s.cons->ngram > 0 ? s.cons->ngram : 0;
     j.repetition_penalty = s.cons ? s.cons->repetition_penalty : 1.0f;
     j.batch_errors = s.batch_errors;
@@ -277,7 +276,7 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
                                    int64_t* rows_bytes) {
     const int K = h.beam_size;
     check_decode_args(h, K, h.eos_token, steps, V, c);
-    check_served(h, c, steps);
+    check_served(h, c);
     check_engine_limits(&h, K, V);
     const size_t row_block = static_cast<size_t>(K) * V;
     const size_t prefix_size = mul(static_cast<size_t>(K), static_cast<size_t>(steps), "prefix size overflow");
@@ -383,8 +382,14 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
             o.from_logprob = static_cast<uint8_t*>(h.arena.get(kFromLogprob, K));
             o.invalid_input = h.validate ? static_cast<uint8_t*>(h.arena.get(kFirstInvalid, 16)) : nullptr;
             void* ws = h.arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
-            engine_check(dbs_cuda_decode_step_ex2(rows_d, DBS_CUDA_DTYPE_F32, 0, &a, &opts, &bs, &o, nullptr, ws,
-                                                  ws_bytes, st),
+            // this step's forced token, if any (reference src/decoder.cpp:125)
+            const int32_t* forced_d = nullptr;
+            if (c && c->forced && c->forced[t] >= 0) {
+                h.staged_forced.assign(1, c->forced[t]);
+                forced_d = upload(&h, kForced, h.staged_forced.data(), 1, st);
+            }
+            engine_check(dbs_hip::step_for_host(rows_d, DBS_CUDA_DTYPE_F32, 0, &a, &opts, &bs, &o, forced_d, ws,
+                                                ws_bytes, st),
                          "HIP decode step");
             download(out_tok.data(), o.tokens, K, st);
             download(out_par.data(), o.parents, K, st);
@@ -582,7 +587,7 @@ DBS_EXPORT int dbs_decode_constrained_ex(DBSDecoderHandle* handle, const float* 
         const Constraints* cp = constraints ? &c : nullptr;
         need(log_probs != nullptr, "log_probs cannot be null");
         check_decode_args(h, h.beam_size, h.eos_token, steps, vocab_size, cp);
-        check_served(h, cp, steps);
+        check_served(h, cp);
         BatchSpec s;
         s.inputs = log_probs;
         s.B = 1;
@@ -623,7 +628,7 @@ DBS_EXPORT int dbs_decode_typed(DBSDecoderHandle* handle, const void* log_probs,
         const auto start = std::chrono::steady_clock::now();
         need(log_probs != nullptr, "log_probs cannot be null");
         check_decode_args(h, h.beam_size, h.eos_token, steps, vocab_size, nullptr);
-        check_served(h, nullptr, steps);
+        check_served(h, nullptr);
         BatchSpec s;
         s.inputs = log_probs;
         s.data_type = data_type;
@@ -659,7 +664,7 @@ DBS_EXPORT int dbs_decode_batch_typed(DBSDecoderHandle* handle, const void* log_
         } catch (const std::invalid_argument& e) {
             example_error(0, e.what());  // the options are shared: example 0 fails first
         }
-        check_served(h, nullptr, steps);
+        check_served(h, nullptr);
         BatchSpec s;
         s.inputs = log_probs;
         s.data_type = data_type;
@@ -730,12 +735,7 @@ DBS_EXPORT int dbs_decode_batch_variable(DBSDecoderHandle* handle, const float* 
                 example_error(b, e.what());
             }
         }
-        for (int b = 0; b < batch_size; ++b) {
-            Constraints c;
-            c.forced = forced_tokens_per_example ? forced_tokens_per_example + static_cast<size_t>(b) * max_steps
-                                                 : nullptr;
-            check_served(h, &c, steps_b[static_cast<size_t>(b)]);
-        }
+        check_served(h, nullptr);
         BatchSpec s;
         s.inputs = log_probs;
         s.B = batch_size;
@@ -747,6 +747,7 @@ DBS_EXPORT int dbs_decode_batch_variable(DBSDecoderHandle* handle, const float* 
         s.eos = eos_b.data();
         s.min_lengths = min_b.data();
         s.banned_pe = banned_tokens_per_example;
+        s.forced_pe = forced_tokens_per_example;
         auto br = std::make_unique<DBSBatchResultHandle>();
         br->results = decode_results(h, s);
         record_result_stats(h, br->results.front(), ns_since(start), false);

@@ -792,7 +792,9 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             }
             step_barrier(lists_global);
         }
-        if (p.use_tau) {
+        // a forced step (uniform over the workgroup): no shortlist is used
+        const int forced = p.forced ? gload(p.forced, static_cast<int64_t>(b) * T + t) : -1;
+        if (p.use_tau && forced < 0) {
             // Lower bounds of the K-th best expanded raw (unconstrained: raw =
             // fl(p + lp), monotone in lp; every beam expanded has the same
             // length, so this step's shortlisted candidates rank by raw).
@@ -855,9 +857,33 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 offer(s, st, c);
             }
         }
+        if (forced >= 0) {
+            // A forced step (reference src/decoder.cpp:125-167,
+            // src/kernels_scalar.cpp:16-26): a read beam's one candidate is
+            // the forced token, under every check another candidate meets (a
+            // finite log-prob, banned tokens, the EOS mask below min_length,
+            // n-gram blocking, the repetition penalty). At most K of them
+            // join the carried beams: 2K <= sort_cap. (The host refuses forced
+            // tokens outside the vocabulary; the bound keeps the read in the
+            // row regardless.)
+            for (int k = tid; k < K; k += kSelectThreads) {
+                if (s.rcount[k] == -2 || forced >= p.V) continue;
+                const int64_t row = p.step_mode ? static_cast<int64_t>(b) * K + k : trace0 + k;
+                const float x = load_one<DT>(static_cast<const char*>(p.x) +
+                                                 static_cast<size_t>(row) * static_cast<size_t>(p.V) * (DT == 0 ? 4 : 2),
+                                             forced);
+                const float lp = LOGITS ? x - s.nraw[k] : x;
+                const int new_len = s.len[k] + 1;
+                if (!(lp < kInf) || lp == -kInf || static_masked(p, b, forced, new_len < min_length_of(p, b))) continue;
+                Cand c;
+                if (make_cand(p, s, prefix_of(p, s, b, k, cur), k, s.raw[k], inv_of(s, pen_len, new_len, p.alpha),
+                              forced, new_len, lp, c))
+                    offer(s, st, c);
+            }
+        }
         // (at most K offers: the first round of shortlisted offers joins them
         // unless the one-pass path below needs the count)
-        if (M > 0 && p.use_tau && K >= kWideBeam) end_round(s, st, K, L.sort_cap);
+        if (M > 0 && p.use_tau && K >= kWideBeam && forced < 0) end_round(s, st, K, L.sort_cap);
 
         // Shortlisted candidates. Unconstrained wide beams: few reach tau, and
         // when they fit the collector beside what it holds, they are offered
@@ -866,7 +892,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         // are a prefix of it: one thread per beam measures its prefix, then
         // offers it.
         bool one_pass = false;
-        if (M > 0 && p.use_tau && K >= kWideBeam) {
+        if (M > 0 && p.use_tau && K >= kWideBeam && forced < 0) {
             // (K <= 64 with a shortlist: lane k of wavefront 0 measures beam
             // k's prefix, eight entries a round; a lane scan places the
             // prefixes at consecutive collector slots, and the four
@@ -913,7 +939,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 if (tid == 0) st.count = st.rcount;
             }
         }
-        if (M > 0 && !one_pass) {
+        if (M > 0 && !one_pass && forced < 0) {
             const float tau = st.tau;
             for (int base = 0; base < K * M; base += kSelectThreads) {
                 const int item = base + tid;
@@ -943,7 +969,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         // strictly before that bound's score and raw.
         for (int k = tid; k < K; k += kSelectThreads) {
             const int cnt = s.rcount[k];
-            if (cnt == -2) continue;
+            if (cnt == -2 || forced >= 0) continue;  // a forced step read its rows whole
             bool fail = cnt < 0;
             if (!fail && s.rbound[k] > -kInf) {
                 const float X = s.raw[k] + s.rbound[k];
@@ -2005,7 +2031,7 @@ std::atomic<int> g_select_kind{0};
 
 bool select_narrow(const DecodeParams& p) {
     if (g_select_kind.load(std::memory_order_relaxed) == 1) return false;
-    if (p.step_mode || p.M <= 0 || p.K > kNarrowMaxK || p.V > (1 << 24)) return false;
+    if (p.step_mode || p.forced || p.M <= 0 || p.K > kNarrowMaxK || p.V > (1 << 24)) return false;
     // constrained: n-gram blocking of n >= 2 and/or a repetition penalty
     // (n = 1 blocking would drop most of a long prefix's shortlist entries)
     if (p.constrained) return p.ngram != 1 && narrow_sig_words(p) > 0;

@@ -23,9 +23,11 @@
  * All 81 functions of the reference's ABI are exported. What the GPU engine
  * does not serve is refused with DBS_ERROR_INVALID_ARGUMENT and a message
  * naming it: the relaxed pool (relaxed_pool_multiplier > 0 and the pool
- * outputs and gradients), forced tokens (a forced_tokens entry >= 0) and
- * token-filter callbacks. Result handles therefore have no pool
- * (dbs_result_pool_size 0, pool accessors NULL).
+ * outputs and gradients) and token-filter callbacks. Result handles
+ * therefore have no pool (dbs_result_pool_size 0, pool accessors NULL).
+ * Forced tokens (an entry >= 0: the one token a read beam may take at that
+ * step) are served by every decode that takes them: the batch decodes into
+ * caller arrays, the result-handle decodes and the model-step decodes.
  */
 #pragma once
 
@@ -128,10 +130,10 @@ typedef int (*DBSTokenFilterFn)(
     int token);
 
 /* Constraints shared by every example of a batch (reference
- * include/dbs.h:139-148). forced_tokens and token_filter must be NULL here. */
+ * include/dbs.h:139-148). token_filter must be NULL here. */
 typedef struct DBSAdvancedConstraintsC {
     const uint8_t* banned_tokens;        /* [V] or NULL: non-zero bans the token */
-    const int32_t* forced_tokens;        /* must be NULL */
+    const int32_t* forced_tokens;        /* [T] or NULL: an entry >= 0 (< V) forces that token at step t */
     int min_length;                      /* negative: the handle's min_length */
     float repetition_penalty;            /* <= 1 disables; 0 (zero-initialised) means 1 */
     int no_repeat_ngram_size;            /* <= 0 disables */
@@ -317,8 +319,8 @@ DBS_EXPORT int64_t dbs_workspace_allocated_bytes(DBSWorkspaceHandle* workspace);
  * include/dbs.h:215-299, 412-437). One example: log_probs [T, K, V]; a
  * batch: [B, T, K, V]; dbs_decode_batch_variable: [B, max_steps,
  * max_beam_size, V] with per-example steps, beam sizes, EOS tokens, minimum
- * lengths and banned masks [B, V] (forced_tokens_per_example [B, max_steps]
- * must hold no entry >= 0). Each result holds the trace, the selected-beam
+ * lengths, banned masks [B, V] and forced tokens [B, max_steps] (an entry
+ * >= 0 forces that token). Each result holds the trace, the selected-beam
  * softmax weights of every step and the final scores. num_threads is
  * accepted and ignored (the GPU decodes every example at once). ---- */
 DBS_EXPORT int dbs_decode(

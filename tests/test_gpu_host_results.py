@@ -446,9 +446,11 @@ def test_refusals_name_what_is_not_served(libs):
     assert "relaxed-pool outputs are not served" in ours.error()
     ours.destroy(h)
     h = ours.create(beam_size=K)
-    forced = np.array([-1, 3, -1], np.int32)
-    assert L.dbs_decode_constrained(h, _p(x, C.c_float), T, V, None, _p(forced, C.c_int32), 0, C.byref(r)) == -1
-    assert "forced_tokens are not served" in ours.error()
+    keep = {}
+    c = HostLib.constraints(keep=keep)
+    c.token_filter = C.c_void_p(1)
+    assert L.dbs_decode_constrained_ex(h, _p(x, C.c_float), T, V, C.byref(c), C.byref(r)) == -1
+    assert "token_filter callbacks are not served" in ours.error()
     ours.destroy(h)
 
 

@@ -187,6 +187,9 @@ DECODE_ERRORS = {
     "steps_per_example zero": (dict(beam_size=2), dict(steps=[0, 1])),
     "infinite repetition penalty": (dict(beam_size=2), dict(rep=float("inf"))),
     "bad dtype": (dict(beam_size=2), dict(dtype=5)),
+    "forced token outside vocabulary": (dict(beam_size=2), dict(forced=[9, -1, -1])),
+    # the shared array as far as each example's steps read it: example 1 fails
+    "forced token outside vocabulary, second example": (dict(beam_size=2), dict(forced=[1, -1, 9], steps=[2, 3])),
 }
 
 
@@ -200,8 +203,8 @@ def test_decode_argument_errors_match(ours, ref, case):
     def call(lib, h):
         keep = {}
         cons = None
-        if "rep" in kw:
-            cons = HostLib.constraints(repetition_penalty=kw["rep"], keep=keep)
+        if "rep" in kw or "forced" in kw:
+            cons = HostLib.constraints(repetition_penalty=kw.get("rep", 1.0), forced=kw.get("forced"), keep=keep)
         if "dtype" in kw:
             o = OutputsExC()
             fs = np.zeros((2, 2), np.float32)
@@ -303,17 +306,15 @@ def test_backward_argument_errors_match(ours, ref):
 
 
 def test_features_the_engine_does_not_serve_are_refused(ours):
-    """Forced tokens, token filters, the relaxed pool and beams beyond the
-    device ABI's limit are refused with INVALID_ARGUMENT before any device
-    work (the reference's CPU library serves them)."""
+    """Token filters, the relaxed pool and beams beyond the device ABI's
+    limit are refused with INVALID_ARGUMENT before any device work (the
+    reference's CPU library serves them)."""
     import ctypes as C
 
     x = np.zeros((1, 2, 2, 5), np.float32)
     h = ours.create(beam_size=2, relaxed_pool_multiplier=2)
     try:
         keep = {}
-        st, _ = ours.decode(h, x, 2, constraints=HostLib.constraints(forced=[1, -1], keep=keep))
-        assert st == -1 and "forced_tokens" in ours.error()
         cons = HostLib.constraints(keep=keep)
         cons.token_filter = C.c_void_p(1)
         st, _ = ours.decode(h, x, 2, constraints=cons)
