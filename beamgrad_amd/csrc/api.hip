@@ -242,18 +242,33 @@ int check_per_example(const DBSCudaDecodeArgs& a, int32_t* status, hipStream_t s
     return host != 0 ? DBS_CUDA_STATUS_INVALID_ARGUMENT : DBS_CUDA_STATUS_OK;
 }
 
+void set_pool(DecodeParams& p, const PoolOutputs* pool) {
+    if (!pool || pool->mult <= 0) return;
+    p.pool_mult = pool->mult;
+    p.pool_parents = pool->parents;
+    p.pool_tokens = pool->tokens;
+    p.pool_lengths = pool->lengths;
+    p.pool_scores = pool->scores;
+    p.pool_raw = pool->raw_scores;
+    p.pool_flp = pool->from_logprob;
+}
+
 int decode_common(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                   const DBSCudaSearchOptions* options, const uint8_t* banned_pe, const DBSCudaDecodeOutputs* outputs,
                   float* row_lse, void* workspace, int64_t workspace_bytes, void* stream_ptr,
                   bool allow_overlap = true, int32_t* first_invalid = nullptr, int32_t** fault_out = nullptr,
-                  const int32_t* forced = nullptr) {
+                  const int32_t* forced = nullptr, const PoolOutputs* pool = nullptr) {
     if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !outputs || !outputs->final_scores)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     const DBSCudaDecodeArgs& a = *args;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     const bool cons = constrained(a);
-    const DecodeLayout L = decode_layout(a.batch_size, a.steps, a.beam_size, a.vocab_size, cons, false, 0);
+    const int pool_mult = pool ? pool->mult : 0;
+    if (pool_mult < 0 || static_cast<int64_t>(pool_mult) * a.beam_size > DBS_CUDA_MAX_BEAM)
+        return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    const DecodeLayout L =
+        decode_layout(a.batch_size, a.steps, a.beam_size, a.vocab_size, cons, false, 0, pool_mult * a.beam_size);
     bool too_small = false;
     Scratch scratch;
     hipError_t e = scratch.acquire(workspace, workspace_bytes, L.total, stream, &too_small);
@@ -285,6 +300,7 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
     p.banned = a.banned_tokens;
     p.banned_pe = banned_pe;
     p.forced = forced;
+    set_pool(p, pool);
     p.rowinfo = reinterpret_cast<RowInfo*>(ws + L.off_rowinfo);
     p.shortlist = reinterpret_cast<ShortEntry*>(ws + L.off_short);
     p.prefix = reinterpret_cast<int32_t*>(ws + L.off_prefix);
@@ -314,7 +330,7 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
 int step_common(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                 const DBSCudaSearchOptions* options, const DBSCudaBeamState* state,
                 const DBSCudaDecodeOutputs* outputs, float* row_lse, void* workspace, int64_t workspace_bytes,
-                void* stream_ptr, const int32_t* forced = nullptr) {
+                void* stream_ptr, const int32_t* forced = nullptr, const PoolOutputs* pool = nullptr) {
     if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !state || !outputs)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
@@ -325,7 +341,11 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
     const bool cons = constrained(a);
     if (cons && state->prefix_stride > 0 && !state->prefixes) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    const DecodeLayout L = decode_layout(a.batch_size, 1, a.beam_size, a.vocab_size, cons, true, state->prefix_stride);
+    const int pool_mult = pool ? pool->mult : 0;
+    if (pool_mult < 0 || static_cast<int64_t>(pool_mult) * a.beam_size > DBS_CUDA_MAX_BEAM)
+        return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    const DecodeLayout L = decode_layout(a.batch_size, 1, a.beam_size, a.vocab_size, cons, true, state->prefix_stride,
+                                         pool_mult * a.beam_size);
     bool too_small = false;
     Scratch scratch;
     hipError_t e = scratch.acquire(workspace, workspace_bytes, L.total, stream, &too_small);
@@ -354,6 +374,7 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
     p.use_tau = 0;
     p.banned = a.banned_tokens;
     p.forced = forced;
+    set_pool(p, pool);
     p.rowinfo = reinterpret_cast<RowInfo*>(ws + L.off_rowinfo);
     p.shortlist = reinterpret_cast<ShortEntry*>(ws + L.off_short);
     p.blocked = reinterpret_cast<int32_t*>(ws + L.off_blocked);
@@ -437,18 +458,28 @@ namespace dbs_hip {
 int decode_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                     const DBSCudaSearchOptions* options, const uint8_t* banned_per_example,
                     const DBSCudaDecodeOutputs* outputs, float* row_lse, int32_t* first_invalid,
-                    const int32_t* forced, void* workspace, int64_t workspace_bytes, hipStream_t stream,
-                    int32_t** fault) {
+                    const int32_t* forced, const PoolOutputs* pool, void* workspace, int64_t workspace_bytes,
+                    hipStream_t stream, int32_t** fault) {
     return decode_common(inputs, data_type, from_logits, args, options, banned_per_example, outputs, row_lse,
-                         workspace, workspace_bytes, stream, true, first_invalid, fault, forced);
+                         workspace, workspace_bytes, stream, true, first_invalid, fault, forced, pool);
 }
 
 int step_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                   const DBSCudaSearchOptions* options, const DBSCudaBeamState* state,
-                  const DBSCudaDecodeOutputs* outputs, const int32_t* forced, void* workspace,
-                  int64_t workspace_bytes, hipStream_t stream) {
+                  const DBSCudaDecodeOutputs* outputs, const int32_t* forced, const PoolOutputs* pool,
+                  void* workspace, int64_t workspace_bytes, hipStream_t stream) {
     return step_common(inputs, data_type, from_logits, args, options, state, outputs, nullptr, workspace,
-                       workspace_bytes, stream, forced);
+                       workspace_bytes, stream, forced, pool);
+}
+
+int64_t workspace_for_host(const DBSCudaDecodeArgs* args, int pool_mult, int step_mode, int prefix_stride) {
+    if (!valid_args(args) || pool_mult < 0 || static_cast<int64_t>(pool_mult) * args->beam_size > DBS_CUDA_MAX_BEAM)
+        return -1;
+    if (step_mode && (args->steps != 1 || args->steps_per_example || prefix_stride < 0)) return -1;
+    return static_cast<int64_t>(decode_layout(args->batch_size, step_mode ? 1 : args->steps, args->beam_size,
+                                              args->vocab_size, constrained(*args), step_mode != 0,
+                                              step_mode ? prefix_stride : 0, pool_mult * args->beam_size)
+                                    .total);
 }
 
 int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, float* draws,

@@ -100,20 +100,23 @@ __global__ void check_examples_kernel(const int32_t* steps, const int32_t* beams
 
 }  // namespace
 
-DecodeLayout decode_layout(int B, int T, int K, int V, bool constrained, bool step_mode, int prefix_stride) {
+DecodeLayout decode_layout(int B, int T, int K, int V, bool constrained, bool step_mode, int prefix_stride,
+                           int keep) {
     DecodeLayout L{};
-    // Shortlist length: K plus a margin, while the row pass can pick its
-    // threshold from the row's 256 lane maxima; wider beams rescan every row.
-    int M = K <= 64 ? ((K + 16 + 7) / 8) * 8 : 0;
+    // Shortlist length: the candidates kept per step (K, or the relaxed
+    // pool) plus a margin, while the row pass can pick its threshold from the
+    // row's 256 lane maxima; more rescan every row.
+    const int kept = keep > 0 ? keep : K;
+    int M = kept <= 64 ? ((kept + 16 + 7) / 8) * 8 : 0;
     if (const char* env = std::getenv("DBS_HIP_SHORTLIST")) {
         // testing knob: 0 forces full rescans, a small value forces fallbacks
         const int m = std::atoi(env);
         if (m >= 0 && m <= 256) M = m;
     }
     L.M = M;
-    L.use_tau = (!constrained && !step_mode && M > 0) ? 1 : 0;
+    L.use_tau = (!constrained && !step_mode && M > 0 && kept == K) ? 1 : 0;
     L.prefix_cap = step_mode ? prefix_stride : T + 1;
-    L.sel = select_layout(B, T, K, M, constrained, step_mode, L.prefix_cap);
+    L.sel = select_layout(B, T, K, M, constrained, step_mode, L.prefix_cap, kept);
     const int64_t rows = step_mode ? static_cast<int64_t>(B) * K : static_cast<int64_t>(B) * T * K;
     auto align = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
     size_t off = 0;
@@ -248,9 +251,10 @@ void wait_policy(DecodeParams& p) {
 }  // namespace
 
 size_t sync_bytes(int B, int T) {
-    // [B, T] step counts, the fault word (padded to 8 bytes), the row ticket
+    // [B, T] step counts, the fault word (padded to 8 bytes), the row ticket,
+    // the split launch's claims [B]
     return ((sizeof(int32_t) * static_cast<size_t>(B) * static_cast<size_t>(T) + 7) & ~static_cast<size_t>(7)) + 8 +
-           sizeof(unsigned long long);
+           sizeof(unsigned long long) + sizeof(int32_t) * static_cast<size_t>(B);
 }
 
 // The row pass, then the select pass. With several steps and at most half
@@ -321,6 +325,7 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     p.step_done = reinterpret_cast<int32_t*>(sync);
     p.fault = reinterpret_cast<int32_t*>(sync + counts);
     p.row_ticket = reinterpret_cast<unsigned long long*>(sync + counts + 8);
+    int32_t* claimed = reinterpret_cast<int32_t*>(sync + counts + 8 + sizeof(unsigned long long));
     p.reserve_cus = reserve;  // a persistent row pass would otherwise hold every CU until it ends
     wait_policy(p);
     std::lock_guard<std::mutex> lock(aux->mutex);
@@ -334,12 +339,28 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     // A persistent row pass is launched first: its grid leaves the select
     // pass's CUs free. A row pass of one workgroup per row would fill every
     // CU before the select pass's workgroups are placed, so the select pass
-    // goes first there (it waits for its rows).
+    // goes first there, split in two launches (DecodeParams::claimed): the
+    // early one before the row pass takes the examples whose first row comes
+    // within 200 us, the late one after it takes the rest. The streams are
+    // not guaranteed to run at once (HIP maps streams onto a few hardware
+    // queues, shared once there are more streams), and no select-pass wait
+    // may depend on a launch submitted after it.
     p.select_hold = hold ? 1 : 0;
     if (e == hipSuccess && persistent) e = launch_row_pass(p, stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(aux->stream, aux->start, 0);
-    if (e == hipSuccess) e = launch_select(p, L.sel, aux->stream);
-    if (e == hipSuccess && !persistent) e = launch_row_pass(p, stream);
+    if (persistent) {
+        if (e == hipSuccess) e = launch_select(p, L.sel, aux->stream);
+    } else {
+        DecodeParams early = p;
+        early.claimed = claimed;
+        early.early = 1;
+        early.early_ticks = 20000;  // 200 us of the 100 MHz counter
+        if (e == hipSuccess) e = launch_select(early, L.sel, aux->stream);
+        if (e == hipSuccess) e = launch_row_pass(p, stream);
+        DecodeParams late = early;
+        late.early = 0;
+        if (e == hipSuccess) e = launch_select(late, L.sel, aux->stream);
+    }
     if (e == hipSuccess) e = hipEventRecord(aux->done, aux->stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(stream, aux->done, 0);
     if (e == hipSuccess) *fault = p.fault;

@@ -85,6 +85,18 @@ struct DecodeParams {
     // device [B, T] (step mode: [B]) or null: an entry >= 0 is the one token
     // a read beam may take at that step (reference src/decoder.cpp:125)
     const int32_t* forced;
+    // Relaxed pool (reference src/decoder.cpp:40, 294-306): with pool_mult
+    // m >= 1 each step keeps the best m * beams candidates of an example, its
+    // pool, of which the first beams are the selection. Outputs [B, T, m * K]
+    // (any may be null); entries past the kept ones, and steps past an
+    // example's own, are dead (parent and token -1, length 0, -inf scores).
+    int pool_mult;
+    int32_t* pool_parents;
+    int32_t* pool_tokens;
+    int32_t* pool_lengths;
+    float* pool_scores;
+    float* pool_raw;
+    uint8_t* pool_flp;
     RowInfo* rowinfo;         // [rows]
     ShortEntry* shortlist;    // [rows, M]
     int32_t* prefix;          // [B, 2, K, P] when constrained and not kept in LDS (P = prefix capacity)
@@ -125,6 +137,16 @@ struct DecodeParams {
     int32_t* fault;
     unsigned long long wait_ticks;
     int wait_extra;
+    // Split launch of a select pass started before its row pass (null: one
+    // launch): the early launch (early = 1) takes example b only once the
+    // row pass has counted its first row within early_ticks, and marks it in
+    // claimed [B]; the late launch, submitted after the row pass, takes the
+    // examples left. Two streams that share one hardware queue run the three
+    // launches in submission order: the early launch then takes none, and no
+    // wait depends on a launch queued behind it.
+    int32_t* claimed;
+    int early;
+    unsigned long long early_ticks;
     // optional [B]: the first row holding NaN or +inf that example b's search
     // read, as t * K + k in reading order, or -1 (the host ABI's error text)
     int32_t* first_invalid;
@@ -150,8 +172,12 @@ struct DecodeLayout {
     size_t off_rowinfo, off_short, off_prefix, off_blocked, off_sync, total;
 };
 
-DecodeLayout decode_layout(int B, int T, int K, int V, bool constrained, bool step_mode, int prefix_stride);
-SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool step_mode, int prefix_cap);
+// keep: candidates a step keeps per example (0: K; the relaxed pool keeps
+// more), which sizes the shortlists and the select pass's collector.
+DecodeLayout decode_layout(int B, int T, int K, int V, bool constrained, bool step_mode, int prefix_stride,
+                           int keep = 0);
+SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool step_mode, int prefix_cap,
+                           int keep = 0);
 
 // Queues the decode (or one step) on `stream` with workspace ws; returns a
 // hipError_t.

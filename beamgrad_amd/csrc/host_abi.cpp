@@ -152,9 +152,20 @@ void check_engine_limits(const DBSDecoderHandle* h, int K, int V) {
                                     " extra EOS tokens are beyond the HIP engine");
 }
 
+int pool_size_of(int K, int m) {
+    if (m <= 0) return 0;
+    const int64_t P = static_cast<int64_t>(K) * m;
+    if (P > DBS_CUDA_MAX_BEAM)
+        throw std::invalid_argument("a relaxed pool of " + std::to_string(P) + " candidates (beam_size * " +
+                                    "relaxed_pool_multiplier) is beyond the HIP engine (at most " +
+                                    std::to_string(DBS_CUDA_MAX_BEAM) + ")");
+    return static_cast<int>(P);
+}
+
 void run_decode(DBSDecoderHandle* h, const DecodeJob& j) {
     const int B = j.B, T = j.T, K = j.K, V = j.V;
     check_engine_limits(h, K, V);
+    const int P = pool_size_of(K, j.pool_mult);
     const size_t BK = static_cast<size_t>(B) * K;
     const size_t BTK = mul(BK, static_cast<size_t>(T), "batch size overflow");
     const size_t elements = mul(BTK, static_cast<size_t>(V), "batch size overflow");
@@ -210,15 +221,26 @@ void run_decode(DBSDecoderHandle* h, const DecodeJob& j) {
     o.raw_scores = device_out(h, kRawScores, j.raw_scores, BTK);
     o.from_logprob = device_out(h, kFromLogprob, j.from_logprob, BTK);
     float* row_lse = device_out(h, kRowLse, j.row_lse, BTK);
+    const size_t BTP = static_cast<size_t>(B) * T * static_cast<size_t>(P);
+    dbs_hip::PoolOutputs pool;
+    if (P > 0) {
+        pool.mult = j.pool_mult;
+        pool.parents = device_out(h, kPoolParents, j.pool_parents, BTP);
+        pool.tokens = device_out(h, kPoolTokens, j.pool_tokens, BTP);
+        pool.lengths = device_out(h, kPoolLengths, j.pool_lengths, BTP);
+        pool.scores = device_out(h, kPoolScores, j.pool_scores, BTP);
+        pool.raw_scores = device_out(h, kPoolRaw, j.pool_raw, BTP);
+        pool.from_logprob = device_out(h, kPoolFromLogprob, j.pool_from_logprob, BTP);
+    }
     int32_t* first_invalid =
         h->validate ? static_cast<int32_t*>(h->arena.get(kFirstInvalid, sizeof(int32_t) * static_cast<size_t>(B)))
                     : nullptr;
-    const int64_t ws_bytes = dbs_cuda_decode_workspace_size(&a);
+    const int64_t ws_bytes = dbs_hip::workspace_for_host(&a, pool.mult, 0, 0);
     need(ws_bytes > 0, "invalid decode arguments");
     void* ws = h->arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
     int32_t* fault = nullptr;
     engine_check(dbs_hip::decode_for_host(x, j.data_type, j.from_logits ? 1 : 0, &a, &opts, banned_pe, &o, row_lse,
-                                          first_invalid, forced, ws, ws_bytes, st, &fault),
+                                          first_invalid, forced, P > 0 ? &pool : nullptr, ws, ws_bytes, st, &fault),
                  "HIP decode");
     int32_t gave_up = 0;
     if (fault) download(&gave_up, fault, 1, st);
@@ -237,6 +259,14 @@ void run_decode(DBSDecoderHandle* h, const DecodeJob& j) {
     download(j.raw_scores, o.raw_scores, BTK, st);
     download(j.from_logprob, o.from_logprob, BTK, st);
     download(j.row_lse, row_lse, BTK, st);
+    if (P > 0) {
+        download(j.pool_parents, pool.parents, BTP, st);
+        download(j.pool_tokens, pool.tokens, BTP, st);
+        download(j.pool_lengths, pool.lengths, BTP, st);
+        download(j.pool_scores, pool.scores, BTP, st);
+        download(j.pool_raw, pool.raw_scores, BTP, st);
+        download(j.pool_from_logprob, pool.from_logprob, BTP, st);
+    }
     hip_check(hipStreamSynchronize(st), "HIP decode");
     // the overlapped select pass gave up waiting for rows of the row pass
     // (bounded at 2 s; only when something starves or serialises the
@@ -385,7 +415,6 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
         example_error(0, "repetition_penalty must be finite and positive (1 disables it)");
     // What the GPU engine does not serve.
     need(!(cons && cons->token_filter), "token_filter callbacks are not served by libdbs_hip (the HIP engine)");
-    need(!pool, "relaxed-pool outputs are not served by libdbs_hip (the HIP engine)");
 
     DecodeJob j;
     j.inputs = inputs;
@@ -411,6 +440,15 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
     j.raw_scores = out->raw_scores;
     j.from_logprob = out->from_logprob;
     j.row_lse = ex ? ex->row_lse : nullptr;
+    if (pool) {
+        j.pool_mult = h->pool_multiplier;
+        j.pool_parents = ex->pool_parents;
+        j.pool_tokens = ex->pool_tokens;
+        j.pool_lengths = ex->pool_lengths;
+        j.pool_scores = ex->pool_scores;
+        j.pool_raw = ex->pool_raw_scores;
+        j.pool_from_logprob = ex->pool_from_logprob;
+    }
     run_decode(h, j);
     const int64_t selected = static_cast<int64_t>(B) * static_cast<int64_t>(trace);
     {

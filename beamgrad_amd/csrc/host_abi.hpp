@@ -28,7 +28,8 @@ namespace dbs_host {
 enum Slot : int {
     kInputs, kBanned, kBannedPe, kSteps, kBeams, kEos, kMinLengths, kFinalScores, kFinalRaw, kFinalLengths, kTokens,
     kParents, kLengths, kScores, kRawScores, kFromLogprob, kRowLse, kFirstInvalid, kWorkspace, kGradFinal,
-    kGradFinalRaw, kGradScores, kGradRaw, kDraws, kDense, kState, kForced, kSlotCount
+    kGradFinalRaw, kGradScores, kGradRaw, kDraws, kDense, kState, kForced, kPoolParents, kPoolTokens,
+    kPoolLengths, kPoolScores, kPoolRaw, kPoolFromLogprob, kSlotCount
 };
 
 struct Arena {
@@ -200,8 +201,20 @@ struct DecodeJob {
     float* raw_scores = nullptr;
     uint8_t* from_logprob = nullptr;
     float* row_lse = nullptr;
+    // the relaxed pool ([B, T, pool_mult * K]; pool_mult 0: none)
+    int pool_mult = 0;
+    int32_t* pool_parents = nullptr;
+    int32_t* pool_tokens = nullptr;
+    int32_t* pool_lengths = nullptr;
+    float* pool_scores = nullptr;
+    float* pool_raw = nullptr;
+    uint8_t* pool_from_logprob = nullptr;
 };
 void run_decode(DBSDecoderHandle* h, const DecodeJob& job);
+
+// The relaxed pool's size for beam K and multiplier m (reference
+// src/decoder.cpp:410-416), refused past what the HIP engine keeps per step.
+int pool_size_of(int K, int m);
 
 // Gradients of a trace's outputs; any may be null.
 struct Grads {

@@ -13,6 +13,25 @@
 
 namespace dbs_hip {
 
+// Relaxed-pool outputs of a decode or step (reference src/decoder.cpp:
+// 294-306): with mult m >= 1 each step keeps the best m * beams candidates of
+// an example, the selection first; device arrays [B, T, m * K] (any may be
+// null), dead entries past the kept ones and past an example's steps.
+struct PoolOutputs {
+    int mult = 0;
+    int32_t* parents = nullptr;
+    int32_t* tokens = nullptr;
+    int32_t* lengths = nullptr;
+    float* scores = nullptr;
+    float* raw_scores = nullptr;
+    uint8_t* from_logprob = nullptr;
+};
+
+// Workspace bytes of decode_for_host (step_mode 0) or step_for_host
+// (step_mode 1, prefix_stride as dbs_cuda_decode_step_workspace_size) with a
+// relaxed pool of pool_mult (0: none); -1 for invalid arguments.
+int64_t workspace_for_host(const DBSCudaDecodeArgs* args, int pool_mult, int step_mode, int prefix_stride);
+
 // dbs_hip_decode_ex3 (per-example banned masks [B, V] or null), plus
 // first_invalid (device int32 [B] or null): the first row holding NaN or
 // +inf that example b's search read, t * K + k in reading order, or -1;
@@ -24,16 +43,16 @@ namespace dbs_hip {
 int decode_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                     const DBSCudaSearchOptions* options, const uint8_t* banned_per_example,
                     const DBSCudaDecodeOutputs* outputs, float* row_lse, int32_t* first_invalid,
-                    const int32_t* forced, void* workspace, int64_t workspace_bytes, hipStream_t stream,
-                    int32_t** fault);
+                    const int32_t* forced, const PoolOutputs* pool, void* workspace, int64_t workspace_bytes,
+                    hipStream_t stream, int32_t** fault);
 
 // dbs_cuda_decode_step_ex2 with forced (device int32 [B] or null): an entry
 // >= 0 (and < V) is the one token a read beam of example b may take at this
-// step. Returns a DBS_CUDA_STATUS_*.
+// step; and a relaxed pool (null: none). Returns a DBS_CUDA_STATUS_*.
 int step_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                   const DBSCudaSearchOptions* options, const DBSCudaBeamState* state,
-                  const DBSCudaDecodeOutputs* outputs, const int32_t* forced, void* workspace,
-                  int64_t workspace_bytes, hipStream_t stream);
+                  const DBSCudaDecodeOutputs* outputs, const int32_t* forced, const PoolOutputs* pool,
+                  void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 // The per-slot path gradients draws [B, T, K] of the surrogate backward for
 // every gradient input of `in` (final scores, final raw scores, scores, raw

@@ -388,8 +388,8 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
                 h.staged_forced.assign(1, c->forced[t]);
                 forced_d = upload(&h, kForced, h.staged_forced.data(), 1, st);
             }
-            engine_check(dbs_hip::step_for_host(rows_d, DBS_CUDA_DTYPE_F32, 0, &a, &opts, &bs, &o, forced_d, ws,
-                                                ws_bytes, st),
+            engine_check(dbs_hip::step_for_host(rows_d, DBS_CUDA_DTYPE_F32, 0, &a, &opts, &bs, &o, forced_d, nullptr,
+                                                ws, ws_bytes, st),
                          "HIP decode step");
             download(out_tok.data(), o.tokens, K, st);
             download(out_par.data(), o.parents, K, st);

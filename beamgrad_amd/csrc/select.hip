@@ -48,6 +48,23 @@ __device__ __forceinline__ bool wait_step_rows(const DecodeParams& p, int b, int
     return true;
 }
 
+// Split launch of the overlapped decode: whether this launch decodes example
+// b. The early launch waits for the example's first row at most
+// p.early_ticks and then claims it; the late launch takes what the early one
+// left. One thread.
+__device__ __forceinline__ bool claim_example(const DecodeParams& p, int b) {
+    if (!p.early) return __hip_atomic_load(p.claimed + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
+    const int need = 1 + p.wait_extra;
+    const int32_t* cnt = p.step_done + static_cast<int64_t>(b) * p.T;
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+        __builtin_amdgcn_s_sleep(4);
+        if (__builtin_amdgcn_s_memrealtime() - t0 > p.early_ticks) return false;
+    }
+    __hip_atomic_store(p.claimed + b, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
 // Overlapped decode: one tagged word of the row pass (RowInfo half or
 // shortlist entry), waited for while its tag is 0; false when the wait gave
 // up (bounded like wait_step_rows).
@@ -428,7 +445,7 @@ __device__ __forceinline__ void end_round(Lds& s, State& st, int K, int sort_cap
 // threshold) falls back to offering round by round.
 template <int DT, bool LOGITS>
 __device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State& st, int b, int k, int64_t row, float lse,
-                           float praw, float inv_pen, int new_len, const PrefixView& pre, int sort_cap) {
+                           float praw, float inv_pen, int new_len, const PrefixView& pre, int sort_cap, int keep) {
     const bool mask_eos = new_len < min_length_of(p, b);
     const int V = p.V;
     const int tid = static_cast<int>(threadIdx.x);
@@ -469,7 +486,7 @@ __device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State&
         const int n = st.rcount;
         for (int r0 = 0; r0 < n; r0 += kSelectThreads) {
             if (r0 + tid < n) offer(s, st, s.rbuf[r0 + tid]);
-            end_round(s, st, p.K, sort_cap);
+            end_round(s, st, keep, sort_cap);
         }
         return;
     }
@@ -484,7 +501,7 @@ __device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State&
                 if (make_cand(p, s, pre, k, praw, inv_pen, v, new_len, lp, c)) offer(s, st, c);
             }
         }
-        end_round(s, st, p.K, sort_cap);
+        end_round(s, st, keep, sort_cap);
     }
 }
 
@@ -501,6 +518,12 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     if constexpr (HOLD) asm volatile("" ::: "a255");
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ State st;
+    if (p.claimed) {
+        __shared__ int s_claim;
+        if (threadIdx.x == 0) s_claim = claim_example(p, static_cast<int>(blockIdx.x)) ? 1 : 0;
+        __syncthreads();
+        if (s_claim == 0) return;
+    }
     const int K = p.K, T = p.T, M = p.M;
     const int SL = sl_stride(K, M);
     const int b = static_cast<int>(blockIdx.x);
@@ -545,6 +568,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
     const int Kb = beams_of(p, b), eos_b = eos_of(p, b);
     const int T_loop = p.step_mode ? 1 : T;
     const int pen_len = L.pen_len;
+    // candidates the collector keeps (the beams, or the relaxed pool), and
+    // how many of them are the example's
+    const int KP = p.pool_mult > 0 ? K * p.pool_mult : K;
+    const int Nb = p.pool_mult > 0 ? Kb * p.pool_mult : Kb;
     for (int l = tid; l < pen_len; l += kSelectThreads) {
         const float pl = length_penalty(l, p.alpha);
         s.pen[l] = pl;
@@ -596,6 +623,15 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             if (tid + u * kSelectThreads < n4) pf_sl[u] = src4[tid + u * kSelectThreads];
     };
 
+    // Pool entry i of the step starting at pool0 (reference src/decoder.cpp:294-306).
+    auto put_pool = [&](int64_t i, const Cand& c) {
+        if (p.pool_parents) p.pool_parents[i] = c.parent;
+        if (p.pool_tokens) p.pool_tokens[i] = c.token;
+        if (p.pool_lengths) p.pool_lengths[i] = c.length;
+        if (p.pool_scores) p.pool_scores[i] = c.score;
+        if (p.pool_raw) p.pool_raw[i] = c.raw;
+        if (p.pool_flp) p.pool_flp[i] = static_cast<uint8_t>(c.flp);
+    };
     // A padding step (reference src/c_api.cpp:764-781): no token, no parent.
     auto pad_step = [&](int64_t trace0) {
         for (int k = tid; k < K; k += kSelectThreads) {
@@ -605,6 +641,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
             if (p.scores) p.scores[trace0 + k] = -kInf;
             if (p.raw_scores) p.raw_scores[trace0 + k] = -kInf;
             if (p.from_logprob) p.from_logprob[trace0 + k] = 0;
+        }
+        if (p.pool_mult > 0) {
+            const int64_t pool0 = trace0 / K * KP;
+            for (int q = tid; q < KP; q += kSelectThreads) put_pool(pool0 + q, dead_cand());
         }
     };
 
@@ -883,7 +923,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
         }
         // (at most K offers: the first round of shortlisted offers joins them
         // unless the one-pass path below needs the count)
-        if (M > 0 && p.use_tau && K >= kWideBeam && forced < 0) end_round(s, st, K, L.sort_cap);
+        if (M > 0 && p.use_tau && K >= kWideBeam && forced < 0) end_round(s, st, KP, L.sort_cap);
 
         // Shortlisted candidates. Unconstrained wide beams: few reach tau, and
         // when they fit the collector beside what it holds, they are offered
@@ -959,10 +999,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                         }
                     }
                 }
-                end_round(s, st, K, L.sort_cap);
+                end_round(s, st, KP, L.sort_cap);
             }
         }
-        compact(s, st, K);
+        compact(s, st, KP);
 
         // Exactness: every candidate left out of a row's shortlist has raw <=
         // fl(p + bound); a row passes when the K-th selected candidate ranks
@@ -975,7 +1015,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 const float X = s.raw[k] + s.rbound[k];
                 if (X > -kInf) {
                     const float SX = X * inv_of(s, pen_len, s.len[k] + 1, p.alpha);
-                    const Cand kth = st.count >= Kb ? s.buf[Kb - 1] : dead_cand();
+                    const Cand kth = st.count >= Nb ? s.buf[Nb - 1] : dead_cand();
                     fail = !((kth.score > SX) || (kth.score == SX && kth.raw > X));
                 }
             }
@@ -998,9 +1038,9 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 const int64_t row = p.step_mode ? static_cast<int64_t>(b) * K + k : trace0 + k;
                 const PrefixView pre = prefix_of(p, s, b, k, cur);
                 rescan_row<DT, LOGITS>(p, s, st, b, k, row, LOGITS ? s.nraw[k] : 0.0f, praw,
-                                       inv_of(s, pen_len, new_len, p.alpha), new_len, pre, L.sort_cap);
+                                       inv_of(s, pen_len, new_len, p.alpha), new_len, pre, L.sort_cap, KP);
             }
-            compact(s, st, K);
+            compact(s, st, KP);
         }
 
         // Selection (reference src/decoder.cpp:314-350): the example's best Kb.
@@ -1023,6 +1063,12 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 s.plen[nxt * K + k] =
                     c.parent >= 0 ? s.plen[cur * K + c.parent] + ((c.flp && c.token >= 0) ? 1 : 0) : 0;
             }
+        }
+        if (p.pool_mult > 0) {
+            // the pool: the example's best Nb, the selection first
+            const int npool = st.count < Nb ? st.count : Nb;
+            const int64_t pool0 = trace0 / K * KP;
+            for (int q = tid; q < KP; q += kSelectThreads) put_pool(pool0 + q, q < npool ? s.buf[q] : dead_cand());
         }
         lds_barrier();
         if (p.constrained && !p.step_mode) {
@@ -1231,6 +1277,11 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
     const int b = static_cast<int>(blockIdx.x) * (static_cast<int>(blockDim.x) >> 6) + wave;
     const int lane = static_cast<int>(threadIdx.x) & 63;
     if (b >= p.B) return;
+    if (p.claimed) {
+        int mine = 1;
+        if (lane == 0) mine = claim_example(p, b) ? 1 : 0;
+        if (__builtin_amdgcn_readfirstlane(mine) == 0) return;
+    }
     unsigned char* smem = smem_all + static_cast<size_t>(wave) * wave_bytes;
     uint4* s_key = reinterpret_cast<uint4*>(smem);                   // [64] rank keys
     ShortEntry* s_sl = reinterpret_cast<ShortEntry*>(smem + 1024);  // [K * M], beam k's list at k * M
@@ -2031,7 +2082,7 @@ std::atomic<int> g_select_kind{0};
 
 bool select_narrow(const DecodeParams& p) {
     if (g_select_kind.load(std::memory_order_relaxed) == 1) return false;
-    if (p.step_mode || p.forced || p.M <= 0 || p.K > kNarrowMaxK || p.V > (1 << 24)) return false;
+    if (p.step_mode || p.forced || p.pool_mult > 0 || p.M <= 0 || p.K > kNarrowMaxK || p.V > (1 << 24)) return false;
     // constrained: n-gram blocking of n >= 2 and/or a repetition penalty
     // (n = 1 blocking would drop most of a long prefix's shortlist entries)
     if (p.constrained) return p.ngram != 1 && narrow_sig_words(p) > 0;
@@ -2042,11 +2093,11 @@ int select_reserve_cus(const DecodeParams& p) {
     return select_narrow(p) ? narrow_groups(p.B) : p.B;
 }
 
-SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool step_mode, int prefix_cap) {
+SelectLayout select_layout(int B, int T, int K, int M, bool constrained, bool step_mode, int prefix_cap, int keep) {
     (void)B;
     SelectLayout L{};
     int sc = 1;
-    while (sc < K + 2 * kSelectThreads) sc <<= 1;
+    while (sc < (keep > K ? keep : K) + 2 * kSelectThreads) sc <<= 1;
     L.sort_cap = sc;
     L.pen_len = step_mode ? 0 : T + 2;
     auto align = [](size_t x) { return (x + 15) & ~static_cast<size_t>(15); };

@@ -22,10 +22,11 @@
  *
  * All 81 functions of the reference's ABI are exported. What the GPU engine
  * does not serve is refused with DBS_ERROR_INVALID_ARGUMENT and a message
- * naming it: the relaxed pool (relaxed_pool_multiplier > 0 and the pool
- * outputs and gradients) and token-filter callbacks. Result handles
- * therefore have no pool (dbs_result_pool_size 0, pool accessors NULL).
- * Forced tokens (an entry >= 0: the one token a read beam may take at that
+ * naming it: the relaxed pool of result handles and its gradients
+ * (relaxed_pool_multiplier > 0 with the result-handle decodes, pool
+ * gradients), pools of more than 1024 candidates, and token-filter
+ * callbacks. The pool outputs of the batch decodes into caller arrays are
+ * served. Forced tokens (an entry >= 0: the one token a read beam may take at that
  * step) are served by every decode that takes them: the batch decodes into
  * caller arrays, the result-handle decodes and the model-step decodes.
  */
@@ -62,7 +63,7 @@ typedef struct DBSOptionsC {
     int eos_token;                       /* -1: no EOS handling */
     float selected_temperature;          /* softmax temperature of the selected-beam weights [1.0] */
     float soft_topk_temperature;         /* [0.25] (relaxed pool: not served) */
-    int relaxed_pool_multiplier;         /* [0] (relaxed pool: not served) */
+    int relaxed_pool_multiplier;         /* [0] m: pool of m * K candidates a step (<= 1024) */
     int vocab_block;                     /* ignored */
     float length_penalty_alpha;          /* GNMT ((5 + len) / 6)^alpha; 0 disables [0] */
     float soft_topk_tolerance;           /* [1e-4] (relaxed pool: not served) */
@@ -235,9 +236,12 @@ DBS_EXPORT int dbs_backward_batch_into(
     int num_threads,
     float* grad_log_probs);
 
-/* Extended outputs (reference include/dbs.h:335-349). The pool arrays must be
- * NULL here (the relaxed pool is not served); row_lse gets, with from_logits,
- * the logsumexp of each row the search read and 0 elsewhere. */
+/* Extended outputs (reference include/dbs.h:335-349). The pool arrays
+ * [B, T, relaxed_pool_multiplier * K] (any may be NULL; one asked for needs a
+ * relaxed_pool_multiplier >= 1) get each step's best m * K candidates, the
+ * selection first, dead entries (parent and token -1, length 0, -inf scores)
+ * past the candidates and past an example's steps; row_lse gets, with
+ * from_logits, the logsumexp of each row the search read and 0 elsewhere. */
 typedef struct DBSDecodeOutputsExC {
     DBSDecodeOutputsC base;
     int32_t* pool_parents;

@@ -131,10 +131,11 @@ class HostLib:
         return c
 
     def decode(self, h, x: np.ndarray, K: int, *, dtype="f32", from_logits=False, steps=None, constraints=None,
-               ex=True, row_lse=True, fill=None) -> tuple[int, dict]:
+               ex=True, row_lse=True, fill=None, pool=0) -> tuple[int, dict]:
         """dbs_decode_batch_into_ex (or, ex=False, dbs_decode_batch_into for
-        f32 log-probs). Outputs are pre-filled with `fill` patterns so every
-        written element is checked. Returns (status, outputs)."""
+        f32 log-probs); pool > 0 asks for the relaxed pool's [B, T, pool]
+        outputs. Outputs are pre-filled with random bytes so every written
+        element is checked. Returns (status, outputs)."""
         x = np.ascontiguousarray(x)
         B, T, KK, V = x.shape
         assert KK == K
@@ -152,6 +153,12 @@ class HostLib:
                "from_logprob": buf((B, T, K), np.uint8)}
         if ex and row_lse:
             out["row_lse"] = buf((B, T, K), np.float32)
+        pool_keys = (("pool_parents", np.int32, C.c_int32), ("pool_tokens", np.int32, C.c_int32),
+                     ("pool_lengths", np.int32, C.c_int32), ("pool_scores", np.float32, C.c_float),
+                     ("pool_raw_scores", np.float32, C.c_float), ("pool_from_logprob", np.uint8, C.c_uint8))
+        if ex and pool:
+            for name, dt, _ in pool_keys:
+                out[name] = buf((B, T, pool), dt)
         base = OutputsC(*(_p(out[n], ct) for n, ct in (
             ("final_scores", C.c_float), ("final_raw_scores", C.c_float), ("final_lengths", C.c_int32),
             ("tokens", C.c_int32), ("parents", C.c_int32), ("lengths", C.c_int32), ("scores", C.c_float),
@@ -163,6 +170,9 @@ class HostLib:
             o.base = base
             if row_lse:
                 o.row_lse = _p(out["row_lse"], C.c_float)
+            if pool:
+                for name, _, ct in pool_keys:
+                    setattr(o, name, _p(out[name], ct))
             status = self.lib.dbs_decode_batch_into_ex(h, x.ctypes.data_as(C.c_void_p), DTYPES[dtype],
                                                        int(bool(from_logits)), B, T, V, _p(steps_a, C.c_int32), cons,
                                                        0, C.byref(o))

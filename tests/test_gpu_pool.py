@@ -1,0 +1,140 @@
+# SPDX-License-Identifier: MIT
+"""The relaxed pool (relaxed_pool_multiplier m >= 1) in libdbs_hip.so,
+computed on the GPU, against the reference's own CPU library
+(oracle/_ref/libdbs_ref.so) called with identical arguments.
+
+With a pool each step keeps the best m * K candidates of an example, the
+selection first (reference src/decoder.cpp:40, 294-350). The batch decodes
+into caller arrays write them to the pool outputs of DBSDecodeOutputsExC
+([B, T, m * K]; dead entries past the candidates and past an example's
+steps); asking for no pool output decodes without one. Cases: random decodes
+(f32/f16/bf16, logits, EOS and extra EOS, min_length, banned tokens, n-gram
+blocking, repetition penalty, per-example steps, forced tokens), pools wider
+than a row's shortlist (every row rescanned), wide beams, the overlapped
+decode. Outputs are compared bit for bit, statuses and messages as text."""
+
+import os
+
+import numpy as np
+import pytest
+
+from beamgrad_amd import _build
+from tests.cases import first_difference, log_softmax, make_case, to_bits
+from tests.host_abi import HostLib, enable_results
+
+pytestmark = pytest.mark.gpu
+
+REF_LIB = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "_ref",
+                       "libdbs_ref.so")
+OUT_KEYS = ("final_scores", "final_raw_scores", "final_lengths", "tokens", "parents", "lengths", "scores",
+            "raw_scores", "from_logprob", "row_lse")
+POOL_KEYS = ("pool_parents", "pool_tokens", "pool_lengths", "pool_scores", "pool_raw_scores", "pool_from_logprob")
+
+
+@pytest.fixture(scope="module")
+def libs():
+    import torch
+
+    assert torch.cuda.is_available()
+    if not os.path.exists(REF_LIB):
+        pytest.skip("oracle/_ref is not built")
+    return enable_results(HostLib(_build.lib_path())), enable_results(HostLib(REF_LIB))
+
+
+def _each(libs, opts, fn, extra_eos=None):
+    out = []
+    for lib in libs:
+        h = lib.create(**opts)
+        try:
+            if extra_eos:
+                assert lib.set_extra_eos(h, extra_eos) == 0, lib.error()
+            out.append(fn(lib, h))
+        finally:
+            lib.destroy(h)
+    return out
+
+
+def _pool_decode(libs, case, m, *, forced=None, pool=True):
+    kw = case["kw"]
+    K = case["K"]
+    opts = dict(beam_size=K, eos_token=kw["eos_token"], length_penalty_alpha=kw["alpha"],
+                min_length=kw["min_length"], relaxed_pool_multiplier=m)
+    constrained = forced is not None or kw.get("banned") is not None or kw.get("no_repeat_ngram_size") or \
+        kw.get("repetition_penalty", 1.0) > 1.0
+
+    def fn(lib, h):
+        keep = {}
+        cons = None
+        if constrained:
+            cons = HostLib.constraints(banned=kw.get("banned"), repetition_penalty=float(kw.get("repetition_penalty", 1.0)),
+                                       no_repeat_ngram_size=int(kw.get("no_repeat_ngram_size") or 0), forced=forced,
+                                       keep=keep)
+        st, out = lib.decode(h, case["xin"], K, dtype=case["dtype"], from_logits=kw["from_logits"], steps=kw["steps"],
+                             constraints=cons, pool=K * m if pool else 0)
+        return st, out, lib.error()
+
+    return _each(libs, opts, fn, kw.get("extra_eos"))
+
+
+def _check(libs, case, m, **more):
+    (s0, o0, e0), (s1, o1, e1) = _pool_decode(libs, case, m, **more)
+    tag = f"seed {case['seed']} {case['dtype']} B{case['B']} T{case['T']} K{case['K']} V{case['V']} m{m}"
+    assert (s0, e0) == (s1, e1), tag
+    assert s0 == 0, (tag, e0)
+    keys = OUT_KEYS + (POOL_KEYS if more.get("pool", True) else ())
+    diff = first_difference(o0, o1, keys)
+    assert diff is None, f"{tag}: {diff}"
+    return o0
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_pool_batch_decodes_match_the_reference(libs, seed):
+    case = make_case(41000 + seed, allow_invalid=False)
+    case["kw"]["banned_per_example"] = None
+    m = [1, 2, 3, 4, 8][seed % 5]
+    if case["K"] * m > 1024:
+        m = 1
+    _check(libs, case, m)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_pool_with_forced_tokens(libs, seed):
+    case = make_case(42000 + seed, allow_invalid=False)
+    case["kw"]["banned_per_example"] = None
+    rng = np.random.default_rng(seed)
+    T, V = case["T"], case["V"]
+    forced = np.where(rng.random(T) < 0.5, rng.integers(0, V, T), -1).astype(np.int32)
+    _check(libs, case, 2, forced=forced)
+
+
+@pytest.mark.parametrize("overlap", [1, 0])
+@pytest.mark.parametrize("shape", [(4, 1000, 4), (16, 4104, 2), (8, 32000, 3), (20, 3000, 2), (64, 2048, 16),
+                                   (5, 257, 13)])
+def test_pool_wide_and_long_rows(libs, shape, overlap):
+    """Pools from 8 to 1024 candidates: within a row's shortlist, and wider
+    (every row read in full), with the select pass beside the row pass and
+    after it."""
+    K, V, m = shape
+    rng = np.random.default_rng(K * 7 + m)
+    B, T = 3, 6
+    x = rng.normal(0.0, 2.0, size=(B, T, K, V)).astype(np.float32)
+    if m % 2:
+        x = log_softmax(x)
+    dtype = "bf16" if K >= 16 else "f32"
+    kw = dict(from_logits=m % 2 == 0, eos_token=int(rng.integers(0, V)), extra_eos=[], min_length=1, alpha=0.6,
+              no_repeat_ngram_size=0, repetition_penalty=1.0, steps=[6, 3, 5], banned=None, banned_per_example=None)
+    case = dict(seed=K, B=B, T=T, K=K, V=V, dtype=dtype, x=x, xin=to_bits(x, dtype), kw=kw)
+    ours = libs[0].lib
+    prev = ours.dbs_hip_set_decode_overlap(overlap)
+    try:
+        _check(libs, case, m)
+    finally:
+        ours.dbs_hip_set_decode_overlap(prev)
+
+
+def test_pool_multiplier_without_pool_outputs(libs):
+    """A multiplier with no pool output asked for: the plain decode."""
+    case = make_case(43000, allow_invalid=False)
+    case["kw"]["banned_per_example"] = None
+    _check(libs, case, 3, pool=False)
+

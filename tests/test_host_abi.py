@@ -306,8 +306,8 @@ def test_backward_argument_errors_match(ours, ref):
 
 
 def test_features_the_engine_does_not_serve_are_refused(ours):
-    """Token filters, the relaxed pool and beams beyond the device ABI's
-    limit are refused with INVALID_ARGUMENT before any device work (the
+    """Token filters, relaxed pools and beams beyond the device ABI's limits
+    are refused with INVALID_ARGUMENT before any device work (the
     reference's CPU library serves them)."""
     import ctypes as C
 
@@ -319,14 +319,12 @@ def test_features_the_engine_does_not_serve_are_refused(ours):
         cons.token_filter = C.c_void_p(1)
         st, _ = ours.decode(h, x, 2, constraints=cons)
         assert st == -1 and "token_filter" in ours.error()
-        o = OutputsExC()
-        fs = np.zeros((1, 2), np.float32)
-        pool = np.zeros(8, np.int32)
-        o.base.final_scores = fs.ctypes.data_as(C.POINTER(C.c_float))
-        o.pool_parents = pool.ctypes.data_as(C.POINTER(C.c_int32))
-        st = ours.lib.dbs_decode_batch_into_ex(h, x.ctypes.data_as(C.c_void_p), 0, 0, 1, 2, 5, None, None, 0,
-                                               C.byref(o))
-        assert st == -1 and "relaxed-pool" in ours.error()
+    finally:
+        ours.destroy(h)
+    h = ours.create(beam_size=300, relaxed_pool_multiplier=4)
+    try:
+        st, _ = ours.decode(h, np.zeros((1, 1, 300, 3), np.float32), 300, pool=1200)
+        assert st == -1 and "relaxed pool of 1200 candidates" in ours.error()
     finally:
         ours.destroy(h)
     h = ours.create(beam_size=1025)
