@@ -36,6 +36,13 @@ struct DBSResultHandle {
     std::vector<float> raw_scores, scores, weights;  // [T * K]
     std::vector<uint8_t> from_logprob;               // [T * K]
     std::vector<float> final_raw_scores, final_scores;  // [K]
+    // the relaxed pool: P candidates a step (0: none), with their soft top-K
+    // inclusion weights
+    int pool_size = 0;
+    float soft_topk_temperature = 0.25f;
+    std::vector<int32_t> pool_parents, pool_tokens, pool_lengths;      // [T * P]
+    std::vector<float> pool_raw_scores, pool_scores, relaxed_weights;  // [T * P]
+    std::vector<uint8_t> pool_from_logprob;                            // [T * P]
 };
 
 struct DBSBatchResultHandle {
@@ -92,6 +99,90 @@ void softmax_selected(const float* scores, float* out, int n, float temperature)
     for (int i = 0; i < n; ++i) out[i] *= inv_sum;
 }
 
+// The soft top-k inclusion weights of one step's pool (reference
+// src/kernels_scalar.cpp:28-45, 298-364): sigmoid((s - theta) / temperature)
+// for every live candidate, theta bisected (as an offset from the best
+// score) until the weights sum to k within the tolerance, or theta is
+// bracketed to tolerance * temperature or to a few ulps; the reference's
+// operations in its order, with its exp, so the weights are its bits.
+constexpr float kPoolGuard = -1.0e30f;  // scores at or below it are dead entries
+
+float det_sigmoid(float x) {
+    if (x >= 0.0f) return 1.0f / (1.0f + dbs_hip::exp_nonpositive(-x));
+    const float e = dbs_hip::exp_nonpositive(x);
+    return e / (1.0f + e);
+}
+
+float inclusion_sum(const float* s, int n, float ref, float offset, float temperature) {
+    float sum = 0.0f;
+    for (int i = 0; i < n; ++i)
+        if (s[i] > kPoolGuard) sum += det_sigmoid(((s[i] - ref) - offset) / temperature);
+    return sum;
+}
+
+void soft_topk_weights(const float* s, float* w, int n, int k, float temperature, float tolerance, int max_iters) {
+    std::fill(w, w + n, 0.0f);
+    int live = 0;
+    float lo_s = std::numeric_limits<float>::infinity(), hi_s = -std::numeric_limits<float>::infinity();
+    for (int i = 0; i < n; ++i) {
+        if (!(s[i] > kPoolGuard)) continue;
+        ++live;
+        lo_s = std::min(lo_s, s[i]);
+        hi_s = std::max(hi_s, s[i]);
+    }
+    if (live == 0 || k <= 0) return;
+    if (k >= live) {
+        for (int i = 0; i < n; ++i) w[i] = s[i] > kPoolGuard ? 1.0f : 0.0f;
+        return;
+    }
+    const float ref = hi_s;
+    float lo = (lo_s - ref) - 80.0f * temperature;
+    float hi = 80.0f * temperature;
+    const float bracket = tolerance * temperature;
+    for (int it = 0; it < max_iters; ++it) {
+        const float mid = 0.5f * (lo + hi);
+        const float err = inclusion_sum(s, n, ref, mid, temperature) - static_cast<float>(k);
+        const float ulps = 4.0f * std::numeric_limits<float>::epsilon() * std::fabs(mid);
+        if (std::fabs(err) <= tolerance || hi - lo <= std::max(bracket, ulps)) {
+            lo = hi = mid;
+            break;
+        }
+        (err > 0.0f ? lo : hi) = mid;
+    }
+    const float offset = 0.5f * (lo + hi);
+    for (int i = 0; i < n; ++i) w[i] = s[i] > kPoolGuard ? det_sigmoid(((s[i] - ref) - offset) / temperature) : 0.0f;
+}
+
+// A step's pool from the device (P entries of a [.., Pmax] row) into the
+// result at step t, with its inclusion weights over the result's K beams.
+void put_pool_step(DBSResultHandle& r, const DBSDecoderHandle& h, int t, const int32_t* par, const int32_t* tok,
+                   const int32_t* len, const float* sc, const float* raw, const uint8_t* flp) {
+    const int P = r.pool_size;
+    const size_t dst = static_cast<size_t>(t) * P;
+    std::copy_n(par, P, r.pool_parents.begin() + dst);
+    std::copy_n(tok, P, r.pool_tokens.begin() + dst);
+    std::copy_n(len, P, r.pool_lengths.begin() + dst);
+    std::copy_n(sc, P, r.pool_scores.begin() + dst);
+    std::copy_n(raw, P, r.pool_raw_scores.begin() + dst);
+    std::copy_n(flp, P, r.pool_from_logprob.begin() + dst);
+    soft_topk_weights(r.pool_scores.data() + dst, r.relaxed_weights.data() + dst, P, r.beam_size,
+                      h.soft_topk_temperature, h.soft_topk_tolerance, h.soft_topk_max_iters);
+}
+
+// A result's pool arrays for `steps` steps of P candidates.
+void size_pool(DBSResultHandle& r, const DBSDecoderHandle& h, int steps, int P) {
+    r.pool_size = P;
+    r.soft_topk_temperature = h.soft_topk_temperature;
+    const size_t n = static_cast<size_t>(steps) * static_cast<size_t>(P);
+    r.pool_parents.assign(n, -1);
+    r.pool_tokens.assign(n, -1);
+    r.pool_lengths.assign(n, 0);
+    r.pool_scores.assign(n, kNegInf);
+    r.pool_raw_scores.assign(n, kNegInf);
+    r.relaxed_weights.assign(n, 0.0f);
+    r.pool_from_logprob.assign(n, 0);
+}
+
 DBSDecoderHandle& handle_of(DBSDecoderHandle* h) {
     need(h != nullptr, "decoder handle cannot be null");
     return *h;
@@ -142,17 +233,25 @@ void check_decode_args(const DBSDecoderHandle& h, int K, int eos, int steps, int
 
 // What the HIP engine does not serve, after the reference's own checks.
 void check_served(const DBSDecoderHandle& h, const Constraints* c) {
-    need(h.pool_multiplier <= 0, "relaxed-pool outputs are not served by libdbs_hip (the HIP engine)");
+    (void)h;
     if (c) need(!c->filter, "token_filter callbacks are not served by libdbs_hip (the HIP engine)");
 }
 
+// Host copies of a decode's relaxed pool [B, T, mult * Kmax].
+struct PoolHost {
+    int mult = 0;
+    std::vector<int32_t> parents, tokens, lengths;
+    std::vector<float> scores, raw;
+    std::vector<uint8_t> flp;
+};
+
 // Result b of a [B, T, Kmax] trace: its first `steps` steps and `beams`
-// slots, with the selected-beam weights of each step.
+// slots, with the selected-beam weights of each step (and its pool).
 void fill_result(DBSResultHandle& r, const DBSDecoderHandle& h, int steps, int beams, int V, int T, int Kmax, int b,
                  const std::vector<int32_t>& parents, const std::vector<int32_t>& tokens,
                  const std::vector<int32_t>& lengths, const std::vector<float>& raw, const std::vector<float>& scores,
                  const std::vector<uint8_t>& flp, const std::vector<float>& final_raw,
-                 const std::vector<float>& final_scores) {
+                 const std::vector<float>& final_scores, const PoolHost* pool) {
     r.steps = steps;
     r.beam_size = beams;
     r.vocab_size = V;
@@ -176,14 +275,27 @@ void fill_result(DBSResultHandle& r, const DBSDecoderHandle& h, int steps, int b
         std::copy_n(flp.begin() + src, beams, r.from_logprob.begin() + dst);
         softmax_selected(r.scores.data() + dst, r.weights.data() + dst, beams, h.selected_temperature);
     }
+    if (pool) {
+        // the example's pool: the first beams * m of each step's row
+        size_pool(r, h, steps, beams * pool->mult);
+        const size_t Pmax = static_cast<size_t>(Kmax) * pool->mult;
+        for (int t = 0; t < steps; ++t) {
+            const size_t src = (static_cast<size_t>(b) * T + t) * Pmax;
+            put_pool_step(r, h, t, pool->parents.data() + src, pool->tokens.data() + src, pool->lengths.data() + src,
+                          pool->scores.data() + src, pool->raw.data() + src, pool->flp.data() + src);
+        }
+    }
     const size_t fsrc = static_cast<size_t>(b) * Kmax;
     r.final_raw_scores.assign(final_raw.begin() + fsrc, final_raw.begin() + fsrc + beams);
     r.final_scores.assign(final_scores.begin() + fsrc, final_scores.begin() + fsrc + beams);
 }
 
+// The bytes of a result's trace and pool arrays (reference src/c_api.cpp:
+// 124-129 counts these).
 int64_t result_bytes(const DBSResultHandle& r) {
     return static_cast<int64_t>(r.parents.size() * 3 * sizeof(int32_t) + r.raw_scores.size() * 3 * sizeof(float) +
-                                r.from_logprob.size() + r.final_scores.size() * 2 * sizeof(float));
+                                r.pool_parents.size() * 3 * sizeof(int32_t) +
+                                r.pool_scores.size() * 3 * sizeof(float));
 }
 
 // One decode of B examples [B, T, K, V] of log-probabilities into results:
@@ -235,11 +347,30 @@ std::vector<DBSResultHandle> decode_results(DBSDecoderHandle& h, const BatchSpec
     j.scores = scores.data();
     j.raw_scores = raw.data();
     j.from_logprob = flp.data();
+    PoolHost pool;
+    if (h.pool_multiplier > 0) {
+        const size_t BTP = BTK * static_cast<size_t>(pool_size_of(s.K, h.pool_multiplier) / s.K);
+        pool.mult = h.pool_multiplier;
+        pool.parents.resize(BTP);
+        pool.tokens.resize(BTP);
+        pool.lengths.resize(BTP);
+        pool.scores.resize(BTP);
+        pool.raw.resize(BTP);
+        pool.flp.resize(BTP);
+        j.pool_mult = pool.mult;
+        j.pool_parents = pool.parents.data();
+        j.pool_tokens = pool.tokens.data();
+        j.pool_lengths = pool.lengths.data();
+        j.pool_scores = pool.scores.data();
+        j.pool_raw = pool.raw.data();
+        j.pool_from_logprob = pool.flp.data();
+    }
     run_decode(&h, j);
     std::vector<DBSResultHandle> out(static_cast<size_t>(s.B));
     for (int b = 0; b < s.B; ++b) {
         fill_result(out[static_cast<size_t>(b)], h, s.steps ? s.steps[b] : s.T, s.beams ? s.beams[b] : s.K, s.V, s.T,
-                    s.K, b, parents, tokens, lengths, raw, scores, flp, final_raw, final_scores);
+                    s.K, b, parents, tokens, lengths, raw, scores, flp, final_raw, final_scores,
+                    pool.mult > 0 ? &pool : nullptr);
     }
     return out;
 }
@@ -247,7 +378,8 @@ std::vector<DBSResultHandle> decode_results(DBSDecoderHandle& h, const BatchSpec
 void record_result_stats(DBSDecoderHandle& h, const DBSResultHandle& r, int64_t ns, bool model_step,
                          int64_t extra_bytes = 0) {
     const int64_t selected = static_cast<int64_t>(r.steps) * r.beam_size;
-    stats_decode(&h, ns, selected, 0, selected * r.vocab_size, result_bytes(r) + extra_bytes, model_step);
+    stats_decode(&h, ns, selected, static_cast<int64_t>(r.steps) * r.pool_size, selected * r.vocab_size,
+                 result_bytes(r) + extra_bytes, model_step);
 }
 
 // ---------------------------------------------------------------------------
@@ -325,7 +457,14 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
     DBSCudaSearchOptions opts{};
     opts.extra_eos_count = static_cast<int>(h.extra_eos.size());
     for (size_t i = 0; i < h.extra_eos.size(); ++i) opts.extra_eos_tokens[i] = h.extra_eos[i];
-    const int64_t ws_bytes = dbs_cuda_decode_step_workspace_size(&a, steps);
+    // the relaxed pool of each step (reference src/decoder.cpp:849)
+    const int P = pool_size_of(K, h.pool_multiplier);
+    if (P > 0) size_pool(r, h, steps, P);
+    std::vector<int32_t> pool_par(static_cast<size_t>(P)), pool_tok(static_cast<size_t>(P)),
+        pool_len(static_cast<size_t>(P));
+    std::vector<float> pool_sc(static_cast<size_t>(P)), pool_raw(static_cast<size_t>(P));
+    std::vector<uint8_t> pool_flp(static_cast<size_t>(P));
+    const int64_t ws_bytes = dbs_hip::workspace_for_host(&a, P > 0 ? h.pool_multiplier : 0, 1, steps);
     need(ws_bytes > 0, "invalid decode arguments");
 
     for (int t = 0; t < steps; ++t) {
@@ -388,9 +527,27 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
                 h.staged_forced.assign(1, c->forced[t]);
                 forced_d = upload(&h, kForced, h.staged_forced.data(), 1, st);
             }
-            engine_check(dbs_hip::step_for_host(rows_d, DBS_CUDA_DTYPE_F32, 0, &a, &opts, &bs, &o, forced_d, nullptr,
-                                                ws, ws_bytes, st),
+            dbs_hip::PoolOutputs pool;
+            if (P > 0) {
+                pool.mult = h.pool_multiplier;
+                pool.parents = static_cast<int32_t*>(h.arena.get(kPoolParents, 4 * static_cast<size_t>(P)));
+                pool.tokens = static_cast<int32_t*>(h.arena.get(kPoolTokens, 4 * static_cast<size_t>(P)));
+                pool.lengths = static_cast<int32_t*>(h.arena.get(kPoolLengths, 4 * static_cast<size_t>(P)));
+                pool.scores = static_cast<float*>(h.arena.get(kPoolScores, 4 * static_cast<size_t>(P)));
+                pool.raw_scores = static_cast<float*>(h.arena.get(kPoolRaw, 4 * static_cast<size_t>(P)));
+                pool.from_logprob = static_cast<uint8_t*>(h.arena.get(kPoolFromLogprob, static_cast<size_t>(P)));
+            }
+            engine_check(dbs_hip::step_for_host(rows_d, DBS_CUDA_DTYPE_F32, 0, &a, &opts, &bs, &o, forced_d,
+                                                P > 0 ? &pool : nullptr, ws, ws_bytes, st),
                          "HIP decode step");
+            if (P > 0) {
+                download(pool_par.data(), pool.parents, pool_par.size(), st);
+                download(pool_tok.data(), pool.tokens, pool_tok.size(), st);
+                download(pool_len.data(), pool.lengths, pool_len.size(), st);
+                download(pool_sc.data(), pool.scores, pool_sc.size(), st);
+                download(pool_raw.data(), pool.raw_scores, pool_raw.size(), st);
+                download(pool_flp.data(), pool.from_logprob, pool_flp.size(), st);
+            }
             download(out_tok.data(), o.tokens, K, st);
             download(out_par.data(), o.parents, K, st);
             download(out_score.data(), o.scores, K, st);
@@ -444,6 +601,9 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
         }
         search_prefix.swap(next_search);
         softmax_selected(r.scores.data() + base, r.weights.data() + base, K, h.selected_temperature);
+        if (P > 0)
+            put_pool_step(r, h, t, pool_par.data(), pool_tok.data(), pool_len.data(), pool_sc.data(), pool_raw.data(),
+                          pool_flp.data());
         parents = out_par;
         tokens = out_tok;
     }
@@ -476,7 +636,9 @@ DBSBackwardHandle backward_of(DBSDecoderHandle& h, const DBSResultHandle& r, con
     const size_t dense = mul(selected, static_cast<size_t>(V), "dense gradient size overflow");
     if (!sparse && dense > static_cast<size_t>(h.max_dense_gradient_elements))
         throw std::length_error("dense gradient allocation exceeds max_dense_gradient_elements; use sparse backward");
-    need(!grw, "relaxed-pool gradients need a relaxed pool: create the decoder with relaxed_pool_multiplier >= 1");
+    need(!grw || r.pool_size > 0,
+         "relaxed-pool gradients need a relaxed pool: create the decoder with relaxed_pool_multiplier >= 1");
+    need(!grw, "relaxed-pool gradients are not served by libdbs_hip (the HIP engine)");
     std::vector<float> g_scores;
     if (gw) {
         g_scores.assign(selected, 0.0f);
@@ -876,7 +1038,7 @@ DBS_EXPORT const DBSResultHandle* dbs_batch_result_at(const DBSBatchResultHandle
 DBS_EXPORT int dbs_result_steps(const DBSResultHandle* r) { return r ? r->steps : 0; }
 DBS_EXPORT int dbs_result_beam_size(const DBSResultHandle* r) { return r ? r->beam_size : 0; }
 DBS_EXPORT int dbs_result_vocab_size(const DBSResultHandle* r) { return r ? r->vocab_size : 0; }
-DBS_EXPORT int dbs_result_pool_size(const DBSResultHandle* r) { (void)r; return 0; }
+DBS_EXPORT int dbs_result_pool_size(const DBSResultHandle* r) { return r ? r->pool_size : 0; }
 DBS_EXPORT const int32_t* dbs_result_tokens(const DBSResultHandle* r) { return r ? data_or_null(r->tokens) : nullptr; }
 DBS_EXPORT const int32_t* dbs_result_parents(const DBSResultHandle* r) {
     return r ? data_or_null(r->parents) : nullptr;
@@ -895,13 +1057,25 @@ DBS_EXPORT const float* dbs_result_final_scores(const DBSResultHandle* r) {
 DBS_EXPORT const float* dbs_result_final_raw_scores(const DBSResultHandle* r) {
     return r ? data_or_null(r->final_raw_scores) : nullptr;
 }
-// the relaxed pool is not served, so a result never has one
-DBS_EXPORT const float* dbs_result_relaxed_weights(const DBSResultHandle* r) { (void)r; return nullptr; }
-DBS_EXPORT const int32_t* dbs_result_pool_tokens(const DBSResultHandle* r) { (void)r; return nullptr; }
-DBS_EXPORT const int32_t* dbs_result_pool_parents(const DBSResultHandle* r) { (void)r; return nullptr; }
-DBS_EXPORT const int32_t* dbs_result_pool_lengths(const DBSResultHandle* r) { (void)r; return nullptr; }
-DBS_EXPORT const float* dbs_result_pool_scores(const DBSResultHandle* r) { (void)r; return nullptr; }
-DBS_EXPORT const float* dbs_result_pool_raw_scores(const DBSResultHandle* r) { (void)r; return nullptr; }
+// the relaxed pool's arrays (NULL without a pool)
+DBS_EXPORT const float* dbs_result_relaxed_weights(const DBSResultHandle* r) {
+    return r ? data_or_null(r->relaxed_weights) : nullptr;
+}
+DBS_EXPORT const int32_t* dbs_result_pool_tokens(const DBSResultHandle* r) {
+    return r ? data_or_null(r->pool_tokens) : nullptr;
+}
+DBS_EXPORT const int32_t* dbs_result_pool_parents(const DBSResultHandle* r) {
+    return r ? data_or_null(r->pool_parents) : nullptr;
+}
+DBS_EXPORT const int32_t* dbs_result_pool_lengths(const DBSResultHandle* r) {
+    return r ? data_or_null(r->pool_lengths) : nullptr;
+}
+DBS_EXPORT const float* dbs_result_pool_scores(const DBSResultHandle* r) {
+    return r ? data_or_null(r->pool_scores) : nullptr;
+}
+DBS_EXPORT const float* dbs_result_pool_raw_scores(const DBSResultHandle* r) {
+    return r ? data_or_null(r->pool_raw_scores) : nullptr;
+}
 
 DBS_EXPORT const float* dbs_backward_grad_log_probs(const DBSBackwardHandle* b) {
     return b ? data_or_null(b->grad_log_probs) : nullptr;
@@ -923,7 +1097,9 @@ DBS_EXPORT int dbs_backward_is_sparse(const DBSBackwardHandle* b) { return b && 
 DBS_EXPORT int64_t dbs_result_selected_count(const DBSResultHandle* r) {
     return r ? static_cast<int64_t>(r->steps) * r->beam_size : 0;
 }
-DBS_EXPORT int64_t dbs_result_pool_count(const DBSResultHandle* r) { (void)r; return 0; }
+DBS_EXPORT int64_t dbs_result_pool_count(const DBSResultHandle* r) {
+    return r ? static_cast<int64_t>(r->steps) * r->pool_size : 0;
+}
 DBS_EXPORT int64_t dbs_result_logprob_count(const DBSResultHandle* r) {
     return r ? static_cast<int64_t>(r->steps) * r->beam_size * r->vocab_size : 0;
 }
@@ -979,7 +1155,8 @@ DBS_EXPORT int dbs_result_summary_json(const DBSResultHandle* r, int eos_token, 
         "\"pool_count\":%lld,\"eos_token\":%d,\"eos_count\":%lld,\"min_length\":%d,\"max_length\":%d,"
         "\"min_final_score\":%.9g,\"max_final_score\":%.9g,\"deterministic_order\":%d}",
         DBS_ABI_VERSION, r->steps, r->beam_size, r->vocab_size,
-        static_cast<long long>(dbs_result_selected_count(r)), 0LL, eos_token,
+        static_cast<long long>(dbs_result_selected_count(r)), static_cast<long long>(dbs_result_pool_count(r)),
+        eos_token,
         static_cast<long long>(dbs_result_eos_count(r, eos_token)), min_len, max_len, static_cast<double>(min_final),
         static_cast<double>(max_final), dbs_result_validate_deterministic_order(r) == 0 ? 1 : 0);
     if (n < 0) {

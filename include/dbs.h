@@ -22,11 +22,11 @@
  *
  * All 81 functions of the reference's ABI are exported. What the GPU engine
  * does not serve is refused with DBS_ERROR_INVALID_ARGUMENT and a message
- * naming it: the relaxed pool of result handles and its gradients
- * (relaxed_pool_multiplier > 0 with the result-handle decodes, pool
- * gradients), pools of more than 1024 candidates, and token-filter
- * callbacks. The pool outputs of the batch decodes into caller arrays are
- * served. Forced tokens (an entry >= 0: the one token a read beam may take at that
+ * naming it: the relaxed pool's gradients (grad_relaxed_weights,
+ * grad_pool_scores, grad_pool_raw_scores), pools of more than 1024
+ * candidates, and token-filter callbacks. The relaxed pool itself is served:
+ * the pool outputs of the batch decodes into caller arrays, and the pool
+ * and soft top-k inclusion weights of result handles. Forced tokens (an entry >= 0: the one token a read beam may take at that
  * step) are served by every decode that takes them: the batch decodes into
  * caller arrays, the result-handle decodes and the model-step decodes.
  */
@@ -62,12 +62,12 @@ typedef struct DBSOptionsC {
     int beam_size;                       /* K [8] */
     int eos_token;                       /* -1: no EOS handling */
     float selected_temperature;          /* softmax temperature of the selected-beam weights [1.0] */
-    float soft_topk_temperature;         /* [0.25] (relaxed pool: not served) */
+    float soft_topk_temperature;         /* [0.25] soft top-k weights of the pool */
     int relaxed_pool_multiplier;         /* [0] m: pool of m * K candidates a step (<= 1024) */
     int vocab_block;                     /* ignored */
     float length_penalty_alpha;          /* GNMT ((5 + len) / 6)^alpha; 0 disables [0] */
-    float soft_topk_tolerance;           /* [1e-4] (relaxed pool: not served) */
-    int soft_topk_max_iters;             /* [48] (relaxed pool: not served) */
+    float soft_topk_tolerance;           /* [1e-4] */
+    int soft_topk_max_iters;             /* [48] */
     int min_length;                      /* EOS masked below this length [0] */
     int validate_inputs;                 /* non-zero: NaN/+inf in a row the search reads is an error */
     int64_t max_dense_gradient_elements; /* cap on T*K*V for dbs_backward_dense() [1e8] */

@@ -286,6 +286,10 @@ def _declare_results(L):
         "dbs_result_final_raw_scores": (_f32p, [vp]),
         "dbs_result_relaxed_weights": (_f32p, [vp]),
         "dbs_result_pool_tokens": (_i32p, [vp]),
+        "dbs_result_pool_parents": (_i32p, [vp]),
+        "dbs_result_pool_lengths": (_i32p, [vp]),
+        "dbs_result_pool_scores": (_f32p, [vp]),
+        "dbs_result_pool_raw_scores": (_f32p, [vp]),
         "dbs_backward_grad_log_probs": (_f32p, [vp]),
         "dbs_backward_grad_initial_scores": (_f32p, [vp]),
         "dbs_backward_sparse_logprob_indices": (C.POINTER(C.c_int64), [vp]),
@@ -339,6 +343,12 @@ def read_result(L, r) -> dict:
     out["final_raw_scores"] = _copy(L.dbs_result_final_raw_scores(r), K, np.float32)
     out["relaxed_weights_null"] = not L.dbs_result_relaxed_weights(r)
     out["pool_tokens_null"] = not L.dbs_result_pool_tokens(r)
+    P = out["pool_size"]
+    if P > 0:
+        for name in ("pool_tokens", "pool_parents", "pool_lengths"):
+            out[name] = _copy(getattr(L, f"dbs_result_{name}")(r), T * P, np.int32)
+        for name in ("pool_scores", "pool_raw_scores", "relaxed_weights"):
+            out[name] = _copy(getattr(L, f"dbs_result_{name}")(r), T * P, np.float32)
     out["counts"] = (L.dbs_result_selected_count(r), L.dbs_result_pool_count(r), L.dbs_result_logprob_count(r),
                      L.dbs_backward_grad_log_probs_count(r), L.dbs_backward_grad_initial_scores_count(r))
     out["order"] = L.dbs_result_validate_deterministic_order(r)

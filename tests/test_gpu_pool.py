@@ -138,3 +138,137 @@ def test_pool_multiplier_without_pool_outputs(libs):
     case["kw"]["banned_per_example"] = None
     _check(libs, case, 3, pool=False)
 
+
+
+# ---------------------------------------------------------------------------
+# Result handles: the pool of every step and its soft top-k inclusion weights
+# ---------------------------------------------------------------------------
+
+def _soft(seed):
+    """Soft top-k options: temperature, tolerance and iteration cap."""
+    return [dict(), dict(soft_topk_temperature=1.0), dict(soft_topk_temperature=0.05, soft_topk_tolerance=1e-2),
+            dict(soft_topk_max_iters=5)][seed % 4]
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_pool_result_decodes(libs, seed):
+    """dbs_decode, dbs_decode_constrained_ex (with forced tokens, n-gram
+    blocking, a repetition penalty) and dbs_decode_batch with a pool: the
+    pool arrays, relaxed weights, counts and statistics."""
+    import ctypes as C
+
+    from tests.host_abi import StatsC, read_result
+
+    case = make_case(44000 + seed, dtypes=["f32"], logits=False, allow_invalid=False)
+    kw = case["kw"]
+    B, K, T, V = case["B"], case["K"], case["T"], case["V"]
+    m = [1, 2, 3, 4][seed % 4]
+    x1 = np.ascontiguousarray(case["xin"][0])
+    xb = np.ascontiguousarray(case["xin"])
+    rng = np.random.default_rng(seed)
+    forced = np.where(rng.random(T) < 0.3, rng.integers(0, V, T), -1).astype(np.int32)
+    opts = dict(beam_size=K, eos_token=kw["eos_token"], length_penalty_alpha=kw["alpha"],
+                min_length=kw["min_length"], relaxed_pool_multiplier=m, selected_temperature=0.5, **_soft(seed))
+
+    def run(lib, h):
+        L = lib.lib
+        f32p = C.POINTER(C.c_float)
+        res = {}
+        r, br = C.c_void_p(), C.c_void_p()
+        st = L.dbs_decode(h, x1.ctypes.data_as(f32p), T, V, C.byref(r))
+        s = StatsC()
+        assert L.dbs_get_stats(h, C.byref(s)) == 0
+        res["decode"] = (st, lib.error(), read_result(L, r) if st == 0 else None, s.last_pool_count)
+        L.dbs_free_result(r)
+        keep = {}
+        c = HostLib.constraints(banned=kw["banned"], repetition_penalty=1.3, no_repeat_ngram_size=2, forced=forced,
+                                keep=keep)
+        st = L.dbs_decode_constrained_ex(h, x1.ctypes.data_as(f32p), T, V, C.byref(c), C.byref(r))
+        res["constrained_ex"] = (st, lib.error(), read_result(L, r) if st == 0 else None)
+        L.dbs_free_result(r)
+        st = L.dbs_decode_batch(h, xb.ctypes.data_as(f32p), B, T, V, 1, C.byref(br))
+        res["batch"] = (st, lib.error(),
+                        [read_result(L, L.dbs_batch_result_at(br, b)) for b in range(L.dbs_batch_result_size(br))])
+        L.dbs_free_batch_result(br)
+        return res
+
+    from tests.test_gpu_host_results import same
+
+    ours, theirs = _each(libs, opts, run, kw["extra_eos"])
+    same(ours, theirs, f"seed {seed} m {m}")
+    assert ours["decode"][0] == 0 and ours["decode"][2]["pool_size"] == K * m
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_pool_variable_batches(libs, seed):
+    """dbs_decode_batch_variable with a pool: each example's pool is
+    beams_b * m candidates."""
+    import ctypes as C
+
+    from tests.host_abi import read_result
+    from tests.test_gpu_host_results import same
+
+    rng = np.random.default_rng(45000 + seed)
+    B, T, Kmax, V = int(rng.integers(1, 5)), int(rng.integers(1, 7)), int(rng.choice([2, 4, 8])), \
+        int(rng.choice([7, 50, 300]))
+    x = np.ascontiguousarray(log_softmax(rng.normal(0, 2.0, (B, T, Kmax, V)).astype(np.float32)))
+    steps = rng.integers(1, T + 1, B).astype(np.int32)
+    beams = rng.integers(1, Kmax + 1, B).astype(np.int32)
+    eos = rng.integers(-1, V, B).astype(np.int32)
+    opts = dict(beam_size=Kmax, eos_token=int(rng.integers(-1, V)), length_penalty_alpha=0.6,
+                relaxed_pool_multiplier=int(rng.integers(1, 4)), **_soft(seed))
+
+    def run(lib, h):
+        L = lib.lib
+        br = C.c_void_p()
+        i32 = C.POINTER(C.c_int32)
+        st = L.dbs_decode_batch_variable(h, x.ctypes.data_as(C.POINTER(C.c_float)), B, T, Kmax, V,
+                                         steps.ctypes.data_as(i32), beams.ctypes.data_as(i32),
+                                         eos.ctypes.data_as(i32), None, None, None, 1, C.byref(br))
+        out = [read_result(L, L.dbs_batch_result_at(br, b)) for b in range(L.dbs_batch_result_size(br))]
+        L.dbs_free_batch_result(br)
+        return st, lib.error(), out
+
+    ours, theirs = _each(libs, opts, run)
+    assert ours[:2] == theirs[:2] and ours[0] == 0, (ours[:2], theirs[:2])
+    for b, (a, c) in enumerate(zip(ours[2], theirs[2])):
+        same(a, c, f"example {b}")
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_pool_model_step_decodes(libs, seed):
+    """Model-step decodes keep a pool each step (the device step API)."""
+    import ctypes as C
+
+    from tests.host_abi import read_result
+    from tests.test_gpu_host_results import _logs_equal, _recorder, same
+
+    case = make_case(46000 + seed, dtypes=["f32"], logits=False, allow_invalid=False)
+    kw = case["kw"]
+    K, T, V = case["K"], case["T"], case["V"]
+    x = np.ascontiguousarray(case["xin"][0])
+    opts = dict(beam_size=K, eos_token=kw["eos_token"], length_penalty_alpha=kw["alpha"],
+                min_length=kw["min_length"], relaxed_pool_multiplier=[1, 2, 4][seed % 3], **_soft(seed))
+
+    def run(lib, h):
+        L = lib.lib
+        out, logs = {}, {}
+        for mode in ("plain", "constrained"):
+            log = []
+            simple, ex = _recorder(x, log)
+            r = C.c_void_p()
+            if mode == "plain":
+                st = L.dbs_decode_model_steps(h, simple, None, 0, T, V, C.byref(r))
+            else:
+                keep = {}
+                c = HostLib.constraints(banned=kw["banned"], repetition_penalty=1.3, no_repeat_ngram_size=2, keep=keep)
+                st = L.dbs_decode_model_steps_ex(h, ex, None, 1, T, V, C.byref(c), C.byref(r))
+            out[mode] = (st, lib.error(), read_result(L, r) if st == 0 else None)
+            logs[mode] = log
+            L.dbs_free_result(r)
+        return out, logs
+
+    (ours, our_logs), (theirs, their_logs) = _each(libs, opts, run, kw["extra_eos"])
+    same(ours, theirs, f"seed {seed}")
+    for mode in our_logs:
+        _logs_equal(our_logs[mode], their_logs[mode])
