@@ -401,8 +401,18 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
     return finish_decode(stream, e, fault);
 }
 
+void set_pool_grads(BackwardParams& p, const PoolGrads* pool) {
+    if (!pool || pool->P <= 0 || !pool->d) return;
+    p.P = pool->P;
+    p.pool_parents = pool->parents;
+    p.pool_tokens = pool->tokens;
+    p.pool_flp = pool->from_logprob;
+    p.pool_d = pool->d;
+}
+
 int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, void* out, int out_type,
-                    bool accumulate, void* workspace, int64_t workspace_bytes, void* stream_ptr) {
+                    bool accumulate, void* workspace, int64_t workspace_bytes, void* stream_ptr,
+                    const PoolGrads* pool = nullptr) {
     if (!valid_args(args) || !in || !out) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!in->parents || !in->tokens || !in->lengths || !in->from_logprob) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (in->reserved0 != 0) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
@@ -445,6 +455,7 @@ int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* 
     p.out = out;
     p.out_type = out_type;
     p.accumulate = accumulate ? 1 : 0;
+    set_pool_grads(p, pool);
     e = launch_path_walk(p, stream);
     if (e == hipSuccess) e = launch_dense_gradient(p, stream);
     return finish(stream, e);
@@ -482,8 +493,13 @@ int64_t workspace_for_host(const DBSCudaDecodeArgs* args, int pool_mult, int ste
                                     .total);
 }
 
-int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, float* draws,
-                        hipStream_t stream) {
+int backward_dense_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, const PoolGrads* pool,
+                            float* grad, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+    return backward_common(args, in, grad, DBS_HIP_GRAD_F32, false, workspace, workspace_bytes, stream, pool);
+}
+
+int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, const PoolGrads* pool,
+                        float* draws, hipStream_t stream) {
     if (!valid_args(args) || !in || !draws || !in->parents || !in->tokens || !in->lengths || !in->from_logprob)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     const DBSCudaDecodeArgs& a = *args;
@@ -503,6 +519,7 @@ int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInpu
     p.g_scores = in->grad_scores;
     p.g_raw = in->grad_raw_scores;
     p.draws = draws;
+    set_pool_grads(p, pool);
     return finish(stream, launch_path_walk(p, stream));
 }
 

@@ -108,6 +108,14 @@ __global__ __launch_bounds__(kWalkThreads) void path_walk_kernel(BackwardParams 
             float s = 0.0f;
             for (int k = 0; k < K; ++k)
                 if (par[k] == q) s = s + draw[k];
+            if (p.pool_d) {
+                // then the pool entries of the step with this parent
+                const int64_t pb = (static_cast<int64_t>(b) * T + t) * p.P;
+                for (int j = 0; j < p.P; ++j) {
+                    const float dj = p.pool_d[pb + j];
+                    if (dj != 0.0f && p.pool_parents[pb + j] == q) s = s + dj;
+                }
+            }
             prev[q] = s;
         }
         __syncthreads();
@@ -336,11 +344,14 @@ __device__ __forceinline__ void zero_row(void* out, int64_t row_off, int V) {
     }
 }
 
-template <int DT, int OT, bool LOGITS>
+// POOL: the relaxed pool's entries join the row's (after the selected
+// slots' entries of the same token: slot K + j), up to K + P entries a row.
+template <int DT, int OT, bool LOGITS, bool POOL = false>
 __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardParams p) {
-    __shared__ int32_t e_tok[DBS_CUDA_MAX_BEAM];
-    __shared__ float e_val[DBS_CUDA_MAX_BEAM];
-    __shared__ int32_t e_slot[DBS_CUDA_MAX_BEAM];
+    constexpr int kEntries = POOL ? 2 * DBS_CUDA_MAX_BEAM : DBS_CUDA_MAX_BEAM;
+    __shared__ int32_t e_tok[kEntries];
+    __shared__ float e_val[kEntries];
+    __shared__ int32_t e_slot[kEntries];
     __shared__ int n_raw;
     __shared__ int n_ent;
     __shared__ float s_sum;
@@ -371,6 +382,19 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardP
                 e_tok[i] = p.tokens[base + k];
                 e_val[i] = d;
                 e_slot[i] = k;
+            }
+        }
+        if constexpr (POOL) {
+            const int64_t pb = (static_cast<int64_t>(b) * T + t) * p.P;
+            for (int j = tid; j < p.P; j += kDenseThreads) {
+                const float d = p.pool_d[pb + j];
+                const int32_t tok = p.pool_tokens[pb + j];
+                if (d != 0.0f && p.pool_parents[pb + j] == q && p.pool_flp[pb + j] && tok >= 0 && tok < V) {
+                    const int i = atomicAdd(&n_raw, 1);
+                    e_tok[i] = tok;
+                    e_val[i] = d;
+                    e_slot[i] = K + j;
+                }
             }
         }
     }
@@ -546,7 +570,16 @@ hipError_t launch_dense_ot(const BackwardParams& p, hipStream_t stream) {
     if (rows > 0x7fffffffLL) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>(rows));
     KernelTimer timer(kKindDense, stream);
-    if (!p.logits) {
+    if (p.pool_d) {
+        if (!p.logits)
+            hipLaunchKernelGGL((dense_gradient_kernel<0, OT, false, true>), grid, dim3(kDenseThreads), 0, stream, p);
+        else if (p.logits_type == 0)
+            hipLaunchKernelGGL((dense_gradient_kernel<0, OT, true, true>), grid, dim3(kDenseThreads), 0, stream, p);
+        else if (p.logits_type == 1)
+            hipLaunchKernelGGL((dense_gradient_kernel<1, OT, true, true>), grid, dim3(kDenseThreads), 0, stream, p);
+        else
+            hipLaunchKernelGGL((dense_gradient_kernel<2, OT, true, true>), grid, dim3(kDenseThreads), 0, stream, p);
+    } else if (!p.logits) {
         hipLaunchKernelGGL((dense_gradient_kernel<0, OT, false>), grid, dim3(kDenseThreads), 0, stream, p);
     } else if (p.logits_type == 0) {
         hipLaunchKernelGGL((dense_gradient_kernel<0, OT, true>), grid, dim3(kDenseThreads), 0, stream, p);
@@ -612,7 +645,10 @@ size_t backward_workspace_bytes(int B, int T, int K) {
 
 hipError_t launch_path_walk(const BackwardParams& p, hipStream_t stream) {
     KernelTimer timer(kKindPathWalk, stream);
-    if (p.K <= 64 && static_cast<int64_t>(p.T) * p.K <= kWalkStageSlots) {
+    if (p.pool_d) {
+        // relaxed-pool terms: the workgroup walk (the only one that adds them)
+        hipLaunchKernelGGL(path_walk_kernel, dim3(p.B), dim3(kWalkThreads), 0, stream, p);
+    } else if (p.K <= 64 && static_cast<int64_t>(p.T) * p.K <= kWalkStageSlots) {
         const dim3 g(p.B), blk(kWalkStageThreads);
         const size_t lds = walk_stage_bytes(p);
         if (p.K <= 8) hipLaunchKernelGGL(path_walk_staged_kernel<8>, g, blk, lds, stream, p);

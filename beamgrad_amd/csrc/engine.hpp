@@ -264,6 +264,15 @@ struct BackwardParams {
     void* out;         // [B, T, K, V]
     int out_type;      // 0 f32, 1 f16, 2 bf16
     int accumulate;    // 1: out += g (f32 only); 0: out = 0 + g everywhere
+    // Relaxed-pool entries [B, T, P] (pool_d null: none; reference
+    // src/decoder.cpp:617-657): each entry's raw-score gradient d, added to
+    // its parent's incoming gradient after the selected children (in entry
+    // order), and to its log-prob entry when it came from one.
+    int P;
+    const int32_t* pool_parents;
+    const int32_t* pool_tokens;
+    const uint8_t* pool_flp;
+    const float* pool_d;
 };
 
 size_t backward_workspace_bytes(int B, int T, int K);

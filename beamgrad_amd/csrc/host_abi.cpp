@@ -25,6 +25,7 @@
 #include "dbs_cuda.h"
 #include "dbs_hip.h"
 #include "host_entry.hpp"
+#include "numerics.hpp"
 
 namespace dbs_host {
 
@@ -289,7 +290,7 @@ void run_decode(DBSDecoderHandle* h, const DecodeJob& j) {
 }
 
 void check_trace(int B, int T, int K, int V, const std::vector<int32_t>& steps_b, const int32_t* parents,
-                 const int32_t* tokens, const int32_t* lengths) {
+                 const int32_t* tokens, const int32_t* lengths, const PoolTerms* pool) {
     for (int b = 0; b < B; ++b) {
         const size_t base = static_cast<size_t>(b) * T * K;
         const size_t n = static_cast<size_t>(steps_b[static_cast<size_t>(b)]) * K;
@@ -297,7 +298,89 @@ void check_trace(int B, int T, int K, int V, const std::vector<int32_t>& steps_b
             if (parents[i] < -1 || parents[i] >= K || tokens[i] < -1 || tokens[i] >= V || lengths[i] < 0)
                 example_error(b, "decode trace is out of range (parents, tokens or lengths)");
         }
+        if (!pool || pool->P <= 0) continue;
+        const size_t pbase = static_cast<size_t>(b) * T * pool->P;
+        const size_t np = static_cast<size_t>(steps_b[static_cast<size_t>(b)]) * pool->P;
+        for (size_t i = pbase; i < pbase + np; ++i) {
+            if (pool->parents[i] < -1 || pool->parents[i] >= K || pool->tokens[i] < -1 || pool->tokens[i] >= V ||
+                pool->lengths[i] < 0)
+                example_error(b, "pool trace is out of range (parents, tokens or lengths)");
+        }
     }
+}
+
+void pool_entry_grads(int T, int P, float alpha, float soft_temperature, const int32_t* parents,
+                      const int32_t* lengths, const float* r, const float* gr, const float* g_scores,
+                      const float* g_raw, float* d) {
+    constexpr float kEps = 1.0e-12f;
+    for (int t = 0; t < T; ++t) {
+        const size_t base = static_cast<size_t>(t) * P;
+        // the relaxed weights' implicit gradient through the bisected
+        // threshold: a_p (gr_p - sum(gr a) / sum(a)) / temperature, a = r (1 - r)
+        bool relaxed = false;
+        float center = 0.0f, inv_temp = 0.0f;
+        if (r && gr) {
+            float denom = 0.0f, numer = 0.0f;
+            for (int p = 0; p < P; ++p) {
+                const float a = r[base + p] * (1.0f - r[base + p]);
+                denom += a;
+                numer += gr[base + p] * a;
+            }
+            if (denom > kEps) {
+                relaxed = true;
+                center = numer / denom;
+                inv_temp = 1.0f / soft_temperature;
+            }
+        }
+        for (int p = 0; p < P; ++p) {
+            const size_t i = base + static_cast<size_t>(p);
+            d[i] = 0.0f;
+            if (parents[i] < 0) continue;
+            float drank = 0.0f;
+            if (relaxed) {
+                const float a = r[i] * (1.0f - r[i]);
+                drank += a * inv_temp * (gr[i] - center);
+            }
+            if (g_scores) drank += g_scores[i];
+            const float inv_penalty = 1.0f / dbs_hip::length_penalty(std::max(1, static_cast<int>(lengths[i])), alpha);
+            float v = drank * inv_penalty;
+            if (g_raw) v += g_raw[i];
+            d[i] = v;
+        }
+    }
+}
+
+std::vector<std::pair<int64_t, float>> step_entries(int T, int K, int V, int b, int t, const std::vector<float>& draws,
+                                                    const int32_t* parents, const int32_t* tokens,
+                                                    const uint8_t* from_logprob, const PoolTerms* pool) {
+    std::vector<std::pair<int64_t, float>> raw;  // in the order the reference produces them
+    auto index = [&](int parent, int token) {
+        return (static_cast<int64_t>(t) * K + parent) * static_cast<int64_t>(V) + token;
+    };
+    const size_t base = (static_cast<size_t>(b) * T + t) * K;
+    for (int k = 0; k < K; ++k) {
+        const size_t i = base + static_cast<size_t>(k);
+        if (draws[i] == 0.0f || parents[i] < 0 || !from_logprob[i] || tokens[i] < 0) continue;
+        raw.emplace_back(index(parents[i], tokens[i]), draws[i]);
+    }
+    if (pool && pool->P > 0) {
+        const size_t pbase = (static_cast<size_t>(b) * T + t) * pool->P;
+        for (int p = 0; p < pool->P; ++p) {
+            const size_t i = pbase + static_cast<size_t>(p);
+            if (pool->d[i] == 0.0f || pool->parents[i] < 0 || !pool->from_logprob[i] || pool->tokens[i] < 0) continue;
+            raw.emplace_back(index(pool->parents[i], pool->tokens[i]), pool->d[i]);
+        }
+    }
+    std::stable_sort(raw.begin(), raw.end(), [](const auto& x, const auto& y) { return x.first < y.first; });
+    std::vector<std::pair<int64_t, float>> merged;
+    for (size_t i = 0; i < raw.size();) {
+        float v = 0.0f;
+        size_t j = i;
+        for (; j < raw.size() && raw[j].first == raw[i].first; ++j) v += raw[j].second;
+        merged.emplace_back(raw[i].first, v);
+        i = j;
+    }
+    return merged;
 }
 
 namespace {
@@ -318,7 +401,8 @@ DBSCudaDecodeArgs trace_args(int B, int T, int K, int V, float alpha) {
 
 std::vector<float> path_draws(DBSDecoderHandle* h, int B, int T, int K, int V, float alpha,
                               const int32_t* steps_per_example, const int32_t* parents, const int32_t* tokens,
-                              const int32_t* lengths, const uint8_t* from_logprob, const Grads& g) {
+                              const int32_t* lengths, const uint8_t* from_logprob, const Grads& g,
+                              const PoolTerms* pool) {
     check_engine_limits(h, K, V);
     const size_t BK = static_cast<size_t>(B) * K, BTK = BK * static_cast<size_t>(T);
     std::lock_guard<std::mutex> lock(h->run_mutex);
@@ -335,7 +419,16 @@ std::vector<float> path_draws(DBSDecoderHandle* h, int B, int T, int K, int V, f
     in.grad_scores = upload(h, kGradScores, g.scores, BTK, st);
     in.grad_raw_scores = upload(h, kGradRaw, g.raw, BTK, st);
     float* draws_d = static_cast<float*>(h->arena.get(kDraws, sizeof(float) * BTK));
-    engine_check(dbs_hip::path_draws_for_host(&a, &in, draws_d, st), "HIP path gradient");
+    dbs_hip::PoolGrads pg;
+    if (pool && pool->P > 0) {
+        const size_t BTP = static_cast<size_t>(B) * T * static_cast<size_t>(pool->P);
+        pg.P = pool->P;
+        pg.parents = upload(h, kPoolParents, pool->parents, BTP, st);
+        pg.tokens = upload(h, kPoolTokens, pool->tokens, BTP, st);
+        pg.from_logprob = upload(h, kPoolFromLogprob, pool->from_logprob, BTP, st);
+        pg.d = upload(h, kPoolD, pool->d.data(), BTP, st);
+    }
+    engine_check(dbs_hip::path_draws_for_host(&a, &in, pg.P > 0 ? &pg : nullptr, draws_d, st), "HIP path gradient");
     std::vector<float> draws(BTK);
     download(draws.data(), draws_d, BTK, st);
     hip_check(hipStreamSynchronize(st), "HIP path gradient");
@@ -485,16 +578,35 @@ size_t backward_chunk_bytes() {
 // row that an entry lands in.
 void backward_batch(DBSDecoderHandle* h, int B, int T, int V, const int32_t* steps_per_example,
                     const int32_t* parents, const int32_t* tokens, const int32_t* lengths, const uint8_t* flp,
-                    const Grads& g, const void* logits, int logits_type, const float* row_lse, float* grad) {
+                    const Grads& g, const void* logits, int logits_type, const float* row_lse, float* grad,
+                    PoolTerms* pool, const float* g_pool_scores, const float* g_pool_raw) {
     const auto start = std::chrono::steady_clock::now();
     const int K = h->beam_size;
     const size_t trace = mul(static_cast<size_t>(T), static_cast<size_t>(K), "batch stride overflow");
     const size_t row_block = mul(trace, static_cast<size_t>(V), "batch stride overflow");
     (void)mul(row_block, static_cast<size_t>(B), "batch size overflow");
     const std::vector<int32_t> steps_b = steps_of(steps_per_example, B, T);
-    check_trace(B, T, K, V, steps_b, parents, tokens, lengths);
-    const std::vector<float> draws =
-        path_draws(h, B, T, K, V, h->alpha, steps_per_example, parents, tokens, lengths, flp, g);
+    const bool with_pool = pool && pool->P > 0;
+    if (with_pool) {
+        need(pool->P <= DBS_CUDA_MAX_BEAM, "a relaxed pool of more than 1024 candidates is beyond the HIP engine");
+        (void)mul(mul(static_cast<size_t>(T), static_cast<size_t>(pool->P), "batch stride overflow"),
+                  static_cast<size_t>(B), "batch size overflow");
+    }
+    check_trace(B, T, K, V, steps_b, parents, tokens, lengths, with_pool ? pool : nullptr);
+    if (with_pool) {
+        // each example's pool entries over its own steps (0 past them)
+        const size_t TP = static_cast<size_t>(T) * pool->P;
+        pool->d.assign(TP * static_cast<size_t>(B), 0.0f);
+        for (int b = 0; b < B; ++b) {
+            const size_t off = static_cast<size_t>(b) * TP;
+            pool_entry_grads(steps_b[static_cast<size_t>(b)], pool->P, h->alpha, h->soft_topk_temperature,
+                             pool->parents + off, pool->lengths + off, nullptr, nullptr,
+                             g_pool_scores ? g_pool_scores + off : nullptr, g_pool_raw ? g_pool_raw + off : nullptr,
+                             pool->d.data() + off);
+        }
+    }
+    const std::vector<float> draws = path_draws(h, B, T, K, V, h->alpha, steps_per_example, parents, tokens, lengths,
+                                                flp, g, with_pool ? pool : nullptr);
     const size_t BTK = static_cast<size_t>(B) * trace;
 
     // (b, t, parent) row and token of every slot with an entry: distinct
@@ -507,12 +619,26 @@ void backward_batch(DBSDecoderHandle* h, int B, int T, int V, const int32_t* ste
         token = tokens[i];
         return true;
     };
-    if (!logits) {
+    // the pool entries' (b, t, parent) rows: entries of their own
+    auto pool_row_of = [&](size_t i, size_t& row) -> bool {
+        if (pool->d[i] == 0.0f || pool->parents[i] < 0 || !pool->from_logprob[i] || pool->tokens[i] < 0) return false;
+        const size_t bt = i / static_cast<size_t>(pool->P);
+        row = bt * static_cast<size_t>(K) + static_cast<size_t>(pool->parents[i]);
+        return true;
+    };
+    if (!logits && !with_pool) {
         for (size_t i = 0; i < BTK; ++i) {
             size_t row = 0;
             int token = 0;
             if (entry_of(i, row, token)) grad[row * static_cast<size_t>(V) + static_cast<size_t>(token)] += draws[i];
         }
+    } else if (!logits) {
+        // each entry merged from 0 (the step's selected draw, then its pool
+        // entries'), then added (reference src/c_api.cpp:948-951)
+        for (int b = 0; b < B; ++b)
+            for (int t = 0; t < steps_b[static_cast<size_t>(b)]; ++t)
+                for (const auto& e : step_entries(T, K, V, b, t, draws, parents, tokens, flp, pool))
+                    grad[static_cast<size_t>(b) * row_block + static_cast<size_t>(e.first)] += e.second;
     } else {
         // From logits: the device writes each gradient row (g - softmax(row) *
         // sum(g), entries summed in token order; zero rows elsewhere), a
@@ -531,6 +657,12 @@ void backward_batch(DBSDecoderHandle* h, int B, int T, int V, const int32_t* ste
                 size_t row = 0;
                 int token = 0;
                 if (entry_of(i, row, token)) rows.push_back(row);
+            }
+            const size_t pstride = with_pool ? static_cast<size_t>(T) * pool->P : 0;
+            const size_t poff = static_cast<size_t>(b0) * pstride, npool = static_cast<size_t>(nb) * pstride;
+            for (size_t i = poff; i < poff + npool; ++i) {
+                size_t row = 0;
+                if (pool_row_of(i, row)) rows.push_back(row);
             }
             if (rows.empty()) continue;
             std::sort(rows.begin(), rows.end());
@@ -557,7 +689,16 @@ void backward_batch(DBSDecoderHandle* h, int B, int T, int V, const int32_t* ste
             const int64_t ws_bytes = dbs_cuda_backward_workspace_size(&a);
             need(ws_bytes > 0, "invalid backward arguments");
             void* ws = h->arena.get(kWorkspace, static_cast<size_t>(ws_bytes));
-            engine_check(dbs_hip_backward_dense(&a, &in, dense, DBS_HIP_GRAD_F32, ws, ws_bytes, st), "HIP backward");
+            dbs_hip::PoolGrads pg;
+            if (with_pool) {
+                pg.P = pool->P;
+                pg.parents = upload(h, kPoolParents, pool->parents + poff, npool, st);
+                pg.tokens = upload(h, kPoolTokens, pool->tokens + poff, npool, st);
+                pg.from_logprob = upload(h, kPoolFromLogprob, pool->from_logprob + poff, npool, st);
+                pg.d = upload(h, kPoolD, pool->d.data() + poff, npool, st);
+            }
+            engine_check(dbs_hip::backward_dense_for_host(&a, &in, with_pool ? &pg : nullptr, dense, ws, ws_bytes, st),
+                         "HIP backward");
             std::vector<float> buf(rows.size() * static_cast<size_t>(V));
             for (size_t r = 0; r < rows.size(); ++r)
                 download(buf.data() + r * V, dense + (rows[r] - off) * V, static_cast<size_t>(V), st);
@@ -698,7 +839,7 @@ DBS_EXPORT int dbs_backward_batch_into(DBSDecoderHandle* handle, int batch_size,
         Grads g;
         g.final_scores = grad_final_scores;
         backward_batch(handle, batch_size, steps, vocab_size, steps_per_example, parents, tokens, lengths,
-                       from_logprob, g, nullptr, 0, nullptr, grad_log_probs);
+                       from_logprob, g, nullptr, 0, nullptr, grad_log_probs, nullptr, nullptr, nullptr);
     });
 }
 
@@ -718,7 +859,6 @@ DBS_EXPORT int dbs_backward_batch_into_ex(DBSDecoderHandle* handle, const DBSBac
         need(!pool_grads || (in->pool_size > 0 && in->pool_parents && in->pool_tokens && in->pool_lengths &&
                              in->pool_from_logprob),
              "pool gradients need pool_size > 0 and the pool trace");
-        need(!pool_grads, "relaxed-pool gradients are not served by libdbs_hip (the HIP engine)");
         if (in->logits) {
             check_dtype(in->logits_type);
             need(in->row_lse != nullptr, "row_lse cannot be null with logits");
@@ -728,9 +868,17 @@ DBS_EXPORT int dbs_backward_batch_into_ex(DBSDecoderHandle* handle, const DBSBac
         g.final_raw = in->grad_final_raw_scores;
         g.scores = in->grad_scores;
         g.raw = in->grad_raw_scores;
+        PoolTerms pool;
+        if (pool_grads) {
+            pool.P = in->pool_size;
+            pool.parents = in->pool_parents;
+            pool.tokens = in->pool_tokens;
+            pool.lengths = in->pool_lengths;
+            pool.from_logprob = in->pool_from_logprob;
+        }
         backward_batch(handle, in->batch_size, in->steps, in->vocab_size, in->steps_per_example, in->parents,
                        in->tokens, in->lengths, in->from_logprob, g, in->logits, in->logits_type, in->row_lse,
-                       grad_inputs);
+                       grad_inputs, pool_grads ? &pool : nullptr, in->grad_pool_scores, in->grad_pool_raw_scores);
     });
 }
 

@@ -17,6 +17,7 @@
 #include <new>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "dbs.h"
@@ -29,7 +30,7 @@ enum Slot : int {
     kInputs, kBanned, kBannedPe, kSteps, kBeams, kEos, kMinLengths, kFinalScores, kFinalRaw, kFinalLengths, kTokens,
     kParents, kLengths, kScores, kRawScores, kFromLogprob, kRowLse, kFirstInvalid, kWorkspace, kGradFinal,
     kGradFinalRaw, kGradScores, kGradRaw, kDraws, kDense, kState, kForced, kPoolParents, kPoolTokens,
-    kPoolLengths, kPoolScores, kPoolRaw, kPoolFromLogprob, kSlotCount
+    kPoolLengths, kPoolScores, kPoolRaw, kPoolFromLogprob, kPoolD, kSlotCount
 };
 
 struct Arena {
@@ -224,17 +225,48 @@ struct Grads {
     const float* raw = nullptr;           // [B, T, K]
 };
 
+// Relaxed-pool entries of a backward, host arrays [B, T, P] (P 0: none):
+// the pool trace and each entry's raw-score gradient d.
+struct PoolTerms {
+    int P = 0;
+    const int32_t* parents = nullptr;
+    const int32_t* tokens = nullptr;
+    const int32_t* lengths = nullptr;
+    const uint8_t* from_logprob = nullptr;
+    std::vector<float> d;
+};
+
+// d of the pool entries of one example's T steps (reference
+// src/decoder.cpp:617-657): the relaxed weights' term (r: the forward's
+// relaxed weights, gr: their gradient, [T, P] or null; soft_temperature the
+// forward's), then the pool score and raw-score gradients (or null); 0 for
+// dead entries.
+void pool_entry_grads(int T, int P, float alpha, float soft_temperature, const int32_t* parents,
+                      const int32_t* lengths, const float* r, const float* gr, const float* g_scores,
+                      const float* g_raw, float* d);
+
 // The checks of a trace handed to a backward (reference src/decoder.cpp:
-// 947-963): indexes in range over each example's own steps.
+// 947-985): indexes in range over each example's own steps, the pool
+// trace's after the trace's.
 void check_trace(int B, int T, int K, int V, const std::vector<int32_t>& steps_b, const int32_t* parents,
-                 const int32_t* tokens, const int32_t* lengths);
+                 const int32_t* tokens, const int32_t* lengths, const PoolTerms* pool = nullptr);
 
 // The per-slot path gradients [B, T, K] of a checked trace (host arrays) on
 // the handle's GPU: slot (b, t, k) gets the raw-score gradient its selected
-// entry receives (reference src/decoder.cpp:540-610), 0 where it has none.
+// entry receives (reference src/decoder.cpp:540-610), 0 where it has none;
+// the pool entries' d join their parents' incoming gradients.
 std::vector<float> path_draws(DBSDecoderHandle* h, int B, int T, int K, int V, float alpha,
                               const int32_t* steps_per_example, const int32_t* parents, const int32_t* tokens,
-                              const int32_t* lengths, const uint8_t* from_logprob, const Grads& g);
+                              const int32_t* lengths, const uint8_t* from_logprob, const Grads& g,
+                              const PoolTerms* pool = nullptr);
+
+// The log-prob entries of step t of example b (selected slots' draws, then
+// the pool entries' d, each merged per entry from 0 in that order; reference
+// src/decoder.cpp:668-683): (index into the example's [T, K, V], value),
+// increasing index.
+std::vector<std::pair<int64_t, float>> step_entries(int T, int K, int V, int b, int t, const std::vector<float>& draws,
+                                                    const int32_t* parents, const int32_t* tokens,
+                                                    const uint8_t* from_logprob, const PoolTerms* pool);
 
 // DBSStatsC bookkeeping (reference src/c_api.cpp:117-158).
 void stats_decode(DBSDecoderHandle* h, int64_t elapsed_ns, int64_t selected, int64_t pool, int64_t logprobs,

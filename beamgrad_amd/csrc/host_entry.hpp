@@ -27,6 +27,19 @@ struct PoolOutputs {
     uint8_t* from_logprob = nullptr;
 };
 
+// Relaxed-pool entries of a backward (reference src/decoder.cpp:617-657):
+// device arrays [B, T, P]; d is each entry's raw-score gradient (computed on
+// the host from the pool gradients), added to its parent's incoming gradient
+// after the selected children and, for an entry from a log-prob, to that
+// entry.
+struct PoolGrads {
+    int P = 0;
+    const int32_t* parents = nullptr;
+    const int32_t* tokens = nullptr;
+    const uint8_t* from_logprob = nullptr;
+    const float* d = nullptr;
+};
+
 // Workspace bytes of decode_for_host (step_mode 0) or step_for_host
 // (step_mode 1, prefix_stride as dbs_cuda_decode_step_workspace_size) with a
 // relaxed pool of pool_mult (0: none); -1 for invalid arguments.
@@ -56,10 +69,15 @@ int step_for_host(const void* inputs, int data_type, int from_logits, const DBSC
 
 // The per-slot path gradients draws [B, T, K] of the surrogate backward for
 // every gradient input of `in` (final scores, final raw scores, scores, raw
-// scores; logits are not read): slot (b, t, k) gets the gradient of the
-// log-prob entry it selected, 0 where it selected none. Returns a
-// DBS_CUDA_STATUS_*.
-int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, float* draws,
-                        hipStream_t stream);
+// scores; logits are not read) and the relaxed-pool entries (pool may be
+// null): slot (b, t, k) gets the gradient of the log-prob entry it selected,
+// 0 where it selected none. Returns a DBS_CUDA_STATUS_*.
+int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, const PoolGrads* pool,
+                        float* draws, hipStream_t stream);
+
+// dbs_hip_backward_dense into a float32 gradient [B, T, K, V] written fresh,
+// with relaxed-pool entries (pool may be null). Returns a DBS_CUDA_STATUS_*.
+int backward_dense_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, const PoolGrads* pool,
+                            float* grad, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 }  // namespace dbs_hip

@@ -638,7 +638,18 @@ DBSBackwardHandle backward_of(DBSDecoderHandle& h, const DBSResultHandle& r, con
         throw std::length_error("dense gradient allocation exceeds max_dense_gradient_elements; use sparse backward");
     need(!grw || r.pool_size > 0,
          "relaxed-pool gradients need a relaxed pool: create the decoder with relaxed_pool_multiplier >= 1");
-    need(!grw, "relaxed-pool gradients are not served by libdbs_hip (the HIP engine)");
+    // the relaxed weights' gradient enters as the pool entries' d
+    PoolTerms pool;
+    if (grw) {
+        pool.P = r.pool_size;
+        pool.parents = r.pool_parents.data();
+        pool.tokens = r.pool_tokens.data();
+        pool.lengths = r.pool_lengths.data();
+        pool.from_logprob = r.pool_from_logprob.data();
+        pool.d.resize(static_cast<size_t>(T) * static_cast<size_t>(pool.P));
+        pool_entry_grads(T, pool.P, r.alpha, r.soft_topk_temperature, pool.parents, pool.lengths,
+                         r.relaxed_weights.data(), grw, nullptr, nullptr, pool.d.data());
+    }
     std::vector<float> g_scores;
     if (gw) {
         g_scores.assign(selected, 0.0f);
@@ -654,50 +665,43 @@ DBSBackwardHandle backward_of(DBSDecoderHandle& h, const DBSResultHandle& r, con
     g.final_scores = gf;
     g.scores = gw ? g_scores.data() : nullptr;
     const int32_t steps[1] = {T};
+    const PoolTerms* pool_p = pool.P > 0 ? &pool : nullptr;
     std::vector<float> draws;
-    if (gw || gf)
+    if (gw || gf || pool_p)
         draws = path_draws(&h, 1, T, K, V, r.alpha, steps, r.parents.data(), r.tokens.data(), r.lengths.data(),
-                           r.from_logprob.data(), g);
+                           r.from_logprob.data(), g, pool_p);
     else
         draws.assign(selected, 0.0f);
 
     DBSBackwardHandle out;
     out.sparse = sparse;
+    // the initial beams' gradient: step 0's selected draws, then its pool
+    // entries' d (reference src/decoder.cpp:566-662)
     out.grad_initial_scores.assign(static_cast<size_t>(K), 0.0f);
     for (int k = 0; k < K; ++k) {
         const float d = draws[static_cast<size_t>(k)];
         const int p = r.parents[static_cast<size_t>(k)];
         if (p >= 0 && d != 0.0f) out.grad_initial_scores[static_cast<size_t>(p)] += d;
     }
-    if (!sparse) out.grad_log_probs.assign(dense, 0.0f);
-    for (size_t i = 0; i < selected; ++i) {
-        const float d = draws[i];
-        if (d == 0.0f || r.parents[i] < 0 || !r.from_logprob[i] || r.tokens[i] < 0) continue;
-        const size_t t = i / static_cast<size_t>(K);
-        const int64_t index =
-            (static_cast<int64_t>(t) * K + r.parents[i]) * static_cast<int64_t>(V) + r.tokens[i];
-        if (sparse) {
-            out.sparse_indices.push_back(index);
-            out.sparse_values.push_back(d);
-        } else {
-            out.grad_log_probs[static_cast<size_t>(index)] += d;
+    if (pool_p && T > 0) {
+        for (int j = 0; j < pool.P; ++j) {
+            const float d = pool.d[static_cast<size_t>(j)];
+            const int p = pool.parents[j];
+            if (p >= 0 && d != 0.0f) out.grad_initial_scores[static_cast<size_t>(p)] += d;
         }
     }
-    if (sparse) {
-        // each selected slot of a step names a distinct (parent, token)
-        // entry, so sorting is all the reference's merge does here
-        std::vector<size_t> order(out.sparse_indices.size());
-        for (size_t i = 0; i < order.size(); ++i) order[i] = i;
-        std::stable_sort(order.begin(), order.end(),
-                         [&](size_t x, size_t y) { return out.sparse_indices[x] < out.sparse_indices[y]; });
-        std::vector<int64_t> idx(order.size());
-        std::vector<float> val(order.size());
-        for (size_t i = 0; i < order.size(); ++i) {
-            idx[i] = out.sparse_indices[order[i]];
-            val[i] = 0.0f + out.sparse_values[order[i]];
+    // the log-prob entries, merged per entry in the reference's order
+    if (!sparse) out.grad_log_probs.assign(dense, 0.0f);
+    for (int t = 0; t < T; ++t) {
+        for (const auto& e : step_entries(T, K, V, 0, t, draws, r.parents.data(), r.tokens.data(),
+                                          r.from_logprob.data(), pool_p)) {
+            if (sparse) {
+                out.sparse_indices.push_back(e.first);
+                out.sparse_values.push_back(e.second);
+            } else {
+                out.grad_log_probs[static_cast<size_t>(e.first)] += e.second;
+            }
         }
-        out.sparse_indices.swap(idx);
-        out.sparse_values.swap(val);
     }
     return out;
 }

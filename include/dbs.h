@@ -22,11 +22,11 @@
  *
  * All 81 functions of the reference's ABI are exported. What the GPU engine
  * does not serve is refused with DBS_ERROR_INVALID_ARGUMENT and a message
- * naming it: the relaxed pool's gradients (grad_relaxed_weights,
- * grad_pool_scores, grad_pool_raw_scores), pools of more than 1024
- * candidates, and token-filter callbacks. The relaxed pool itself is served:
- * the pool outputs of the batch decodes into caller arrays, and the pool
- * and soft top-k inclusion weights of result handles. Forced tokens (an entry >= 0: the one token a read beam may take at that
+ * naming it: token-filter callbacks and pools of more than 1024
+ * candidates. The relaxed pool is served: the pool outputs of the batch
+ * decodes into caller arrays, the pool and soft top-k inclusion weights of
+ * result handles, and the pool's gradients (grad_relaxed_weights,
+ * grad_pool_scores, grad_pool_raw_scores). Forced tokens (an entry >= 0: the one token a read beam may take at that
  * step) are served by every decode that takes them: the batch decodes into
  * caller arrays, the result-handle decodes and the model-step decodes.
  */

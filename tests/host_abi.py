@@ -184,10 +184,12 @@ class HostLib:
 
     def backward(self, h, trace: dict, V: int, initial: np.ndarray, *, steps=None, ex=True, grad_final=None,
                  grad_final_raw=None, grad_scores=None, grad_raw=None, logits=None, logits_dtype="f32",
-                 row_lse=None) -> tuple[int, np.ndarray]:
+                 row_lse=None, pool=None, grad_pool_scores=None, grad_pool_raw=None) -> tuple[int, np.ndarray]:
         """dbs_backward_batch_into_ex (or, ex=False, dbs_backward_batch_into
         with the final-score gradient) accumulating into a copy of
-        `initial`. Returns (status, gradient)."""
+        `initial`; `pool` holds a relaxed pool's trace (pool_parents,
+        pool_tokens, pool_lengths, pool_from_logprob [B, T, P]) for the pool
+        gradients. Returns (status, gradient)."""
         keep = {}
 
         def arr(name, a, dt):
@@ -216,8 +218,16 @@ class HostLib:
         inp.lengths, inp.from_logprob = _p(ln, C.c_int32), _p(flp, C.c_uint8)
         for name, field, g in (("gf", "grad_final_scores", grad_final), ("gfr", "grad_final_raw_scores",
                                                                         grad_final_raw),
-                               ("gs", "grad_scores", grad_scores), ("gr", "grad_raw_scores", grad_raw)):
+                               ("gs", "grad_scores", grad_scores), ("gr", "grad_raw_scores", grad_raw),
+                               ("gps", "grad_pool_scores", grad_pool_scores),
+                               ("gpr", "grad_pool_raw_scores", grad_pool_raw)):
             setattr(inp, field, _p(arr(name, g, np.float32), C.c_float))
+        if pool is not None:
+            inp.pool_size = int(pool["pool_parents"].shape[-1])
+            inp.pool_parents = _p(arr("pp", pool["pool_parents"], np.int32), C.c_int32)
+            inp.pool_tokens = _p(arr("pt", pool["pool_tokens"], np.int32), C.c_int32)
+            inp.pool_lengths = _p(arr("pl", pool["pool_lengths"], np.int32), C.c_int32)
+            inp.pool_from_logprob = _p(arr("pf", pool["pool_from_logprob"], np.uint8), C.c_uint8)
         if logits is not None:
             keep["logits"] = np.ascontiguousarray(logits)
             inp.logits = keep["logits"].ctypes.data_as(C.c_void_p)

@@ -11,7 +11,14 @@ steps); asking for no pool output decodes without one. Cases: random decodes
 (f32/f16/bf16, logits, EOS and extra EOS, min_length, banned tokens, n-gram
 blocking, repetition penalty, per-example steps, forced tokens), pools wider
 than a row's shortlist (every row rescanned), wide beams, the overlapped
-decode. Outputs are compared bit for bit, statuses and messages as text."""
+decode. Result handles keep each example's pool and its soft top-k
+inclusion weights (one example, batches, variable batches with per-example
+beams, model-step decodes; several temperatures, tolerances and iteration
+caps). The pool's gradients: relaxed-weight gradients of the result-handle
+backward (dense and sparse, with the initial scores'), pool score and
+raw-score gradients of the batch backward (log-probs and logits), and the
+pool trace's errors. Outputs are compared bit for bit, statuses and
+messages as text."""
 
 import os
 
@@ -272,3 +279,120 @@ def test_pool_model_step_decodes(libs, seed):
     same(ours, theirs, f"seed {seed}")
     for mode in our_logs:
         _logs_equal(our_logs[mode], their_logs[mode])
+
+
+# ---------------------------------------------------------------------------
+# Pool gradients: each pool entry's raw-score gradient joins its parent's
+# path after the step's selected children, and its log-prob entry
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("seed", range(12))
+def test_pool_result_backward(libs, seed):
+    """dbs_backward_dense / _sparse / _default / dbs_backward of a pooled
+    result with relaxed-weight gradients (alone, with selected-weight and
+    final-score gradients): the gradients and the initial scores'."""
+    import ctypes as C
+
+    from tests.host_abi import read_backward
+    from tests.test_gpu_host_results import same
+
+    case = make_case(47000 + seed, dtypes=["f32"], logits=False, allow_invalid=False)
+    kw = case["kw"]
+    K, T, V = case["K"], case["T"], case["V"]
+    m = [1, 2, 3][seed % 3]
+    x = np.ascontiguousarray(case["xin"][0])
+    rng = np.random.default_rng(seed)
+    P = K * m
+    grw = rng.normal(0, 1, T * P).astype(np.float32)
+    gw = rng.normal(0, 1, T * K).astype(np.float32)
+    gf = rng.normal(0, 1, K).astype(np.float32)
+    which = [(None, grw, None), (gw, grw, gf), (None, grw, gf), (gw, grw, None)][seed % 4]
+    opts = dict(beam_size=K, eos_token=kw["eos_token"], length_penalty_alpha=kw["alpha"],
+                min_length=kw["min_length"], relaxed_pool_multiplier=m, selected_temperature=0.7, **_soft(seed))
+
+    def run(lib, h):
+        L = lib.lib
+        r = C.c_void_p()
+        assert L.dbs_decode(h, x.ctypes.data_as(C.POINTER(C.c_float)), T, V, C.byref(r)) == 0, lib.error()
+        out = {}
+        f32 = C.POINTER(C.c_float)
+        ptr = [None if a is None else a.ctypes.data_as(f32) for a in which]
+        for name in ("dbs_backward_dense", "dbs_backward_sparse", "dbs_backward_default", "dbs_backward"):
+            b = C.c_void_p()
+            st = getattr(L, name)(h, r, ptr[0], ptr[1], ptr[2], C.byref(b))
+            out[name] = (st, lib.error(), read_backward(L, b, T * K * V, K) if st == 0 else None)
+            L.dbs_free_backward(b)
+        L.dbs_free_result(r)
+        return out
+
+    ours, theirs = _each(libs, opts, run, kw["extra_eos"])
+    same(ours, theirs, f"seed {seed} m {m}")
+    assert ours["dbs_backward_dense"][0] == 0
+
+
+def _pool_trace_case(libs, seed, logits, dtype):
+    case = make_case(48000 + seed, dtypes=[dtype], logits=logits, allow_invalid=False)
+    case["kw"]["banned_per_example"] = None
+    m = [1, 2, 4][seed % 3]
+    out = _check(libs, case, m)
+    return case, m, out
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_pool_batch_backward(libs, seed):
+    """dbs_backward_batch_into_ex with pool score and raw-score gradients
+    on a pooled decode's trace (log-probs, and logits with row_lse),
+    accumulating into a buffer with values; with and without the selected
+    slots' gradients."""
+    logits = seed % 2 == 1
+    dtype = ["f32", "bf16", "f16"][seed % 3]
+    case, m, out = _pool_trace_case(libs, seed, logits, dtype)
+    kw = case["kw"]
+    B, T, K, V = case["B"], case["T"], case["K"], case["V"]
+    P = K * m
+    rng = np.random.default_rng(seed)
+    init = rng.normal(size=(B, T, K, V)).astype(np.float32)
+    init[rng.random(init.shape) < 0.1] = -0.0
+    gps = rng.normal(size=(B, T, P)).astype(np.float32)
+    gpr = rng.normal(size=(B, T, P)).astype(np.float32)
+    gps[rng.random(gps.shape) < 0.2] = 0.0
+    runs = [dict(grad_pool_scores=gps), dict(grad_pool_raw=gpr, grad_final=rng.normal(size=(B, K)).astype(np.float32)),
+            dict(grad_pool_scores=gps, grad_pool_raw=gpr, grad_scores=rng.normal(size=(B, T, K)).astype(np.float32))]
+    pool = {k: out[k] for k in ("pool_parents", "pool_tokens", "pool_lengths", "pool_from_logprob")}
+    opts = dict(beam_size=K, eos_token=kw["eos_token"], length_penalty_alpha=kw["alpha"],
+                min_length=kw["min_length"], relaxed_pool_multiplier=m)
+    for run in runs:
+        extra = dict(logits=case["xin"], logits_dtype=dtype, row_lse=out["row_lse"]) if logits else {}
+
+        def fn(lib, h):
+            st, g = lib.backward(h, out, V, init, steps=kw["steps"], pool=pool, **extra, **run)
+            return st, g, lib.error()
+
+        (s0, g0, e0), (s1, g1, e1) = _each(libs, opts, fn)
+        assert (s0, e0) == (s1, e1), (sorted(run), e0, e1)
+        assert s0 == 0, e0
+        bad = np.argwhere(g0.view(np.uint32) != g1.view(np.uint32))
+        assert bad.size == 0, (sorted(run), tuple(bad[0]), g0[tuple(bad[0])], g1[tuple(bad[0])])
+
+
+def test_pool_trace_errors_match(libs):
+    """A pool trace out of range, and pool gradients without a pool trace,
+    give the reference's status and text."""
+    case, m, out = _pool_trace_case(libs, 3, False, "f32")
+    kw = case["kw"]
+    B, T, K, V = case["B"], case["T"], case["K"], case["V"]
+    init = np.zeros((B, T, K, V), np.float32)
+    pool = {k: np.array(out[k]) for k in ("pool_parents", "pool_tokens", "pool_lengths", "pool_from_logprob")}
+    bad_pool = dict(pool)
+    bad_pool["pool_tokens"] = pool["pool_tokens"].copy()
+    bad_pool["pool_tokens"][B - 1, 0, 0] = V
+    gps = np.ones((B, T, K * m), np.float32)
+    opts = dict(beam_size=K, eos_token=kw["eos_token"], length_penalty_alpha=kw["alpha"], relaxed_pool_multiplier=m)
+
+    def fn(lib, h):
+        got = [lib.backward(h, out, V, init, steps=kw["steps"], pool=bad_pool, grad_pool_scores=gps)[0], lib.error()]
+        got += [lib.backward(h, out, V, init, steps=kw["steps"], grad_pool_scores=gps)[0], lib.error()]
+        return got
+
+    ours, theirs = _each(libs, opts, fn)
+    assert ours == theirs and ours[0] == -1, (ours, theirs)
