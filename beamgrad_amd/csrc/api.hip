@@ -330,7 +330,8 @@ int decode_common(const void* inputs, int data_type, int from_logits, const DBSC
 int step_common(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                 const DBSCudaSearchOptions* options, const DBSCudaBeamState* state,
                 const DBSCudaDecodeOutputs* outputs, float* row_lse, void* workspace, int64_t workspace_bytes,
-                void* stream_ptr, const int32_t* forced = nullptr, const PoolOutputs* pool = nullptr) {
+                void* stream_ptr, const int32_t* forced = nullptr, const PoolOutputs* pool = nullptr,
+                const uint8_t* row_mask = nullptr) {
     if (!inputs || !valid_dtype(data_type) || !valid_args(args) || !state || !outputs)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!valid_options(options, *args)) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
@@ -344,8 +345,9 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
     const int pool_mult = pool ? pool->mult : 0;
     if (pool_mult < 0 || static_cast<int64_t>(pool_mult) * a.beam_size > DBS_CUDA_MAX_BEAM)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
-    const DecodeLayout L = decode_layout(a.batch_size, 1, a.beam_size, a.vocab_size, cons, true, state->prefix_stride,
-                                         pool_mult * a.beam_size);
+    DecodeLayout L = decode_layout(a.batch_size, 1, a.beam_size, a.vocab_size, cons, true, state->prefix_stride,
+                                   pool_mult * a.beam_size);
+    if (row_mask) L.M = 0;  // filtered rows are read in full
     bool too_small = false;
     Scratch scratch;
     hipError_t e = scratch.acquire(workspace, workspace_bytes, L.total, stream, &too_small);
@@ -374,6 +376,7 @@ int step_common(const void* inputs, int data_type, int from_logits, const DBSCud
     p.use_tau = 0;
     p.banned = a.banned_tokens;
     p.forced = forced;
+    p.row_mask = row_mask;
     set_pool(p, pool);
     p.rowinfo = reinterpret_cast<RowInfo*>(ws + L.off_rowinfo);
     p.shortlist = reinterpret_cast<ShortEntry*>(ws + L.off_short);
@@ -477,10 +480,11 @@ int decode_for_host(const void* inputs, int data_type, int from_logits, const DB
 
 int step_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                   const DBSCudaSearchOptions* options, const DBSCudaBeamState* state,
-                  const DBSCudaDecodeOutputs* outputs, const int32_t* forced, const PoolOutputs* pool,
-                  void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-    return step_common(inputs, data_type, from_logits, args, options, state, outputs, nullptr, workspace,
-                       workspace_bytes, stream, forced, pool);
+                  const DBSCudaDecodeOutputs* outputs, float* row_lse, const int32_t* forced,
+                  const PoolOutputs* pool, const uint8_t* row_mask, void* workspace, int64_t workspace_bytes,
+                  hipStream_t stream) {
+    return step_common(inputs, data_type, from_logits, args, options, state, outputs, row_lse, workspace,
+                       workspace_bytes, stream, forced, pool, row_mask);
 }
 
 int64_t workspace_for_host(const DBSCudaDecodeArgs* args, int pool_mult, int step_mode, int prefix_stride) {

@@ -85,6 +85,10 @@ struct DecodeParams {
     // device [B, T] (step mode: [B]) or null: an entry >= 0 is the one token
     // a read beam may take at that step (reference src/decoder.cpp:125)
     const int32_t* forced;
+    // step mode, device [B, K, V] or null: 1 where a token filter refused
+    // the token for that row (reference src/decoder.cpp:259-282); every read
+    // row is then read in full by the select pass (no shortlists)
+    const uint8_t* row_mask;
     // Relaxed pool (reference src/decoder.cpp:40, 294-306): with pool_mult
     // m >= 1 each step keeps the best m * beams candidates of an example, its
     // pool, of which the first beams are the selection. Outputs [B, T, m * K]

@@ -506,10 +506,11 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
     }
     if (cons && (!(rep > 0.0f) || !std::isfinite(rep)))
         example_error(0, "repetition_penalty must be finite and positive (1 disables it)");
-    // What the GPU engine does not serve.
-    need(!(cons && cons->token_filter), "token_filter callbacks are not served by libdbs_hip (the HIP engine)");
-
-    DecodeJob j;
+    if (cons && cons->token_filter) {
+        check_engine_limits(h, K, V);
+        decode_batch_filtered(h, inputs, data_type, from_logits, B, T, V, steps_b, cons, out, ex);
+    } else {
+        DecodeJob j;
     j.inputs = inputs;
     j.data_type = data_type;
     j.from_logits = from_logits;
@@ -543,6 +544,7 @@ void decode_batch(DBSDecoderHandle* h, const void* inputs, int data_type, bool f
         j.pool_from_logprob = ex->pool_from_logprob;
     }
     run_decode(h, j);
+    }
     const int64_t selected = static_cast<int64_t>(B) * static_cast<int64_t>(trace);
     {
         std::lock_guard<std::mutex> lock(h->stats_mutex);

@@ -30,7 +30,7 @@ enum Slot : int {
     kInputs, kBanned, kBannedPe, kSteps, kBeams, kEos, kMinLengths, kFinalScores, kFinalRaw, kFinalLengths, kTokens,
     kParents, kLengths, kScores, kRawScores, kFromLogprob, kRowLse, kFirstInvalid, kWorkspace, kGradFinal,
     kGradFinalRaw, kGradScores, kGradRaw, kDraws, kDense, kState, kForced, kPoolParents, kPoolTokens,
-    kPoolLengths, kPoolScores, kPoolRaw, kPoolFromLogprob, kPoolD, kSlotCount
+    kPoolLengths, kPoolScores, kPoolRaw, kPoolFromLogprob, kPoolD, kRowMask, kSlotCount
 };
 
 struct Arena {
@@ -212,6 +212,14 @@ struct DecodeJob {
     uint8_t* pool_from_logprob = nullptr;
 };
 void run_decode(DBSDecoderHandle* h, const DecodeJob& job);
+
+// dbs_decode_batch_into(_ex) with a token filter (host_results.cpp): each
+// example decoded step by step on the device step API, the filter's
+// verdicts for each step's rows asked on the host in the reference's call
+// order (reference src/decoder.cpp:259-282).
+void decode_batch_filtered(DBSDecoderHandle* h, const void* inputs, int data_type, bool from_logits, int B, int T,
+                           int V, const std::vector<int32_t>& steps_b, const DBSAdvancedConstraintsC* cons,
+                           const DBSDecodeOutputsC* out, const DBSDecodeOutputsExC* ex);
 
 // The relaxed pool's size for beam K and multiplier m (reference
 // src/decoder.cpp:410-416), refused past what the HIP engine keeps per step.

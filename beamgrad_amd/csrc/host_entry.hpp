@@ -59,13 +59,16 @@ int decode_for_host(const void* inputs, int data_type, int from_logits, const DB
                     const int32_t* forced, const PoolOutputs* pool, void* workspace, int64_t workspace_bytes,
                     hipStream_t stream, int32_t** fault);
 
-// dbs_cuda_decode_step_ex2 with forced (device int32 [B] or null): an entry
-// >= 0 (and < V) is the one token a read beam of example b may take at this
-// step; and a relaxed pool (null: none). Returns a DBS_CUDA_STATUS_*.
+// dbs_cuda_decode_step_ex2 (row_lse: device [B, K] or null) with forced
+// (device int32 [B] or null): an entry >= 0 (and < V) is the one token a
+// read beam of example b may take at this step; a relaxed pool (null:
+// none); and row_mask (device [B, K, V] or null): 1 where a token filter
+// refused the token for that row. Returns a DBS_CUDA_STATUS_*.
 int step_for_host(const void* inputs, int data_type, int from_logits, const DBSCudaDecodeArgs* args,
                   const DBSCudaSearchOptions* options, const DBSCudaBeamState* state,
-                  const DBSCudaDecodeOutputs* outputs, const int32_t* forced, const PoolOutputs* pool,
-                  void* workspace, int64_t workspace_bytes, hipStream_t stream);
+                  const DBSCudaDecodeOutputs* outputs, float* row_lse, const int32_t* forced,
+                  const PoolOutputs* pool, const uint8_t* row_mask, void* workspace, int64_t workspace_bytes,
+                  hipStream_t stream);
 
 // The per-slot path gradients draws [B, T, K] of the surrogate backward for
 // every gradient input of `in` (final scores, final raw scores, scores, raw

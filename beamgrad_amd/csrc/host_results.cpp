@@ -199,6 +199,9 @@ struct Constraints {
     float repetition_penalty = 1.0f;
     int ngram = 0;
     bool filter = false;
+    DBSTokenFilterFn filter_fn = nullptr;
+    void* filter_user = nullptr;
+    int batch_index = 0;
 };
 
 Constraints constraints_of(const DBSAdvancedConstraintsC* c) {
@@ -210,6 +213,9 @@ Constraints constraints_of(const DBSAdvancedConstraintsC* c) {
     out.repetition_penalty = c->repetition_penalty > 0.0f ? c->repetition_penalty : 1.0f;
     out.ngram = c->no_repeat_ngram_size;
     out.filter = c->token_filter != nullptr;
+    out.filter_fn = c->token_filter;
+    out.filter_user = c->token_filter_user_data;
+    out.batch_index = c->batch_index;
     return out;
 }
 
@@ -231,10 +237,75 @@ void check_decode_args(const DBSDecoderHandle& h, int K, int eos, int steps, int
     (void)mul(selected, static_cast<size_t>(V), "log-prob tensor size overflow");
 }
 
+// The token filter's verdicts for step t (reference src/decoder.cpp:
+// 131-167, 196-282, in its call order): for each read beam in order (a
+// finite score, not a finished beam carried; from logits, a row with a
+// finite entry), each token in order that passes the forced, banned,
+// minimum-length and n-gram checks goes to the filter with the beam's
+// prefix (prefix [K, stride], len[k] tokens each); mask[k * V + v] = 1
+// where the filter refused it. With validate_inputs, a read row holding NaN
+// or +inf raises where the reference's scan raises: from logits before the
+// row's calls, from log-probs after them.
+void filter_step(const DBSDecoderHandle& h, const Constraints& c, int t, int V, bool from_logits, const float* rows,
+                 const std::vector<float>& raw, const std::vector<uint8_t>& finished,
+                 const std::vector<int32_t>& len, const std::vector<int32_t>& prefix, int stride, int min_length,
+                 std::vector<uint8_t>& mask) {
+    const int K = h.beam_size, eos = h.eos_token;
+    auto is_eos = [&](int v) {
+        if (eos < 0) return false;
+        return v == eos || std::find(h.extra_eos.begin(), h.extra_eos.end(), v) != h.extra_eos.end();
+    };
+    const int forced = c.forced ? c.forced[t] : -1;
+    mask.assign(static_cast<size_t>(K) * V, 0);
+    std::vector<uint8_t> blocked(static_cast<size_t>(V));
+    const auto where = [&](int k) { return " (step " + std::to_string(t) + ", beam " + std::to_string(k) + ")"; };
+    for (int k = 0; k < K; ++k) {
+        const size_t ki = static_cast<size_t>(k);
+        if (!std::isfinite(raw[ki]) || (eos >= 0 && finished[ki])) continue;
+        const float* row = rows + ki * static_cast<size_t>(V);
+        bool invalid = false, finite = false;
+        for (int v = 0; v < V; ++v) {
+            if (!(row[v] < std::numeric_limits<float>::infinity())) invalid = true;
+            else if (row[v] > kNegInf) finite = true;
+        }
+        if (from_logits) {
+            if (invalid && h.validate) throw std::invalid_argument("logits contain NaN or +inf" + where(k));
+            if (!finite) continue;  // no finite logit: the row is not scanned
+        }
+        const int L = len[ki];
+        const int32_t* pre = prefix.data() + ki * static_cast<size_t>(stride);
+        std::fill(blocked.begin(), blocked.end(), 0);
+        const int n = c.ngram;
+        auto block = [&](int32_t tok) {
+            if (tok >= 0 && tok < V) blocked[static_cast<size_t>(tok)] = 1;
+        };
+        if (n == 1) {
+            for (int i = 0; i < L; ++i) block(pre[i]);
+        } else if (n > 1 && L >= n - 1) {
+            const int tail = L - (n - 1);
+            for (int i = 0; i + n <= L; ++i) {
+                bool same = true;
+                for (int j = 0; j < n - 1 && same; ++j) same = pre[i + j] == pre[tail + j];
+                if (same) block(pre[i + n - 1]);
+            }
+        }
+        const bool mask_eos = L + 1 < min_length;
+        for (int v = 0; v < V; ++v) {
+            if (forced >= 0 && v != forced) continue;
+            if (c.banned && c.banned[v]) continue;
+            if (mask_eos && is_eos(v)) continue;
+            if (blocked[static_cast<size_t>(v)]) continue;
+            if (c.filter_fn(c.filter_user, c.batch_index, t, k, L > 0 ? pre : nullptr, L, v) == 0)
+                mask[ki * static_cast<size_t>(V) + static_cast<size_t>(v)] = 1;
+        }
+        if (!from_logits && invalid && h.validate) throw std::invalid_argument("log_probs contains NaN or +inf" + where(k));
+    }
+}
+
 // What the HIP engine does not serve, after the reference's own checks.
 void check_served(const DBSDecoderHandle& h, const Constraints* c) {
     (void)h;
-    if (c) need(!c->filter, "token_filter callbacks are not served by libdbs_hip (the HIP engine)");
+    (void)c;
 }
 
 // Host copies of a decode's relaxed pool [B, T, mult * Kmax].
@@ -403,9 +474,17 @@ struct StepView {
 // the state (raw scores, lengths, finished flags and token prefixes) stays
 // on the device between steps, each step's rows (pre-filled with -inf) are
 // copied in and its selection copied back.
+// How a step-by-step decode reads its rows: from logits (row_lse: host
+// [steps, K] or null, 0 for rows not read).
+struct StepRows {
+    bool from_logits = false;
+    float* row_lse = nullptr;
+    int32_t* final_lengths = nullptr;  // host [K] or null
+};
+
 template <class Fill>
 DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const Constraints* c, Fill&& fill,
-                                   int64_t* rows_bytes) {
+                                   int64_t* rows_bytes, const StepRows& how = StepRows{}) {
     const int K = h.beam_size;
     check_decode_args(h, K, h.eos_token, steps, V, c);
     check_served(h, c);
@@ -443,7 +522,9 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
     std::vector<float> rows;
 
     const int min_length = c && c->min_length >= 0 ? c->min_length : h.min_length;
-    const bool constrained = c && (c->ngram > 0 || c->repetition_penalty > 1.0f);
+    // full prefixes: for the constraints, and for a token filter's calls
+    const bool constrained = c && (c->ngram > 0 || c->repetition_penalty > 1.0f || c->filter);
+    std::vector<uint8_t> filter_mask;
     DBSCudaDecodeArgs a{};
     a.batch_size = 1;
     a.steps = 1;
@@ -487,6 +568,9 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
                       view_prefix.data()};
         rows.assign(row_block, kNegInf);
         fill(view, rows.data());
+        if (c && c->filter)
+            filter_step(h, *c, t, V, how.from_logits, rows.data(), raw, finished, len, search_prefix, steps,
+                        min_length, filter_mask);
 
         std::vector<int32_t> out_tok(static_cast<size_t>(K)), out_par(static_cast<size_t>(K));
         std::vector<float> out_score(static_cast<size_t>(K));
@@ -537,9 +621,14 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
                 pool.raw_scores = static_cast<float*>(h.arena.get(kPoolRaw, 4 * static_cast<size_t>(P)));
                 pool.from_logprob = static_cast<uint8_t*>(h.arena.get(kPoolFromLogprob, static_cast<size_t>(P)));
             }
-            engine_check(dbs_hip::step_for_host(rows_d, DBS_CUDA_DTYPE_F32, 0, &a, &opts, &bs, &o, forced_d,
-                                                P > 0 ? &pool : nullptr, ws, ws_bytes, st),
+            const uint8_t* mask_d =
+                c && c->filter ? upload(&h, kRowMask, filter_mask.data(), filter_mask.size(), st) : nullptr;
+            float* lse_d = how.row_lse ? static_cast<float*>(h.arena.get(kRowLse, 4 * static_cast<size_t>(K))) : nullptr;
+            engine_check(dbs_hip::step_for_host(rows_d, DBS_CUDA_DTYPE_F32, how.from_logits ? 1 : 0, &a, &opts, &bs,
+                                                &o, lse_d, forced_d, P > 0 ? &pool : nullptr, mask_d, ws, ws_bytes,
+                                                st),
                          "HIP decode step");
+            if (lse_d) download(how.row_lse + static_cast<size_t>(t) * K, lse_d, static_cast<size_t>(K), st);
             if (P > 0) {
                 download(pool_par.data(), pool.parents, pool_par.size(), st);
                 download(pool_tok.data(), pool.tokens, pool_tok.size(), st);
@@ -567,8 +656,10 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
                 const float* row = rows.data() + static_cast<size_t>(k) * V;
                 for (int v = 0; v < V; ++v) {
                     if (!(row[v] < std::numeric_limits<float>::infinity()))
-                        throw std::invalid_argument("log_probs contains NaN or +inf (step " + std::to_string(t) +
-                                                    ", beam " + std::to_string(k) + ")");
+                        throw std::invalid_argument(std::string(how.from_logits ? "logits contain NaN or +inf"
+                                                                                : "log_probs contains NaN or +inf") +
+                                                    " (step " + std::to_string(t) + ", beam " + std::to_string(k) +
+                                                    ")");
                 }
             }
         }
@@ -614,6 +705,7 @@ DBSResultHandle decode_model_steps(DBSDecoderHandle& h, int steps, int V, const 
         const int l = std::max(1, static_cast<int>(len[i]));
         r.final_scores[i] = raw[i] / dbs_hip::length_penalty(l, h.alpha);
         r.final_raw_scores[i] = raw[i];
+        if (how.final_lengths) how.final_lengths[i] = len[i];
     }
     *rows_bytes = static_cast<int64_t>(rows.capacity() * sizeof(float));
     return r;
@@ -738,6 +830,85 @@ bool cpu_has(const char* feature) {
 
 }  // namespace
 
+namespace dbs_host {
+
+void decode_batch_filtered(DBSDecoderHandle* hp, const void* inputs, int data_type, bool from_logits, int B, int T,
+                           int V, const std::vector<int32_t>& steps_b, const DBSAdvancedConstraintsC* cons,
+                           const DBSDecodeOutputsC* out, const DBSDecodeOutputsExC* ex) {
+    DBSDecoderHandle& h = *hp;
+    const int K = h.beam_size;
+    const size_t block = static_cast<size_t>(K) * static_cast<size_t>(V);
+    const size_t esize = dtype_bytes(data_type);
+    const int P = ex && (ex->pool_parents || ex->pool_tokens || ex->pool_lengths || ex->pool_scores ||
+                         ex->pool_raw_scores || ex->pool_from_logprob)
+                      ? pool_size_of(K, h.pool_multiplier)
+                      : 0;
+    std::vector<float> lse;
+    std::vector<int32_t> final_len(static_cast<size_t>(K));
+    for (int b = 0; b < B; ++b) {
+        const int steps = steps_b[static_cast<size_t>(b)];
+        Constraints c = constraints_of(cons);
+        c.batch_index = b;  // reference src/c_api.cpp:782-786
+        const unsigned char* x = static_cast<const unsigned char*>(inputs) + static_cast<size_t>(b) * T * block * esize;
+        StepRows how;
+        how.from_logits = from_logits;
+        lse.assign(static_cast<size_t>(steps) * K, 0.0f);
+        how.row_lse = ex && ex->row_lse && from_logits ? lse.data() : nullptr;
+        how.final_lengths = final_len.data();
+        int64_t rows_bytes = 0;
+        DBSResultHandle r;
+        try {
+            r = decode_model_steps(
+                h, steps, V, &c,
+                [&](const StepView& v, float* rows) {
+                    const unsigned char* src = x + static_cast<size_t>(v.step) * block * esize;
+                    if (data_type == DBS_DTYPE_F32) {
+                        std::memcpy(rows, src, block * sizeof(float));
+                        return;
+                    }
+                    const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src);
+                    for (size_t i = 0; i < block; ++i)
+                        rows[i] = data_type == DBS_DTYPE_F16 ? dbs_hip::half_to_f32(s16[i]) : dbs_hip::bf16_to_f32(s16[i]);
+                },
+                &rows_bytes, how);
+        } catch (const std::invalid_argument& e) {
+            example_error(b, e.what());
+        }
+        // the example's trace, padded past its steps (reference src/c_api.cpp:739-781)
+        for (int t = 0; t < T; ++t) {
+            for (int k = 0; k < K; ++k) {
+                const size_t o = (static_cast<size_t>(b) * T + t) * K + k, i = static_cast<size_t>(t) * K + k;
+                const bool live = t < steps;
+                if (out->tokens) out->tokens[o] = live ? r.tokens[i] : -1;
+                if (out->parents) out->parents[o] = live ? r.parents[i] : -1;
+                if (out->lengths) out->lengths[o] = live ? r.lengths[i] : 0;
+                if (out->scores) out->scores[o] = live ? r.scores[i] : kNegInf;
+                if (out->raw_scores) out->raw_scores[o] = live ? r.raw_scores[i] : kNegInf;
+                if (out->from_logprob) out->from_logprob[o] = live ? r.from_logprob[i] : 0;
+                if (ex && ex->row_lse) ex->row_lse[o] = live && how.row_lse ? lse[i] : 0.0f;
+            }
+            for (int q = 0; q < P; ++q) {
+                const size_t o = (static_cast<size_t>(b) * T + t) * P + q, i = static_cast<size_t>(t) * P + q;
+                const bool live = t < steps;
+                if (ex->pool_parents) ex->pool_parents[o] = live ? r.pool_parents[i] : -1;
+                if (ex->pool_tokens) ex->pool_tokens[o] = live ? r.pool_tokens[i] : -1;
+                if (ex->pool_lengths) ex->pool_lengths[o] = live ? r.pool_lengths[i] : 0;
+                if (ex->pool_scores) ex->pool_scores[o] = live ? r.pool_scores[i] : kNegInf;
+                if (ex->pool_raw_scores) ex->pool_raw_scores[o] = live ? r.pool_raw_scores[i] : kNegInf;
+                if (ex->pool_from_logprob) ex->pool_from_logprob[o] = live ? r.pool_from_logprob[i] : 0;
+            }
+        }
+        for (int k = 0; k < K; ++k) {
+            const size_t o = static_cast<size_t>(b) * K + k;
+            out->final_scores[o] = r.final_scores[static_cast<size_t>(k)];
+            if (out->final_raw_scores) out->final_raw_scores[o] = r.final_raw_scores[static_cast<size_t>(k)];
+            if (out->final_lengths) out->final_lengths[o] = final_len[static_cast<size_t>(k)];
+        }
+    }
+}
+
+}  // namespace dbs_host
+
 extern "C" {
 
 // ---- decodes into result handles (reference src/c_api.cpp:402-700) ----
@@ -754,6 +925,20 @@ DBS_EXPORT int dbs_decode_constrained_ex(DBSDecoderHandle* handle, const float* 
         need(log_probs != nullptr, "log_probs cannot be null");
         check_decode_args(h, h.beam_size, h.eos_token, steps, vocab_size, cp);
         check_served(h, cp);
+        if (cp && cp->filter) {
+            // a token filter: step by step, its verdicts from the host
+            const size_t block = static_cast<size_t>(h.beam_size) * static_cast<size_t>(vocab_size);
+            int64_t rows_bytes = 0;
+            auto r = std::make_unique<DBSResultHandle>(decode_model_steps(
+                h, steps, vocab_size, cp,
+                [&](const StepView& v, float* rows) {
+                    std::copy_n(log_probs + static_cast<size_t>(v.step) * block, block, rows);
+                },
+                &rows_bytes));
+            record_result_stats(h, *r, ns_since(start), false);
+            *out_result = r.release();
+            return;
+        }
         BatchSpec s;
         s.inputs = log_probs;
         s.B = 1;
@@ -969,7 +1154,8 @@ DBS_EXPORT int dbs_decode_model_steps_ex(DBSDecoderHandle* handle, DBSModelStepE
         need(out_result != nullptr, "out_result cannot be null");
         DBSDecoderHandle& h = handle_of(handle);
         const auto start = std::chrono::steady_clock::now();
-        const Constraints c = constraints_of(constraints);
+        Constraints c = constraints_of(constraints);
+        c.batch_index = batch_index;  // what a token filter is told (reference src/c_api.cpp:592-596)
         int64_t rows_bytes = 0;
         DBSResultHandle r = decode_model_steps(h, steps, vocab_size, constraints ? &c : nullptr,
                                                [&](const StepView& v, float* rows) {

@@ -473,6 +473,7 @@ __device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State&
             const Cand c0{raw0 * inv_pen, raw0, k, v, new_len, 1};
             if (before(thr, c0)) continue;  // penalties only lower a candidate
             if (static_masked(p, b, v, mask_eos)) continue;
+            if (p.row_mask && gload(p.row_mask, row * V + v)) continue;
             Cand c;
             if (!make_cand(p, s, pre, k, praw, inv_pen, v, new_len, lp, c)) continue;
             if (before(thr, c)) continue;
@@ -496,7 +497,8 @@ __device__ __forceinline__ void rescan_row(const DecodeParams& p, Lds& s, State&
         if (v < V) {
             const float x = load_one<DT>(base, v);
             const float lp = LOGITS ? x - lse : x;
-            if ((lp < kInf) && lp != -kInf && !static_masked(p, b, v, mask_eos)) {
+            if ((lp < kInf) && lp != -kInf && !static_masked(p, b, v, mask_eos) &&
+                !(p.row_mask && gload(p.row_mask, row * V + v))) {
                 Cand c;
                 if (make_cand(p, s, pre, k, praw, inv_pen, v, new_len, lp, c)) offer(s, st, c);
             }
@@ -915,6 +917,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(DecodeParams p, 
                 const float lp = LOGITS ? x - s.nraw[k] : x;
                 const int new_len = s.len[k] + 1;
                 if (!(lp < kInf) || lp == -kInf || static_masked(p, b, forced, new_len < min_length_of(p, b))) continue;
+                if (p.row_mask && gload(p.row_mask, row * p.V + forced)) continue;
                 Cand c;
                 if (make_cand(p, s, prefix_of(p, s, b, k, cur), k, s.raw[k], inv_of(s, pen_len, new_len, p.alpha),
                               forced, new_len, lp, c))

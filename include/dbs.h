@@ -22,8 +22,10 @@
  *
  * All 81 functions of the reference's ABI are exported. What the GPU engine
  * does not serve is refused with DBS_ERROR_INVALID_ARGUMENT and a message
- * naming it: token-filter callbacks and pools of more than 1024
- * candidates. The relaxed pool is served: the pool outputs of the batch
+ * naming it: only what is beyond the engine's sizes (pools of more than
+ * 1024 candidates, beams above 1024). Token-filter callbacks are served: a
+ * decode with a filter runs step by step on the device, the filter asked on
+ * the host in the reference's call order. The relaxed pool is served: the pool outputs of the batch
  * decodes into caller arrays, the pool and soft top-k inclusion weights of
  * result handles, and the pool's gradients (grad_relaxed_weights,
  * grad_pool_scores, grad_pool_raw_scores). Forced tokens (an entry >= 0: the one token a read beam may take at that
@@ -118,9 +120,10 @@ typedef struct DBSModelStepInfoC {
  * (reference include/dbs.h:123-127). */
 typedef int (*DBSModelStepExFn)(void* user_data, const DBSModelStepInfoC* info, float* out_log_probs);
 
-/* Token filter callback of the reference (reference include/dbs.h:129-137).
- * Declared for the layout of DBSAdvancedConstraintsC; a non-NULL filter is
- * rejected here (a per-candidate host callback has no place in a GPU scan). */
+/* Token filter callback of the reference (reference include/dbs.h:129-137):
+ * called for each read beam in order and each token in order that passes
+ * the forced, banned, minimum-length and n-gram checks, with the beam's
+ * prefix; 0 refuses the token. */
 typedef int (*DBSTokenFilterFn)(
     void* user_data,
     int batch_index,
@@ -131,14 +134,14 @@ typedef int (*DBSTokenFilterFn)(
     int token);
 
 /* Constraints shared by every example of a batch (reference
- * include/dbs.h:139-148). token_filter must be NULL here. */
+ * include/dbs.h:139-148). */
 typedef struct DBSAdvancedConstraintsC {
     const uint8_t* banned_tokens;        /* [V] or NULL: non-zero bans the token */
     const int32_t* forced_tokens;        /* [T] or NULL: an entry >= 0 (< V) forces that token at step t */
     int min_length;                      /* negative: the handle's min_length */
     float repetition_penalty;            /* <= 1 disables; 0 (zero-initialised) means 1 */
     int no_repeat_ngram_size;            /* <= 0 disables */
-    DBSTokenFilterFn token_filter;       /* must be NULL */
+    DBSTokenFilterFn token_filter;       /* NULL, or a filter (batch decodes: told the example's index) */
     void* token_filter_user_data;
     int batch_index;                     /* ignored by the batch functions */
 } DBSAdvancedConstraintsC;

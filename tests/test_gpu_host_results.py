@@ -435,18 +435,16 @@ def test_result_errors_match_the_reference(libs):
 
 def test_refusals_name_what_is_not_served(libs):
     """What the HIP engine does not serve is refused with a message naming
-    it (the reference computes these)."""
+    it (the reference computes these): a relaxed pool of more than 1024
+    candidates."""
     ours = libs[0]
     L = ours.lib
-    T, K, V = 3, 2, 10
+    T, K, V = 2, 300, 10
     x = np.ascontiguousarray(log_softmax(np.zeros((T, K, V), np.float32)))
     r = C.c_void_p()
-    h = ours.create(beam_size=K)
-    keep = {}
-    c = HostLib.constraints(keep=keep)
-    c.token_filter = C.c_void_p(1)
-    assert L.dbs_decode_constrained_ex(h, _p(x, C.c_float), T, V, C.byref(c), C.byref(r)) == -1
-    assert "token_filter callbacks are not served" in ours.error()
+    h = ours.create(beam_size=K, relaxed_pool_multiplier=4)
+    assert L.dbs_decode(h, _p(x, C.c_float), T, V, C.byref(r)) == -1
+    assert "relaxed pool of 1200 candidates" in ours.error()
     ours.destroy(h)
 
 

@@ -306,21 +306,9 @@ def test_backward_argument_errors_match(ours, ref):
 
 
 def test_features_the_engine_does_not_serve_are_refused(ours):
-    """Token filters, relaxed pools and beams beyond the device ABI's limits
-    are refused with INVALID_ARGUMENT before any device work (the
-    reference's CPU library serves them)."""
-    import ctypes as C
-
-    x = np.zeros((1, 2, 2, 5), np.float32)
-    h = ours.create(beam_size=2, relaxed_pool_multiplier=2)
-    try:
-        keep = {}
-        cons = HostLib.constraints(keep=keep)
-        cons.token_filter = C.c_void_p(1)
-        st, _ = ours.decode(h, x, 2, constraints=cons)
-        assert st == -1 and "token_filter" in ours.error()
-    finally:
-        ours.destroy(h)
+    """Relaxed pools and beams beyond the device ABI's limits are refused
+    with INVALID_ARGUMENT before any device work (the reference's CPU
+    library serves them)."""
     h = ours.create(beam_size=300, relaxed_pool_multiplier=4)
     try:
         st, _ = ours.decode(h, np.zeros((1, 1, 300, 3), np.float32), 300, pool=1200)
