@@ -12,6 +12,10 @@
 namespace dbs_hip {
 
 constexpr int kLutHalf = 4096;  // bfloat16 term-table slots per sign
+// Cache policy of the row passes' streamed row loads: nt (non-temporal).
+// Every row is read once per pass; on MI355X a read-only stream of 16-byte
+// loads reaches 6.6 TB/s with it against 5.9 TB/s without.
+constexpr int kRowLoadPolicy = 2;
 
 typedef short v2i16 __attribute__((ext_vector_type(2)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));

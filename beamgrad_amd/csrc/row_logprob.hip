@@ -83,7 +83,7 @@ __device__ __forceinline__ int load_row(const DecodeParams& p, int64_t r, bool v
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(a0 - lead), 0, 16 * nblk, 0x00020000);
 #pragma unroll
-    for (int c = C0; c < C1; ++c) d[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * tid, 4096 * c, 0);
+    for (int c = C0; c < C1; ++c) d[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * tid, 4096 * c, kRowLoadPolicy);
     return lead / esz;
 }
 

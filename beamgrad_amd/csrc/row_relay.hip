@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kRlThreads) void row_relay_kernel(DecodeParams p, i
         return row_buffer(rrow + 256 * s_begin, seg_bytes);
     };
     auto issue_chunk = [&](const __amdgpu_buffer_rsrc_t& rs, int voff, int c) __attribute__((always_inline)) {
-        const v4u32 q = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 4096 * c, 0);
+        const v4u32 q = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 4096 * c, kRowLoadPolicy);
         reg[4 * c] = q.x;
         reg[4 * c + 1] = q.y;
         reg[4 * c + 2] = q.z;
