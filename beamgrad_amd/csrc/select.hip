@@ -1725,26 +1725,46 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
             return ok ? Cand{r * ik, r, k, e.token, nlk, 1} : dead;
         };
         if (ncand <= 64) {
-            // one candidate per lane, ranked by the count of those before it
-            for (int i = 0; i < ns; ++i) {
-                const ShortEntry e = s_sl[lane * M + i];
+            // one candidate per lane, ranked by the count of those before it:
+            // lane L < nsurv takes survivor L (of beam k, the last beam whose
+            // survivors start at or before L), read from the shortlist;
+            // lanes [nsurv, ncand) take the carried beams in beam order
+            const int excl = incl - ns;
+            int k = 0;
+            for (int kk = 1; kk < K; ++kk)
+                if (lane >= __builtin_amdgcn_readlane(excl, kk)) k = kk;
+            const int ik0 = lane - __shfl(excl, k);
+            const ShortEntry e = s_sl[k * M + (lane < nsurv ? ik0 : 0)];
+            const float rk = __shfl(raw, k), ivk = __shfl(inv, k);
+            const int nlk = __shfl(new_len, k);
+            Cand c = dead;
+            if (lane < nsurv) {
                 if constexpr (CON) {
                     // the log-prob in the score field: the constraints are
                     // applied below, one candidate per lane
-                    s_cand[incl - ns + i] = Cand{e.lp, 0.0f, lane, e.token, new_len, 1};
+                    c = Cand{e.lp, 0.0f, k, e.token, nlk, 1};
                 } else {
-                    const float r = raw + e.lp;
-                    s_cand[incl - ns + i] = Cand{r * inv, r, lane, e.token, new_len, 1};
+                    const float r = rk + e.lp;
+                    c = Cand{r * ivk, r, k, e.token, nlk, 1};
                 }
             }
-            if (carried) {
-                const int slot = nsurv + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
-                                             static_cast<uint32_t>(carried_m >> 32),
-                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(carried_m), 0u)));
-                s_cand[slot] = carry;
+            if (carried_m != 0) {
+                // the (lane - nsurv)-th carried beam
+                int src = 0, seen = 0;
+                for (int kk = 0; kk < K; ++kk) {
+                    if (((carried_m >> kk) & 1ull) == 0) continue;
+                    if (seen == lane - nsurv) src = kk;
+                    ++seen;
+                }
+                Cand cb;
+                cb.score = bits_f32(static_cast<uint32_t>(__shfl(static_cast<int>(f32_bits(carry.score)), src)));
+                cb.raw = bits_f32(static_cast<uint32_t>(__shfl(static_cast<int>(f32_bits(carry.raw)), src)));
+                cb.parent = __shfl(carry.parent, src);
+                cb.token = __shfl(carry.token, src);
+                cb.length = __shfl(carry.length, src);
+                cb.flp = __shfl(carry.flp, src);
+                if (lane >= nsurv && lane < ncand) c = cb;
             }
-            wave_sync();
-            Cand c = lane < ncand ? s_cand[lane] : dead;
             if constexpr (CON) {
                 const bool surv = lane < nsurv;  // (the carried-forward beams follow the survivors)
                 const int k = surv ? c.parent : 0;
@@ -1786,10 +1806,18 @@ __global__ __launch_bounds__(64 * kNarrowWaves) void select_narrow_kernel(Decode
             }
             nsel = static_cast<int>(__popcll(__builtin_amdgcn_ballot_w64(valid)));
             nsel = nsel < Kb ? nsel : Kb;
-            wave_sync();
-            if (valid && rank < Kb) s_cand[rank] = c;
-            wave_sync();
-            if (lane < nsel) sel = s_cand[lane];
+            // each selected candidate to the lane of its rank (lanes not
+            // selected write lane 63, which holds no selection: Kb <= 16)
+            const int to = 4 * ((valid && rank < Kb) ? rank : 63);
+            Cand sc;
+            sc.score = bits_f32(static_cast<uint32_t>(__builtin_amdgcn_ds_permute(to, static_cast<int>(f32_bits(c.score)))));
+            sc.raw = bits_f32(static_cast<uint32_t>(__builtin_amdgcn_ds_permute(to, static_cast<int>(f32_bits(c.raw)))));
+            sc.parent = __builtin_amdgcn_ds_permute(to, c.parent);
+            sc.token = __builtin_amdgcn_ds_permute(to, c.token);
+            sc.length = __builtin_amdgcn_ds_permute(to, c.length);
+            sc.flp = __builtin_amdgcn_ds_permute(to, c.flp);
+            if (lane < nsel) sel = sc;
+            wave_sync();  // the keys' LDS may be reused
         } else {
             Cand thr = dead;
             for (int s0 = 0; s0 < nsurv; s0 += 64) {
