@@ -109,6 +109,7 @@ SIGNATURES = {
     "dbs_hip_decode_ex4": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.POINTER(DecodeArgs), C.POINTER(SearchOptions),
                                      C.c_void_p, C.POINTER(DecodeOutputs), C.c_void_p, C.c_void_p, C.c_int64,
                                      C.POINTER(C.c_void_p), C.c_void_p]),
+    "dbs_hip_decode_read_back": (C.c_int, [C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]),
     "dbs_hip_search_sequences": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
                                            C.c_void_p, C.c_void_p]),
     "dbs_hip_minimum_risk": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_float, C.c_int, C.c_void_p,

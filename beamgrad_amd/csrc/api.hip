@@ -659,6 +659,15 @@ DBS_CUDA_EXPORT int dbs_hip_decode_ex4(const void* inputs, int data_type, int fr
                          workspace, workspace_bytes, stream, true, nullptr, fault_word);
 }
 
+DBS_CUDA_EXPORT int dbs_hip_decode_read_back(const void* src, int64_t bytes, void* dst, const int32_t* fault_word,
+                                             void* stream) {
+    if (bytes < 0 || (bytes > 0 && (!src || !dst))) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
+    const hipError_t e = decode_read_back(src, static_cast<size_t>(bytes), dst, fault_word,
+                                          static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) (void)hipGetLastError();
+    return status_of(e);
+}
+
 DBS_CUDA_EXPORT int dbs_hip_decode_noalloc(const void* inputs, int data_type, int from_logits,
                                            const DBSCudaDecodeArgs* args, const DBSCudaSearchOptions* options,
                                            const uint8_t* banned_per_example, const DBSCudaDecodeOutputs* outputs,

@@ -17,6 +17,7 @@
 
 #include <atomic>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 #include "engine.hpp"
@@ -156,13 +157,33 @@ struct Aux {
     hipEvent_t start = nullptr, done = nullptr;
     int cus = 0;
     uint64_t last_use = 0;
-    std::mutex mutex;  // one decode's enqueue sequence at a time on this set
+    uint64_t epoch = 0;  // changes whenever `stream` is destroyed and created anew
+    std::mutex mutex;    // one decode's enqueue sequence (or read-back) at a time on this set
 };
 constexpr int kMaxAux = 64;
 Aux g_aux[kMaxAux];
 int g_aux_used = 0;
 uint64_t g_aux_clock = 0;
 std::mutex g_aux_mutex;  // guards the table, not the launches
+uint64_t g_aux_epoch = 0;
+
+// The overlapped decode this thread launched last: the set and the stream its
+// select pass ran on (for the read-back that ends it).
+struct LastOverlap {
+    const int32_t* fault = nullptr;
+    Aux* set = nullptr;
+    hipStream_t stream = nullptr;
+    uint64_t epoch = 0;
+};
+thread_local LastOverlap t_last_overlap;
+
+// Pinned host memory for read-backs, per thread (a copy into pageable memory
+// goes through the runtime's own staging and costs ~10 us more per call).
+struct Staging {
+    void* ptr = nullptr;
+    size_t cap = 0;
+};
+thread_local Staging t_staging;
 
 // Stream, events and CU count of a set on `device` (current).
 hipError_t aux_create(Aux& a, int device) {
@@ -172,6 +193,7 @@ hipError_t aux_create(Aux& a, int device) {
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&a.stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&a.start, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&a.done, hipEventDisableTiming);
+    a.epoch = ++g_aux_epoch;
     if (e != hipSuccess) {
         if (a.stream) (void)hipStreamDestroy(a.stream);
         if (a.start) (void)hipEventDestroy(a.start);
@@ -363,7 +385,45 @@ hipError_t launch_decode(const DecodeParams& p0, const DecodeLayout& L, hipStrea
     }
     if (e == hipSuccess) e = hipEventRecord(aux->done, aux->stream);
     if (e == hipSuccess) e = hipStreamWaitEvent(stream, aux->done, 0);
-    if (e == hipSuccess) *fault = p.fault;
+    if (e == hipSuccess) {
+        *fault = p.fault;
+        t_last_overlap = LastOverlap{p.fault, aux, aux->stream, aux->epoch};
+    }
+    return e;
+}
+
+hipError_t decode_read_back(const void* src, size_t bytes, void* dst, const int32_t* fault, hipStream_t stream) {
+    if (bytes == 0) return hipSuccess;
+    Staging& st = t_staging;
+    if (st.cap < bytes) {
+        // no copy is pending into the old buffer: every read-back waits for its copy
+        if (st.ptr) (void)hipHostFree(st.ptr);
+        st.ptr = nullptr;
+        st.cap = 0;
+        const size_t cap = bytes < 4096 ? 4096 : bytes;
+        const hipError_t e = hipHostMalloc(&st.ptr, cap, hipHostMallocDefault);
+        if (e != hipSuccess) {
+            st.ptr = nullptr;
+            return e;
+        }
+        st.cap = cap;
+    }
+    // The select pass's stream, when `fault` is the last overlapped decode of
+    // this thread and that stream still exists (its set's mutex, held until
+    // the copy has landed, keeps it from being destroyed); else `stream`.
+    const LastOverlap last = t_last_overlap;
+    std::unique_lock<std::mutex> held;
+    hipStream_t on = stream;
+    if (fault && last.fault == fault && last.set) {
+        std::lock_guard<std::mutex> table(g_aux_mutex);
+        if (last.set->epoch == last.epoch && last.set->stream == last.stream) {
+            held = std::unique_lock<std::mutex>(last.set->mutex);
+            on = last.stream;
+        }
+    }
+    hipError_t e = hipMemcpyAsync(st.ptr, src, bytes, hipMemcpyDeviceToHost, on);
+    if (e == hipSuccess) e = hipStreamSynchronize(on);
+    if (e == hipSuccess) std::memcpy(dst, st.ptr, bytes);
     return e;
 }
 

@@ -239,6 +239,14 @@ struct WidenTrace {
     int T;
 };
 hipError_t launch_widen_trace(const WidenTrace& w, hipStream_t stream);
+// The read-back that ends a decode: `bytes` bytes at `src` (written only by
+// the decode's select pass: its flags or its fault word) copied to `dst` on
+// the host through pinned memory, waiting for nothing else. After an
+// overlapped decode (`fault`: its fault word; it must be the last one this
+// thread launched) the copy runs on the select pass's stream right behind it,
+// so the wait skips the hop back to `stream` and work queued there since;
+// otherwise it runs on `stream`.
+hipError_t decode_read_back(const void* src, size_t bytes, void* dst, const int32_t* fault, hipStream_t stream);
 hipError_t launch_length_penalty(const int32_t* lengths, int64_t n, float alpha, float* out, hipStream_t stream);
 hipError_t launch_check_steps(const int32_t* steps, int B, int T, int32_t* status, hipStream_t stream);
 // Range check of every per-example array (steps in [1, T], beams in [1, K],

@@ -57,6 +57,24 @@ DBS_CUDA_EXPORT int dbs_hip_decode_ex4(
     int32_t** fault_word,
     void* stream);
 
+/* The read-back that ends a decode of dbs_hip_decode_ex4 on `stream`: copies
+ * `bytes` bytes at `src` -- the decode's invalid_input flags or its
+ * *fault_word, which only its select pass writes -- to `dst` on the host and
+ * returns once they are there. Given the fault word of the overlapped decode
+ * the calling thread launched last, the copy runs on that decode's second
+ * stream right behind its select pass, so the wait covers neither the hop back
+ * to `stream` nor work queued on `stream` after the decode; with
+ * fault_word == NULL (or any other decode) it runs on `stream` and waits for
+ * it. Returns a status. No counterpart in the reference, whose CUDA op reads
+ * its flags back with a copy on the caller's stream (reference
+ * python/csrc/cuda_ops.cpp:177-184). */
+DBS_CUDA_EXPORT int dbs_hip_decode_read_back(
+    const void* src,
+    int64_t bytes,
+    void* dst,
+    const int32_t* fault_word,
+    void* stream);
+
 /* dbs_hip_decode_ex3 without a workspace argument and without any device
  * allocation, for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the

@@ -34,7 +34,7 @@ class HipEngine:
                alpha=0.0, no_repeat_ngram_size=0, repetition_penalty=1.0, steps=None, banned=None,
                banned_per_example=None, use_ex3: bool | None = None, workspace: bool = True,
                x_offset: int = 0, beams=None, eos_tokens=None, min_lengths=None, expect_status=None,
-               with_status: bool = False, noalloc: bool = False) -> dict:
+               with_status: bool = False, noalloc: bool = False, read_back: bool = False) -> dict:
         B, T, K, V = xin.shape
         x = _dev(xin.view(np.int16) if xin.dtype == np.uint16 else xin)
         if x_offset:
@@ -80,6 +80,31 @@ class HipEngine:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if workspace else None
         if use_ex3 is None:
             use_ex3 = bpe_d is not None
+        fault = C.c_void_p()
+        if read_back:
+            # dbs_hip_decode_ex4, then the flags and the fault word read back
+            # by dbs_hip_decode_read_back before anything else waits
+            status = self.lib.dbs_hip_decode_ex4(
+                _abi.ptr(x), _abi.DTYPE[dtype], int(from_logits), C.byref(args), C.byref(opts), _abi.ptr(bpe_d),
+                C.byref(o), _abi.ptr(out["row_lse"]), _abi.ptr(ws), ws_bytes, C.byref(fault), self.stream())
+            assert status == _abi.STATUS_OK, self.lib.dbs_cuda_status_string(status)
+            flags = np.full(B, 0xAB, np.uint8)
+            word = np.full(1, -7, np.int32)
+            st = self.lib.dbs_hip_decode_read_back(_abi.ptr(out["invalid"]), B, flags.ctypes.data, fault, self.stream())
+            assert st == _abi.STATUS_OK, self.lib.dbs_cuda_status_string(st)
+            if fault.value:
+                st = self.lib.dbs_hip_decode_read_back(fault, 4, word.ctypes.data, fault, self.stream())
+                assert st == _abi.STATUS_OK, self.lib.dbs_cuda_status_string(st)
+            torch.cuda.current_stream().synchronize()
+            res = {k: v.cpu().numpy() for k, v in out.items()}
+            res["read_back_flags"], res["read_back_fault"] = flags, (int(word[0]) if fault.value else None)
+            res["fault_word"] = None
+            if fault.value:
+                # the word read by a plain copy, from its place in the workspace
+                at = fault.value - ws.data_ptr()
+                assert 0 <= at <= ws_bytes - 4
+                res["fault_word"] = int(ws[at:at + 4].cpu().numpy().view(np.int32)[0])
+            return res
         if noalloc:
             status = self.lib.dbs_hip_decode_noalloc(
                 _abi.ptr(x), _abi.DTYPE[dtype], int(from_logits), C.byref(args), C.byref(opts), _abi.ptr(bpe_d),

@@ -37,7 +37,7 @@ def lib():
 
 def test_every_declared_symbol_is_exported(lib):
     names = declared_symbols()
-    assert len(names) == 31  # 17 reference entry points + 14 additions
+    assert len(names) == 32  # 17 reference entry points + 15 additions
     out = subprocess.run(["nm", "-D", "--defined-only", _build.lib_path()], capture_output=True, text=True,
                          check=True).stdout
     exported = set(re.findall(r" T (dbs_\w+)", out))

@@ -254,3 +254,56 @@ def test_more_caller_streams_than_overlap_sets(hip, oracle, overlap_on):
             assert first_difference(got, want) is None, (rep, i)
     torch.cuda.synchronize()
     assert _timeouts(overlap_on) == 0
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("overlap", [1, 0])
+def test_read_back_after_a_decode(hip, oracle, monkeypatch, seed, overlap):
+    """dbs_hip_decode_read_back after dbs_hip_decode_ex4: the flags and the
+    fault word it copies equal a plain copy taken after the stream is
+    synchronised, overlapped (the copy runs on the select pass's stream) or
+    not (on the caller's stream), with and without a forced give-up; the
+    trace matches the oracle."""
+    lib = hip.lib
+    prev = lib.dbs_hip_set_decode_overlap(overlap)
+    try:
+        case = _big_case(7700 + seed)
+        give_up = overlap == 1 and seed % 2 == 1
+        if give_up:
+            _forced_give_up(monkeypatch)
+        res = hip.decode(case["xin"], case["dtype"], read_back=True, **case["kw"])
+    finally:
+        lib.dbs_hip_set_decode_overlap(prev)
+    assert np.array_equal(res["read_back_flags"], res["invalid"])
+    assert res["read_back_fault"] == res["fault_word"]
+    overlapped = res["fault_word"] is not None
+    assert overlapped == (overlap == 1 and case["T"] > 1)
+    if give_up and overlapped:
+        assert res["fault_word"] != 0 and (res["invalid"] == 2).all()
+    else:
+        assert (res["invalid"] == 0).all() and not res["fault_word"]
+        want = oracle.decode(case["xin"], dtype=case["dtype"], **case["kw"])
+        assert first_difference(res, want) is None
+
+
+def test_read_back_on_many_caller_streams(hip, oracle, overlap_on):
+    """Decodes read back through the torch ops on 70 caller streams (more
+    than the library's 64 overlap sets, so sets are rebound between a decode
+    and the next): every result matches the oracle, no wait gives up."""
+    import beamgrad_amd as bg
+
+    case, x, opts = _torch_case(7720)
+    kw = case["kw"]
+    want = oracle.decode(case["xin"], dtype=case["dtype"], **kw)
+    streams = [torch.cuda.Stream() for _ in range(70)]
+    for i, s in enumerate(streams + streams[:6]):
+        with torch.cuda.stream(s):
+            out = bg.decode(x, opts(i % 2 == 0), kw["steps"], from_logits=True)
+            s.synchronize()
+        got = {k: getattr(out, k).cpu().numpy() for k in ("final_scores", "final_raw_scores", "scores",
+                                                             "raw_scores")}
+        for k in ("final_lengths", "tokens", "parents", "lengths"):
+            got[k] = getattr(out, k).cpu().numpy().astype(np.int32)
+        assert first_difference(got, want, tuple(got)) is None, i
+    torch.cuda.synchronize()
+    assert _timeouts(overlap_on) == 0
