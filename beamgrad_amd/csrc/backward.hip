@@ -346,9 +346,13 @@ __device__ __forceinline__ void zero_row(void* out, int64_t row_off, int V) {
 
 // POOL: the relaxed pool's entries join the row's (after the selected
 // slots' entries of the same token: slot K + j), up to K + P entries a row.
-template <int DT, int OT, bool LOGITS, bool POOL = false>
+// SMALL: rows of at most 64 entries (K <= 64 without the pool: one entry a
+// selected slot at most), whose entry arrays take 768 bytes of LDS instead of
+// 12 KB: with the bfloat16 term table (32 KB) four workgroups fit a CU
+// instead of three.
+template <int DT, int OT, bool LOGITS, bool POOL = false, bool SMALL = false>
 __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardParams p) {
-    constexpr int kEntries = POOL ? 2 * DBS_CUDA_MAX_BEAM : DBS_CUDA_MAX_BEAM;
+    constexpr int kEntries = SMALL ? 64 : (POOL ? 2 * DBS_CUDA_MAX_BEAM : DBS_CUDA_MAX_BEAM);
     __shared__ int32_t e_tok[kEntries];
     __shared__ float e_val[kEntries];
     __shared__ int32_t e_slot[kEntries];
@@ -585,6 +589,8 @@ hipError_t launch_dense_ot(const BackwardParams& p, hipStream_t stream) {
         hipLaunchKernelGGL((dense_gradient_kernel<0, OT, true>), grid, dim3(kDenseThreads), 0, stream, p);
     } else if (p.logits_type == 1) {
         hipLaunchKernelGGL((dense_gradient_kernel<1, OT, true>), grid, dim3(kDenseThreads), 0, stream, p);
+    } else if (p.K <= 64) {
+        hipLaunchKernelGGL((dense_gradient_kernel<2, OT, true, false, true>), grid, dim3(kDenseThreads), 0, stream, p);
     } else {
         hipLaunchKernelGGL((dense_gradient_kernel<2, OT, true>), grid, dim3(kDenseThreads), 0, stream, p);
     }
