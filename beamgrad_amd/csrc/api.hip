@@ -413,8 +413,10 @@ void set_pool_grads(BackwardParams& p, const PoolGrads* pool) {
     p.pool_d = pool->d;
 }
 
+// mode: 0 writes the gradient everywhere, 1 accumulates into float32, 2
+// writes only the rows that receive an entry (the buffer holds zeros).
 int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, void* out, int out_type,
-                    bool accumulate, void* workspace, int64_t workspace_bytes, void* stream_ptr,
+                    int mode, void* workspace, int64_t workspace_bytes, void* stream_ptr,
                     const PoolGrads* pool = nullptr) {
     if (!valid_args(args) || !in || !out) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
     if (!in->parents || !in->tokens || !in->lengths || !in->from_logprob) return DBS_CUDA_STATUS_INVALID_ARGUMENT;
@@ -457,7 +459,7 @@ int backward_common(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* 
     p.draws = reinterpret_cast<float*>(ws);
     p.out = out;
     p.out_type = out_type;
-    p.accumulate = accumulate ? 1 : 0;
+    p.accumulate = mode;
     set_pool_grads(p, pool);
     e = launch_path_walk(p, stream);
     if (e == hipSuccess) e = launch_dense_gradient(p, stream);
@@ -499,7 +501,7 @@ int64_t workspace_for_host(const DBSCudaDecodeArgs* args, int pool_mult, int ste
 
 int backward_dense_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, const PoolGrads* pool,
                             float* grad, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-    return backward_common(args, in, grad, DBS_HIP_GRAD_F32, false, workspace, workspace_bytes, stream, pool);
+    return backward_common(args, in, grad, DBS_HIP_GRAD_F32, 0, workspace, workspace_bytes, stream, pool);
 }
 
 int path_draws_for_host(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* in, const PoolGrads* pool,
@@ -725,20 +727,22 @@ DBS_CUDA_EXPORT int dbs_cuda_backward(const DBSCudaDecodeArgs* args, const int32
     in.lengths = lengths;
     in.from_logprob = from_logprob;
     in.grad_final_scores = grad_final_scores;
-    return backward_common(args, &in, grad_log_probs, 0, true, workspace, workspace_bytes, stream);
+    return backward_common(args, &in, grad_log_probs, 0, 1, workspace, workspace_bytes, stream);
 }
 
 DBS_CUDA_EXPORT int dbs_cuda_backward_ex(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* inputs,
                                          float* grad_inputs, void* workspace, int64_t workspace_bytes, void* stream) {
-    return backward_common(args, inputs, grad_inputs, 0, true, workspace, workspace_bytes, stream);
+    return backward_common(args, inputs, grad_inputs, 0, 1, workspace, workspace_bytes, stream);
 }
 
 DBS_CUDA_EXPORT int dbs_hip_backward_dense(const DBSCudaDecodeArgs* args, const DBSCudaBackwardInputs* inputs,
                                            void* grad_out, int grad_type, void* workspace, int64_t workspace_bytes,
                                            void* stream) {
+    const int mode = (grad_type & DBS_HIP_GRAD_ZEROED) ? 2 : 0;
+    grad_type &= ~DBS_HIP_GRAD_ZEROED;
     if (grad_type != DBS_HIP_GRAD_F32 && grad_type != DBS_HIP_GRAD_F16 && grad_type != DBS_HIP_GRAD_BF16)
         return DBS_CUDA_STATUS_INVALID_ARGUMENT;
-    return backward_common(args, inputs, grad_out, grad_type, false, workspace, workspace_bytes, stream);
+    return backward_common(args, inputs, grad_out, grad_type, mode, workspace, workspace_bytes, stream);
 }
 
 DBS_CUDA_EXPORT int dbs_cuda_length_penalty(const int32_t* lengths, int64_t count, float alpha, float* out,

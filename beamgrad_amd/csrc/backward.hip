@@ -373,7 +373,11 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardP
     const int q = static_cast<int>(r % K);
     const int steps_b = p.steps ? p.steps[b] : T;
     const int64_t row_off = r * V;
-    const bool accumulate = p.accumulate != 0;
+    // p.accumulate: 0 writes every row fresh, 1 adds into float32, 2 writes
+    // fresh only the rows that receive an entry (the caller's buffer already
+    // holds zeros everywhere else)
+    const bool accumulate = p.accumulate == 1;
+    const bool zeroed = p.accumulate == 2;
 
     if (tid == 0) n_raw = 0;
     __syncthreads();
@@ -440,7 +444,7 @@ __global__ __launch_bounds__(kDenseThreads) void dense_gradient_kernel(BackwardP
     const int ne = n_ent;
 
     if (!LOGITS || ne == 0) {
-        if (!accumulate) zero_row<OT>(p.out, row_off, V);
+        if (!accumulate && !zeroed) zero_row<OT>(p.out, row_off, V);
         if (ne > 0) {
             __syncthreads();  // the entries land after the zeros of this workgroup
             for (int i = tid; i < ne; i += kDenseThreads) store_out<OT>(p.out, row_off + e_tok[i], e_val[i], accumulate);

@@ -275,7 +275,7 @@ struct BackwardParams {
     float* draws;      // [B, T, K] per-slot entry gradients (workspace or caller output)
     void* out;         // [B, T, K, V]
     int out_type;      // 0 f32, 1 f16, 2 bf16
-    int accumulate;    // 1: out += g (f32 only); 0: out = 0 + g everywhere
+    int accumulate;    // 1: out += g (f32 only); 0: out = 0 + g everywhere; 2: only rows with an entry (out holds 0)
     // Relaxed-pool entries [B, T, P] (pool_d null: none; reference
     // src/decoder.cpp:617-657): each entry's raw-score gradient d, added to
     // its parent's incoming gradient after the selected children (in entry

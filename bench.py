@@ -11,7 +11,8 @@ count). Beside it: the row pass's HBM roofline fraction (kernel time from the
 engine's HIP events on its own stream), the reference CPU library on the same
 batch (num_threads = 0, median of 5 runs), and under ``c5`` the second half
 of the metric: the C5 forward + minimum-risk loss + backward step latency with
-the forward's and the backward's (dense gradient's) roofline, and the
+the forward's and the backward's (dense gradient's: the rows with a path
+gradient, written into zeros the forward stores) roofline, and the
 reference CPU library's decode + backward of the same batch fed the same
 final-score gradient. Every roofline also states the box's measured device
 copy bandwidth (``copy_gbs``) and the fraction of it reached.
@@ -340,11 +341,13 @@ def hbm_roofline(bytes_per_launch: float, avg_ms: float, kernel: str, traffic=No
 
 def c5_summary(m: dict) -> dict:
     """The fwd+bwd half of the metric on C5: step latency and the backward's
-    (dense gradient) roofline: bf16 gradient writes plus the logits rows with
-    a path gradient read once."""
+    (dense gradient's) roofline. The zeros of the bf16 gradient are stored by
+    a fill the forward queues (while the host runs the loss and autograd);
+    the dense gradient launch reads each logits row with a path gradient once
+    and writes that row of the gradient once."""
     cfg = m["cfg"]
-    B, T, K, V = cfg["B"], cfg["T"], cfg["K"], cfg["V"]
-    bwd_bytes = B * T * K * V * 2 + m["rows_with_gradient"] * V * 2
+    V = cfg["V"]
+    bwd_bytes = 2 * m["rows_with_gradient"] * V * 2
     out = {"workload": f"C5: {cfg['desc']}", "ms_per_step": m["ms_per_step"],
            "kernels_ms": {k: round(v["avg_ms"], 4) for k, v in m["kernels"].items()},
            "rows_read": m["rows_read"], "rows_with_gradient": m["rows_with_gradient"]}

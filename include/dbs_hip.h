@@ -105,6 +105,12 @@ DBS_CUDA_EXPORT int dbs_hip_decode_noalloc(
 #define DBS_HIP_GRAD_F32 0
 #define DBS_HIP_GRAD_F16 1
 #define DBS_HIP_GRAD_BF16 2
+/* OR-ed into grad_type: grad_out already holds zeros (e.g. cleared while the
+ * host was busy between the decode and its backward), and only the rows
+ * [b, t, q] that receive an entry are written, each as the call without the
+ * flag writes it; every other row is left as it is. Same result as the call
+ * without the flag on that buffer. */
+#define DBS_HIP_GRAD_ZEROED 0x100
 
 /* The gradient of dbs_cuda_backward_ex written, not accumulated: every
  * element of grad_out [B, T, K, V] is stored once, as 0 + g rounded to
